@@ -1,0 +1,358 @@
+"""ctypes front end of ``libtnref.so`` plus numpy closed forms (TEST INFRASTRUCTURE ONLY).
+
+Reference paths cited below are relative to the torchnative checkout:
+``K`` = ``torchnative/rust/vendor/candle-core/src/quantized/k_quants.rs``,
+``A`` = ``torchnative/rust/torch_c/src/aten.rs``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+
+__all__ = [
+    "lib", "build", "QK", "Q4_0_BYTES", "Q8_0_BYTES",
+    "f16_from_f32", "f16_to_f32", "bf16_from_f32", "bf16_to_f32",
+    "q4_0_quantize", "q4_0_dequantize", "q8_0_quantize", "q8_0_dequantize",
+    "vec_dot_q4_0_q8_0", "q4_0_linear", "sdpa", "sdpa_bf16",
+    "q4_0_parts", "q8_0_parts", "exact_linear_q4_0", "gamma", "accumulation_k",
+    "linear_bound", "sdpa_closed_form", "sdpa_det", "q8_0_ties", "signed_max_ties",
+    "synth_q4_0_weight", "sdpa_tolerance",
+]
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtnref.so")
+QK = 32
+Q4_0_BYTES = 18
+Q8_0_BYTES = 34
+U32 = 2.0 ** -24
+U64 = 2.0 ** -53
+
+_lib = None
+
+
+def build() -> str:
+    """Compile ``libtnref.so`` with the committed Makefile."""
+    subprocess.run(["make", "-s", "-B", "-C", HERE, "libtnref.so"], check=True)
+    return LIB_PATH
+
+
+def lib():
+    """Load the oracle library, building it only if nothing is built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        build()
+    L = ctypes.CDLL(LIB_PATH)
+    P, I64, I, D = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double
+    L.tnref_f16_from_f32.restype = ctypes.c_uint16
+    L.tnref_f16_from_f32.argtypes = [ctypes.c_float]
+    L.tnref_f16_to_f32.restype = ctypes.c_float
+    L.tnref_f16_to_f32.argtypes = [ctypes.c_uint16]
+    for name in ("tnref_f32_to_f16_n", "tnref_f32_to_bf16_n", "tnref_bf16_to_f32_n",
+                 "tnref_q4_0_quantize", "tnref_q4_0_dequantize",
+                 "tnref_q8_0_quantize", "tnref_q8_0_dequantize"):
+        getattr(L, name).argtypes = [P, I64, P] if "quant" in name else [P, P, I64]
+        getattr(L, name).restype = None
+    L.tnref_vec_dot_q4_0_q8_0.restype = ctypes.c_float
+    L.tnref_vec_dot_q4_0_q8_0.argtypes = [I64, P, P]
+    L.tnref_q4_0_linear.restype = I
+    L.tnref_q4_0_linear.argtypes = [I64, I64, I64, P, P, P, P, I]
+    for name in ("tnref_sdpa_f32", "tnref_sdpa_f64"):
+        fn = getattr(L, name)
+        fn.restype = I
+        fn.argtypes = [I64] * 6 + [P, P, P, P, I, D, P, P, I]
+    _lib = L
+    return L
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+# --- reduced floats ---------------------------------------------------------
+
+
+def f16_from_f32(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().tnref_f32_to_f16_n(_p(x), _p(out), x.size)
+    return out
+
+
+def f16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    return np.array([lib().tnref_f16_to_f32(int(v)) for v in h.reshape(-1)],
+                    dtype=np.float32).reshape(h.shape)
+
+
+def bf16_from_f32(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().tnref_f32_to_bf16_n(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+# --- codecs -----------------------------------------------------------------
+
+
+def q4_0_quantize(x) -> bytes:
+    """GGML Q4_0 blob of a float32 array whose size is a multiple of 32 (K:241-277)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    assert x.size % QK == 0
+    out = np.empty(x.size // QK * Q4_0_BYTES, dtype=np.uint8)
+    lib().tnref_q4_0_quantize(_p(x), x.size, _p(out))
+    return out.tobytes()
+
+
+def q4_0_dequantize(blob, n) -> np.ndarray:
+    b = np.frombuffer(bytes(blob), dtype=np.uint8)
+    assert b.size == n // QK * Q4_0_BYTES
+    out = np.empty(n, dtype=np.float32)
+    lib().tnref_q4_0_dequantize(_p(b), n, _p(out))
+    return out
+
+
+def q8_0_quantize(x) -> bytes:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    assert x.size % QK == 0
+    out = np.empty(x.size // QK * Q8_0_BYTES, dtype=np.uint8)
+    lib().tnref_q8_0_quantize(_p(x), x.size, _p(out))
+    return out.tobytes()
+
+
+def q8_0_dequantize(blob, n) -> np.ndarray:
+    b = np.frombuffer(bytes(blob), dtype=np.uint8)
+    assert b.size == n // QK * Q8_0_BYTES
+    out = np.empty(n, dtype=np.float32)
+    lib().tnref_q8_0_dequantize(_p(b), n, _p(out))
+    return out
+
+
+def vec_dot_q4_0_q8_0(k, w_row: bytes, xq_row: bytes) -> float:
+    w = np.frombuffer(bytes(w_row), dtype=np.uint8)
+    x = np.frombuffer(bytes(xq_row), dtype=np.uint8)
+    return float(np.float32(lib().tnref_vec_dot_q4_0_q8_0(k, _p(w), _p(x))))
+
+
+def q4_0_linear(x, w_blob, n, bias=None, threads=1) -> np.ndarray:
+    """``torch._C._quantized_linear`` restated: y = Q8_0(x) . W^T (+ bias).
+
+    x is float32 [..., K]; the result is float32 [..., N]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    m = x.size // k if k else 0
+    w = np.frombuffer(bytes(w_blob), dtype=np.uint8)
+    assert w.size == n * (k // QK) * Q4_0_BYTES, "blob size does not match [N, K]"
+    y = np.empty(x.shape[:-1] + (n,), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    rc = lib().tnref_q4_0_linear(m, k, n, _p(x), _p(w), _p(b), _p(y), int(threads))
+    assert rc == 0
+    return y
+
+
+# --- SDPA -------------------------------------------------------------------
+
+
+def sdpa(q, k, v, mask=None, is_causal=False, scale=None, threads=1, dtype=np.float32):
+    """The default path of A:10330-10423 in float32 or float64.
+
+    Returns ``(out, lse)``. q [B,Hq,L,D], k/v [B,Hkv,S,D]; mask broadcastable
+    to [B,Hq,L,S]."""
+    dt = np.dtype(dtype)
+    q = np.ascontiguousarray(q, dtype=dt)
+    k = np.ascontiguousarray(k, dtype=dt)
+    v = np.ascontiguousarray(v, dtype=dt)
+    B, Hq, L, D = q.shape
+    _, Hkv, S, _ = k.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    m = None
+    if mask is not None:
+        m = np.ascontiguousarray(np.broadcast_to(np.asarray(mask, dtype=dt), (B, Hq, L, S)))
+    out = np.empty((B, Hq, L, D), dtype=dt)
+    lse = np.empty((B, Hq, L), dtype=dt)
+    fn = lib().tnref_sdpa_f64 if dt == np.float64 else lib().tnref_sdpa_f32
+    rc = fn(B, Hq, Hkv, L, S, D, _p(q), _p(k), _p(v), _p(m), int(bool(is_causal)),
+            float(scale), _p(out), _p(lse), int(threads))
+    assert rc == 0
+    return out, lse
+
+
+def sdpa_bf16(q_bits, k_bits, v_bits, mask=None, is_causal=False, scale=None, threads=1):
+    """bf16 inputs (as uint16 bit patterns): widened to f32 for the whole body,
+    the output narrowed back to bf16 RNE, the lse kept f32 (A:10196-10206,
+    A:10412). Returns ``(out_bits uint16, lse float32)``."""
+    q = bf16_to_f32(q_bits)
+    k = bf16_to_f32(k_bits)
+    v = bf16_to_f32(v_bits)
+    out, lse = sdpa(q, k, v, mask, is_causal, scale, threads)
+    return bf16_from_f32(out), lse
+
+
+# --- closed forms (numpy, independent of libtnref) ----------------------------
+
+
+def q4_0_parts(blob, n, k):
+    """(d float64 [n, nb], q int64 [n, nb, 32]) with element j / j+16 from the
+    low / high nibble of byte j (K:219-239)."""
+    raw = np.frombuffer(bytes(blob), dtype=np.uint8).reshape(n, k // QK, Q4_0_BYTES)
+    d = raw[:, :, 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
+    qs = raw[:, :, 2:]
+    lo = (qs & 0x0F).astype(np.int64) - 8
+    hi = (qs >> 4).astype(np.int64) - 8
+    return d, np.concatenate([lo, hi], axis=2)
+
+
+def q8_0_parts(blob, m, k):
+    raw = np.frombuffer(bytes(blob), dtype=np.uint8).reshape(m, k // QK, Q8_0_BYTES)
+    d = raw[:, :, 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
+    q = raw[:, :, 2:].copy().view(np.int8).astype(np.int64)
+    return d, q
+
+
+def exact_linear_q4_0(xq_blob, w_blob, m, n, k):
+    """(value, abs_sum, ref_err), each float64 [m, n]: the exact dyadic value of
+    the quantised matmul from the two blobs. Every block term is exact in
+    float64 (15 + 11 + 11 bits); only the summation rounds, by at most
+    ``ref_err``."""
+    dw, qw = q4_0_parts(w_blob, n, k)
+    dx, qx = q8_0_parts(xq_blob, m, k)
+    ints = np.einsum("rbk,obk->rob", qx, qw)
+    absints = np.einsum("rbk,obk->rob", np.abs(qx), np.abs(qw))
+    scale = dx[:, None, :] * dw[None, :, :]
+    terms = ints.astype(np.float64) * scale
+    if m * n <= 4096:
+        value = np.array([math.fsum(r) for r in terms.reshape(-1, terms.shape[-1])]).reshape(m, n)
+        rel = U64
+    else:
+        nb = terms.shape[-1]
+        value = terms.sum(axis=-1)
+        rel = nb * U64 / (1.0 - nb * U64)
+    abs_sum = (absints.astype(np.float64) * np.abs(scale)).sum(axis=2)
+    return value, abs_sum, rel * abs_sum
+
+
+def gamma(kk):
+    return kk * U32 / (1.0 - kk * U32)
+
+
+def accumulation_k(k):
+    """Roundings on a block term's path to the output in the x86_64 scalar
+    path (K:312-329): ``(s * d_w)`` and ``* d_x`` round once each; the
+    sequential sum passes a term through at most nb-1 additions. Counted as
+    nb + 2 (one spare)."""
+    return k // QK + 2
+
+
+def linear_bound(k, abs_sum, ref_err):
+    return gamma(accumulation_k(k)) * abs_sum + ref_err
+
+
+def sdpa_closed_form(q, k, v, mask=None, is_causal=False, scale=None):
+    """softmax(q k^T * scale + causal + mask) v and its logsumexp in float64,
+    written from the mathematics with an explicit repeat_interleave of the
+    key/value heads and an explicit upper-left triangular mask."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    B, Hq, L, D = q.shape
+    Hkv, S = k.shape[1], k.shape[2]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    rep = Hq // Hkv
+    kk = np.repeat(k, rep, axis=1)
+    vv = np.repeat(v, rep, axis=1)
+    s = np.einsum("bhld,bhsd->bhls", q, kk) * scale
+    if is_causal:
+        tri = np.tril(np.ones((L, S), dtype=bool))  # row i keeps keys 0..=i
+        s = np.where(tri, s, -np.inf)
+    if mask is not None:
+        s = s + np.asarray(mask, np.float64)
+    mx = s.max(axis=-1, keepdims=True)
+    w = np.exp(s - mx)
+    tot = w.sum(axis=-1, keepdims=True)
+    out = np.einsum("bhls,bhsd->bhld", w / tot, vv)
+    lse = (np.log(tot) + mx)[..., 0]
+    return out, lse
+
+
+def sdpa_det(n, seed):
+    """``n`` values k/128, exact in bf16/f16/f32/f64: the reference test
+    inputs' generator (tests/_support/test_shim.py:12103-12116)."""
+    out, state = [], seed * 2654435761 % 2147483647
+    for _ in range(n):
+        state = (state * 1103515245 + 12345) % 2147483648
+        out.append((state % 321 - 160) / 128.0)
+    return out
+
+
+def q8_0_ties(x):
+    """Elements whose Q8_0 rounding lands on an exact .5 (where half-even and
+    half-away disagree)."""
+    f = np.float32
+    xs = np.asarray(x, dtype=f).reshape(-1, QK)
+    d = (np.abs(xs).max(axis=1) / f(127)).astype(f)
+    inv = np.where(d == 0, f(0), f(1) / np.where(d == 0, f(1), d)).astype(f)
+    v = (xs * inv[:, None]).astype(f)
+    return int(np.sum(np.abs(v - np.floor(v)) == f(0.5)))
+
+
+def signed_max_ties(x, block=QK):
+    xs = np.asarray(x, dtype=np.float32).reshape(-1, block)
+    ax = np.abs(xs)
+    amax = ax.max(axis=1, keepdims=True)
+    at = (ax == amax) & (amax > 0)
+    return int(np.sum(np.any(at & (xs > 0), axis=1) & np.any(at & (xs < 0), axis=1)))
+
+
+def synth_q4_0_weight(n, k, sigma, seed):
+    """The synthetic weight of BASELINE configs 1/3/5 as a GGML blob: codes
+    uniform in [-8, 7] stored as nib = code + 8, per-block d = f16_rne(|N(0,
+    sigma)| / 7). Built directly in the format (no quantiser involved)."""
+    rng = np.random.default_rng(seed)
+    nb = k // QK
+    codes = rng.integers(-8, 8, size=(n, nb, QK), dtype=np.int64)
+    d = (np.abs(rng.standard_normal((n, nb))) * sigma / 7.0).astype(np.float32)
+    dh = f16_from_f32(d)
+    nib = (codes + 8).astype(np.uint8)
+    packed = (nib[:, :, :16] | (nib[:, :, 16:] << 4)).astype(np.uint8)
+    blob = np.empty((n, nb, Q4_0_BYTES), dtype=np.uint8)
+    blob[:, :, 0] = (dh & 0xFF).astype(np.uint8)
+    blob[:, :, 1] = (dh >> 8).astype(np.uint8)
+    blob[:, :, 2:] = packed
+    return blob.tobytes()
+
+
+def sdpa_tolerance(ref32, ref64, kind="float32", p=None, v_abs=None):
+    """Per-element bound on |gpu - ref32| for one SDPA output tensor.
+
+    The rule (docs/numerics/AGREE.md section 2 of the reference, applied per
+    tensor): 4x the reference's own fp32-vs-fp64 distance, floored at 10 ulp
+    (1.186e-6) of the tensor's scale. For a bf16 output add one bf16 ulp of
+    |ref| (both sides round to bf16) and, when ``p``/``v_abs`` are given, the
+    P-narrowing term 2^-9 * sum_j P_ij |V_jd|."""
+    ref32 = np.asarray(ref32, np.float64)
+    ref64 = np.asarray(ref64, np.float64)
+    fin = np.isfinite(ref64)
+    own = float(np.max(np.abs(ref32 - ref64)[fin])) if fin.any() else 0.0
+    scale_ = float(np.max(np.abs(ref64[fin]))) if fin.any() else 0.0
+    tol = max(4.0 * own, 1.186e-6 * scale_)
+    tol = np.full(ref32.shape, tol)
+    if kind == "bfloat16":
+        mag = np.abs(ref64)
+        e = np.floor(np.log2(np.where(mag > 0, mag, 1e-38)))
+        tol = tol + np.where(mag > 0, 2.0 ** (e - 7), 2.0 ** -133)
+        if p is not None:
+            tol = tol + 2.0 ** -9 * p
+    return tol
