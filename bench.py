@@ -1,0 +1,310 @@
+"""Benchmark of the hot path on one MI355X (the BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+One step is one pass of the hot path over one batch of synthetic input, with
+the inputs already resident in HBM. The headline line is BASELINE config 2
+(causal GQA SDPA prefill, bf16, B=1, 9/3 heads, D=64, S=2048); the other
+configs are measured in the same run and reported under "parts":
+
+  c1  q4_0 decode GEMV [1,576] x [1536,576]^T, streamed over 1,024 distinct
+      weight copies in one launch (509 MB > the 256 MB MALL), plus the latency
+      of one C1-sized call;
+  c2  SDPA prefill, bf16 (headline) and fp32;
+  c3  q4_0 prefill GEMM x bf16 [512,4096] x W [14336,4096]^T, bf16 out;
+  c4  decode attention, B=16, 32/8 heads, D=128, bf16, lens ~ U[512,4096],
+      rotated over 3 KV sets (> MALL).
+
+Kernel time comes from HIP events on the stream the kernels run on; the
+step time from the host clock around synchronised regions. The CPU baseline
+is the C oracle (the restatement of the reference's CPU arithmetic) timed on
+this host's cores on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+
+
+def _synth_q4_0_blob(n, k, sigma, seed):
+    """Q4_0 blob in the BASELINE format: codes uniform in [-8,7] (nib = code+8),
+    d = f16_rne(|N(0, sigma)| / 7)."""
+    rng = np.random.default_rng(seed)
+    nb = k // 32
+    nib = rng.integers(0, 16, size=(n, nb, 32), dtype=np.uint8)
+    d = (np.abs(rng.standard_normal((n, nb))) * sigma / 7.0).astype(np.float32).astype(np.float16)
+    blob = np.empty((n, nb, 18), dtype=np.uint8)
+    blob[:, :, 0:2] = d.view(np.uint8).reshape(n, nb, 2)
+    blob[:, :, 2:] = nib[:, :, :16] | (nib[:, :, 16:] << 4)
+    return blob.reshape(-1)
+
+
+class Timer:
+    """Host wall clock around a synchronised region plus HIP events on the
+    stream the work is issued to."""
+
+    def __init__(self, tn, stream=None):
+        self.tn, self.stream = tn, stream
+        self.e0, self.e1 = tn.Event(), tn.Event()
+
+    def run(self, fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        self.tn.synchronize()
+        t0 = time.perf_counter()
+        self.e0.record(self.stream)
+        for _ in range(steps):
+            fn()
+        self.e1.record(self.stream)
+        self.tn.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3
+        return wall / steps, self.e0.elapsed_ms(self.e1) / steps
+
+
+def bench_sdpa(tn, L, dtype, steps, warmup, B=1, Hq=9, Hkv=3, S=2048, D=64, seed=2):
+    rng = np.random.default_rng(seed)
+    q = tn.tensor(rng.standard_normal((B, Hq, S, D)).astype(np.float32), dtype=dtype, device="hip")
+    k = tn.tensor(rng.standard_normal((B, Hkv, S, D)).astype(np.float32), dtype=dtype, device="hip")
+    v = tn.tensor(rng.standard_normal((B, Hkv, S, D)).astype(np.float32), dtype=dtype, device="hip")
+    out = tn.empty((B, Hq, S, D), dtype, "hip")
+    lse = tn.empty((B, Hq, S), "float32", "hip")
+    code = L.TN_BF16 if dtype == "bfloat16" else L.TN_F32
+    lib = L.lib()
+
+    def step():
+        st = lib.tn_sdpa_fwd(None, code, q.data_ptr(), k.data_ptr(), v.data_ptr(), B, Hq, Hkv, S, S, D, None, 0, 1,
+                             float("nan"), out.data_ptr(), lse.data_ptr())
+        if st:
+            L.check(st)
+
+    ms, kern_ms = Timer(tn).run(step, steps, warmup)
+    flops = 4.0 * D * Hq * B * S * (S + 1) / 2
+    peak = BF16_PEAK_TFLOPS if dtype == "bfloat16" else FP32_PEAK_TFLOPS
+    ach = flops / (kern_ms * 1e-3) / 1e12
+    return {"ms_per_step": ms, "kernel_ms": kern_ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
+            "roofline": {"bound": "mfma", "achieved": ach, "peak": peak, "unit": "TFLOP/s", "frac": ach / peak,
+                         "traffic": None}}
+
+
+def bench_gemv(tn, L, steps, warmup, copies=1024):
+    n, k = 1536, 576
+    lib = L.lib()
+    rng = np.random.default_rng(1)
+    x = tn.tensor(rng.standard_normal((1, k)).astype(np.float32), device="hip")
+    # 1,024 distinct [1536, 576] weights, contiguous: one launch streams all of them
+    qs = tn.empty((copies * n * k // 2,), "uint8", "hip")
+    dd = tn.empty((copies * n * k // 32 * 2,), "uint8", "hip")
+    chunk = 64
+    for c0 in range(0, copies, chunk):
+        blob = _synth_q4_0_blob(chunk * n, k, 0.02, 1000 + c0)
+        bt = tn.tensor(blob, device="hip")
+        off_q = c0 * n * k // 2
+        off_d = c0 * n * k // 32 * 2
+        L.check(lib.tn_q4_0_from_blob(None, bt.data_ptr(), chunk * n, k, qs.data_ptr() + off_q, dd.data_ptr() + off_d))
+    y = tn.empty((1, copies * n), "float32", "hip")
+
+    def step_all():
+        st = lib.tn_q4_0_linear(None, x.data_ptr(), L.TN_F32, 1, k, qs.data_ptr(), dd.data_ptr(), copies * n, None,
+                                y.data_ptr(), L.TN_F32)
+        if st:
+            L.check(st)
+
+    ms, kern_ms = Timer(tn).run(step_all, steps, warmup)
+    w_bytes = n * (k // 32) * 18
+    per_copy = w_bytes + n * 4
+    total_bytes = copies * per_copy + k * 4
+    ach = total_bytes / (kern_ms * 1e-3) / 1e9
+    # one C1-sized call, cycling through the copies so the weight is cold
+    idx = [0]
+
+    def step_one():
+        c = idx[0] % copies
+        idx[0] += 1
+        st = lib.tn_q4_0_linear(None, x.data_ptr(), L.TN_F32, 1, k, qs.data_ptr() + c * n * k // 2,
+                                dd.data_ptr() + c * n * k // 16, n, None, y.data_ptr(), L.TN_F32)
+        if st:
+            L.check(st)
+
+    one_ms, one_kern = Timer(tn).run(step_one, max(steps, 50), warmup)
+    return {"ms_per_step": ms, "kernel_ms": kern_ms, "copies": copies, "bytes_per_launch": total_bytes,
+            "algorithmic_bytes_per_c1_call": w_bytes + k * 4 + n * 4, "gbs": total_bytes / (ms * 1e-3) / 1e9,
+            "single_call_us": one_kern * 1e3,
+            "single_call_gbs": (w_bytes + k * 4 + n * 4) / (one_kern * 1e-3) / 1e9,
+            "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": ach / HBM_PEAK_GBS, "traffic": None}}
+
+
+def bench_gemm(tn, L, steps, warmup):
+    m, k, n = 512, 4096, 14336
+    lib = L.lib()
+    rng = np.random.default_rng(3)
+    x = tn.tensor(rng.standard_normal((m, k)).astype(np.float32), dtype="bfloat16", device="hip")
+    q = tn._quantized_from_blob(_synth_q4_0_blob(n, k, 0.01, 33).tobytes(), (n, k), "q4_0", device="hip")
+    y = tn.empty((m, n), "bfloat16", "hip")
+
+    def step():
+        st = lib.tn_q4_0_linear(None, x.data_ptr(), L.TN_BF16, m, k, q._qs.data_ptr(), q._d.data_ptr(), n, None,
+                                y.data_ptr(), L.TN_BF16)
+        if st:
+            L.check(st)
+
+    ms, kern_ms = Timer(tn).run(step, steps, warmup)
+    flops = 2.0 * m * k * n
+    ach = flops / (kern_ms * 1e-3) / 1e12
+    return {"ms_per_step": ms, "kernel_ms": kern_ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
+            "bytes": n * (k // 32) * 18 + m * k * 2 + m * n * 2,
+            "roofline": {"bound": "mfma", "achieved": ach, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": ach / BF16_PEAK_TFLOPS, "traffic": None}}
+
+
+def bench_decode(tn, L, steps, warmup, sets=3):
+    B, Hq, Hkv, D, cap = 16, 32, 8, 128, 4096
+    lib = L.lib()
+    rng = np.random.default_rng(4)
+    lens_np = rng.integers(512, 4097, size=B).astype(np.int32)
+    lens = tn.tensor(lens_np, device="hip")
+    max_len = int(lens_np.max())
+    q = tn.tensor(rng.standard_normal((B, Hq, D)).astype(np.float32), dtype="bfloat16", device="hip")
+    caches = []
+    for s in range(sets):
+        kc = tn.empty((B, Hkv, cap, D), "bfloat16", "hip")
+        vc = tn.empty((B, Hkv, cap, D), "bfloat16", "hip")
+        for t in (kc, vc):
+            bits = tn.tensor(rng.standard_normal((B * Hkv * cap * D // 8,)).astype(np.float32), dtype="bfloat16",
+                             device="hip")
+            # fill with N(0,1) bf16 (8 repeats of a random block keep host memory small)
+            for r in range(8):
+                L.check(lib.tn_memcpy_d2d(t.data_ptr() + r * bits.nbytes, bits.data_ptr(), bits.nbytes, None))
+        caches.append((kc, vc))
+    out = tn.empty((B, Hq, D), "bfloat16", "hip")
+    lse = tn.empty((B, Hq), "float32", "hip")
+    idx = [0]
+
+    def step():
+        kc, vc = caches[idx[0] % sets]
+        idx[0] += 1
+        st = lib.tn_sdpa_decode(None, L.TN_BF16, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, Hq, Hkv, cap, D,
+                                lens.data_ptr(), max_len, float("nan"), out.data_ptr(), lse.data_ptr())
+        if st:
+            L.check(st)
+
+    ms, kern_ms = Timer(tn).run(step, steps, warmup)
+    kv_bytes = int(lens_np.sum()) * Hkv * D * 2 * 2
+    total = kv_bytes + 2 * B * Hq * D * 2
+    ach = total / (kern_ms * 1e-3) / 1e9
+    return {"ms_per_step": ms, "kernel_ms": kern_ms, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9,
+            "lens_sum": int(lens_np.sum()),
+            "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": ach / HBM_PEAK_GBS, "traffic": None}}
+
+
+def cpu_baseline_sdpa(threads):
+    """The oracle's restatement of the reference's default SDPA path (f32
+    body, bf16 in/out) on config 2 -- 4 of the 9 query heads (with their 2 KV
+    heads), scaled to the full workload's TFLOP/s."""
+    import oracle as O
+
+    rng = np.random.default_rng(2)
+    S, D = 2048, 64
+    hq, hkv = 3, 1  # one GQA group; x3 for the 9/3-head workload
+    q = O.bf16_to_f32(O.bf16_from_f32(rng.standard_normal((1, hq, S, D)).astype(np.float32)))
+    k = O.bf16_to_f32(O.bf16_from_f32(rng.standard_normal((1, hkv, S, D)).astype(np.float32)))
+    v = O.bf16_to_f32(O.bf16_from_f32(rng.standard_normal((1, hkv, S, D)).astype(np.float32)))
+    O.sdpa(q[:, :, :64], k, v, is_causal=True, threads=threads)  # warm
+    t0 = time.perf_counter()
+    out, _ = O.sdpa(q, k, v, is_causal=True, threads=threads)
+    O.bf16_from_f32(out)
+    sec = time.perf_counter() - t0
+    flops = 4.0 * D * hq * S * (S + 1) / 2  # the same algorithmic flop count as the GPU line
+    return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"config 2 restricted to one GQA group (3 of 9 query heads, 1 of 3 KV heads), causal, "
+                      f"bf16 inputs widened to f32; {sec:.2f} s for {flops / 1e9:.2f} GFLOP"}
+
+
+def cpu_threads():
+    n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c3,c4)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} asked); the path would shard by "
+              "KV-head group for SDPA and by output columns for the q4 linear, with no collective on the path. "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torchnative_amd as tn
+    from torchnative_amd import _lib as L
+
+    info = tn._hip_probe()
+    only = set(filter(None, args.only.split(",")))
+    want = (lambda p: not only or p in only)
+    parts = {}
+    if want("c1"):
+        print("bench: c1 q4_0 GEMV", file=sys.stderr, flush=True)
+        parts["c1_q4_gemv"] = bench_gemv(tn, L, args.steps, args.warmup)
+    if want("c2f32"):
+        print("bench: c2 SDPA prefill fp32", file=sys.stderr, flush=True)
+        parts["c2_sdpa_prefill_fp32"] = bench_sdpa(tn, L, "float32", args.steps, args.warmup)
+    if want("c3"):
+        print("bench: c3 q4_0 GEMM", file=sys.stderr, flush=True)
+        parts["c3_q4_gemm"] = bench_gemm(tn, L, args.steps, args.warmup)
+    if want("c4"):
+        print("bench: c4 decode attention", file=sys.stderr, flush=True)
+        parts["c4_decode_attention"] = bench_decode(tn, L, args.steps, args.warmup)
+    print("bench: c2 SDPA prefill bf16 (headline)", file=sys.stderr, flush=True)
+    head = bench_sdpa(tn, L, "bfloat16", args.steps, args.warmup)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("bench: cpu baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline_sdpa(cpu_threads())
+
+    line = {
+        "metric": "q4 GEMV HBM GB/s + SDPA TFLOP/s (% roofline); decode tokens/s, 1 GPU",
+        "value": head["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE config 2: causal GQA SDPA prefill, B=1, 9 q heads / 3 kv heads, "
+                               "head_dim 64, seq 2048, bf16 in/out, f32 accumulate",
+                   "flops_per_step": head["flops"]},
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "device": info.get("name"),
+        "parts": parts,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

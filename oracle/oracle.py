@@ -334,14 +334,16 @@ def synth_q4_0_weight(n, k, sigma, seed):
     return blob.tobytes()
 
 
-def sdpa_tolerance(ref32, ref64, kind="float32", p=None, v_abs=None):
+def sdpa_tolerance(ref32, ref64, kind="float32", p=None, got=None):
     """Per-element bound on |gpu - ref32| for one SDPA output tensor.
 
     The rule (docs/numerics/AGREE.md section 2 of the reference, applied per
     tensor): 4x the reference's own fp32-vs-fp64 distance, floored at 10 ulp
     (1.186e-6) of the tensor's scale. For a bf16 output add one bf16 ulp of
     |ref| (both sides round to bf16) and, when ``p``/``v_abs`` are given, the
-    P-narrowing term 2^-9 * sum_j P_ij |V_jd|."""
+    P-narrowing term 2^-9 * sum_j P_ij |V_jd| (pass ``p`` = that sum). The
+    bf16 spacing is taken at max(|ref|, |got|): a value just under a power of
+    two may round up across it."""
     ref32 = np.asarray(ref32, np.float64)
     ref64 = np.asarray(ref64, np.float64)
     fin = np.isfinite(ref64)
@@ -350,7 +352,7 @@ def sdpa_tolerance(ref32, ref64, kind="float32", p=None, v_abs=None):
     tol = max(4.0 * own, 1.186e-6 * scale_)
     tol = np.full(ref32.shape, tol)
     if kind == "bfloat16":
-        mag = np.abs(ref64)
+        mag = np.abs(ref64) if got is None else np.maximum(np.abs(ref64), np.abs(np.asarray(got, np.float64)))
         e = np.floor(np.log2(np.where(mag > 0, mag, 1e-38)))
         tol = tol + np.where(mag > 0, 2.0 ** (e - 7), 2.0 ** -133)
         if p is not None:

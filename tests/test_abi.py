@@ -1,0 +1,130 @@
+"""The C ABI library loads, exports every symbol include/tnhip.h declares, and
+its host-side argument checks refuse by name with the reference's wording.
+None of these calls reaches the GPU: every refusal happens before a HIP call.
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "tnhip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tn_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from torchnative_amd import _lib
+
+    return _lib.lib()
+
+
+def test_library_exports_every_declared_symbol(L):
+    from torchnative_amd import _lib
+
+    names = _declared_symbols()
+    assert len(names) >= 30
+    for name in names:
+        assert hasattr(L, name), name
+    # and the Python binding knows every one of them, with a signature
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+
+
+def test_abi_version_and_op_list(L):
+    assert L.tn_abi_version() == 1
+    ops = L.tn_ops().decode()
+    assert "torch._C._quantized_linear(q4_0)" in ops
+    assert "aten._scaled_dot_product_flash_attention_for_cpu.default" in ops
+
+
+def test_linear_refusals_use_the_reference_wording(L):
+    from torchnative_amd import _lib
+
+    # bf16/f32 only (quant.rs:299-306): float16 activation refused by name
+    st = L.tn_q4_0_linear(None, None, _lib.TN_F16, 1, 64, None, None, 8, None, None, _lib.TN_F32)
+    assert st == _lib.TN_ENOTIMPL
+    assert "activation must be float32" in _lib.last_error()
+    # K not a block multiple -> the shape error of quant.rs:326-331
+    st = L.tn_q4_0_linear(None, None, _lib.TN_F32, 1, 33, None, None, 8, None, None, _lib.TN_F32)
+    assert st == _lib.TN_EINVAL
+    assert "mat1 and mat2 shapes cannot be multiplied" in _lib.last_error()
+    # quantiser: last dim not a multiple of 32 (quant.rs:145-161)
+    st = L.tn_q4_0_quantize(None, None, 4, 48, None, None)
+    assert st == _lib.TN_ENOTIMPL
+    assert "must have their last dim divisible by block size -- got 48" in _lib.last_error()
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.TN_ENOTIMPL)
+
+
+def test_sdpa_refusals_name_the_reason(L):
+    from torchnative_amd import _lib
+
+    args = dict(B=1, Hq=9, Hkv=3, L=8, S=8, D=64)
+
+    def call(dtype=_lib.TN_BF16, mask=None, **kw):
+        a = {**args, **kw}
+        return L.tn_sdpa_fwd(None, dtype, None, None, None, a["B"], a["Hq"], a["Hkv"], a["L"], a["S"], a["D"],
+                             mask, 0, 1, float("nan"), None, None)
+
+    assert call(D=16) == _lib.TN_ENOTIMPL and "head_dim 16" in _lib.last_error()
+    assert call(Hkv=4) == _lib.TN_ENOTIMPL and "do not divide" in _lib.last_error()
+    assert call(S=0) == _lib.TN_ENOTIMPL and "zero key length" in _lib.last_error()
+    assert call(dtype=_lib.TN_F64) == _lib.TN_ENOTIMPL and "Double" in _lib.last_error()
+    assert call(mask=1) == _lib.TN_ENOTIMPL and "attn_mask" in _lib.last_error()
+    # empty batch: nothing to write, success without touching a pointer
+    assert call(B=0) == _lib.TN_OK
+    st = L.tn_sdpa_decode(None, _lib.TN_BF16, None, None, None, 2, 32, 8, 64, 128, None, 65, float("nan"),
+                          None, None)
+    assert st == _lib.TN_EINVAL and "max_len" in _lib.last_error()
+
+
+def test_counters_shape_and_refusal_count(L):
+    import torchnative_amd as tn
+
+    tn._C._hip_counters_reset()
+    before = tn._hip_counters()
+    assert set(before) == {"dispatches", "bytes_uploaded", "host_downloads", "bytes_downloaded", "refusals",
+                           "workspace_bytes"}
+    from torchnative_amd import _lib
+
+    L.tn_q4_0_quantize(None, None, 4, 48, None, None)
+    assert tn._hip_counters()["refusals"] == before["refusals"] + 1
+
+
+def test_python_mirror_refuses_host_operands_instead_of_falling_back():
+    import torchnative_amd as tn
+
+    x = tn.tensor(np.zeros((1, 64), np.float32))  # a cpu tensor
+    with pytest.raises(NotImplementedError, match="does not fall back to the host"):
+        tn._quantize(x, "q4_0")
+    with pytest.raises(NotImplementedError, match="activation-side block format"):
+        tn._quantize(x, "q8_1")
+    with pytest.raises(ValueError, match="needs 18 bytes; got 17"):
+        tn._quantized_from_blob(b"\0" * 17, (1, 32), "q4_0")
+    q = tn._quantized_from_blob(b"\0" * 36, (1, 64), "q4_0")  # stays on the host: no compute
+    assert tn._quantized_blob(q) == b"\0" * 36 and tn._quantized_nbytes(q) == 36
+    with pytest.raises(NotImplementedError, match="hip device"):
+        tn._quantized_linear(x, q)
+    with pytest.raises(NotImplementedError, match="is not implemented for the hip device"):
+        tn._aten_dispatch("aten.mm.default", x, x)
+    with pytest.raises(RuntimeError, match="Currently do not support dropout > 0"):
+        q4 = tn.tensor(np.zeros((1, 1, 2, 64), np.float32))
+        tn._aten_dispatch("aten._scaled_dot_product_flash_attention_for_cpu.default", q4, q4, q4, 0.5)
+
+
+def test_bf16_host_conversion_is_round_to_nearest_even():
+    from torchnative_amd.tensor import bf16_bits_from_f32
+
+    import oracle as O
+
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(10000).astype(np.float32),
+                        np.array([1.00390625, 1.005859375, np.inf, -np.inf, 0.0, -0.0], np.float32)])
+    assert np.array_equal(bf16_bits_from_f32(x), O.bf16_from_f32(x))

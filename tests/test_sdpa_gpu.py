@@ -1,0 +1,185 @@
+"""SDPA on the MI355X against the CPU oracle of the reference's default path.
+
+Tolerance (written out in `_bound`): per output tensor, 4x the reference's own
+fp32-vs-fp64 distance on the same inputs, floored at 1.186e-6 of the tensor's
+scale (the reference's docs/numerics/AGREE.md section 2 rule). A bf16 run adds
+one bf16 ulp of |ref| (both sides round to bf16) and the P-narrowing term
+2^-9 * sum_j P_ij |V_jd| (upstream's blocked kernel narrows P to bf16 between
+the products, flash.rs:503-516). The lse is compared in f32 with the same
+base rule.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+OP = "aten._scaled_dot_product_flash_attention_for_cpu.default"
+
+
+@pytest.fixture(scope="module")
+def tn():
+    import torchnative_amd as tn
+
+    print("device:", tn._hip_probe(), flush=True)
+    return tn
+
+
+def _det(shape, seed):
+    return np.array(O.sdpa_det(int(np.prod(shape)), seed), dtype=np.float64).reshape(shape)
+
+
+def _bound(ref32, ref64, pav=None, bf16=False, got=None):
+    own = float(np.max(np.abs(ref32.astype(np.float64) - ref64)))
+    scale = float(np.max(np.abs(ref64)))
+    tol = np.full(ref64.shape, max(4.0 * own, 1.186e-6 * scale))
+    if bf16:
+        # both sides round to bf16: half a spacing each, taken at the larger
+        # magnitude (a value just under a power of two may round up across it)
+        mag = np.abs(ref64) if got is None else np.maximum(np.abs(ref64), np.abs(got))
+        e = np.floor(np.log2(np.where(mag > 0, mag, 2.0 ** -126)))
+        tol = tol + 2.0 ** (e - 7) + 2.0 ** -9 * pav
+    return tol
+
+
+def _run(tn, dtype, q, k, v, causal, threads=16):
+    """GPU result plus the oracle's f32 and f64 answers on the same inputs."""
+    B, Hq, L, D = q.shape
+    if dtype == "bfloat16":
+        qb, kb, vb = (tn.tensor(a.astype(np.float32), dtype="bfloat16", device="hip") for a in (q, k, v))
+        qw, kw, vw = (t.numpy().astype(np.float64) for t in (qb, kb, vb))  # exact widening
+        o, lse = tn._aten_dispatch(OP, qb, kb, vb, 0.0, causal)
+    else:
+        qw, kw, vw = (a.astype(np.float32).astype(np.float64) for a in (q, k, v))
+        o, lse = tn._aten_dispatch(OP, *(tn.tensor(a.astype(np.float32), device="hip") for a in (q, k, v)), 0.0,
+                                   causal)
+    r32, l32 = O.sdpa(qw, kw, vw, is_causal=causal, threads=threads)
+    r64, l64 = O.sdpa(qw, kw, vw, is_causal=causal, threads=threads, dtype=np.float64)
+    pav = None
+    if dtype == "bfloat16":
+        pav, _ = O.sdpa(qw, kw, np.abs(vw), is_causal=causal, threads=threads, dtype=np.float64)
+    return o, lse, (r32, l32, r64, l64, pav)
+
+
+def _check(tn, dtype, q, k, v, causal):
+    o, lse, (r32, l32, r64, l64, pav) = _run(tn, dtype, q, k, v, causal)
+    got = o.numpy().astype(np.float64)
+    if dtype == "bfloat16":
+        ref = O.bf16_to_f32(O.bf16_from_f32(r32)).astype(np.float64)
+        tol = _bound(r32, r64, pav, bf16=True, got=got)
+    else:
+        ref = r32.astype(np.float64)
+        tol = _bound(r32, r64)
+    err = np.abs(got - ref)
+    assert np.all(np.isfinite(got))
+    worst = float(np.max(err / tol))
+    assert worst <= 1.0, f"{dtype} causal={causal} {q.shape}x{k.shape}: {worst:.3g}x the bound, max err {err.max():.3g}"
+    lt = _bound(l32, l64)
+    lerr = float(np.max(np.abs(lse.numpy().astype(np.float64) - l32) / lt))
+    assert lerr <= 1.0, f"lse {lerr:.3g}x the bound"
+    return worst
+
+
+SHAPES = [
+    # (batch, q heads, kv heads, q_len, kv_len, head_dim)
+    (1, 9, 3, 26, 26, 64),       # the reference's _SDPA_SHAPES entry with D=64 (test_shim.py:12077)
+    (1, 2, 2, 33, 33, 64),       # second query block (cases.py:11430)
+    (1, 2, 2, 70, 70, 128),      # three query blocks
+    (1, 1, 1, 40, 600, 64),      # past the 512-key split (cases.py:11433)
+    (2, 8, 2, 65, 130, 128),     # tails in both dims, batch 2, GQA 4
+    (1, 4, 4, 2, 5, 64),         # q_len < kv_len: upper-left causal
+    (1, 3, 1, 100, 37, 64),      # q_len > kv_len
+]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_sdpa_matches_the_oracle_within_the_derived_bound(tn, shape, causal, dtype):
+    b, hq, hkv, l, s, d = shape
+    q, k, v = _det((b, hq, l, d), 1), _det((b, hkv, s, d), 2), _det((b, hkv, s, d), 3)
+    _check(tn, dtype, q, k, v, causal)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_config2_causal_gqa_prefill_at_full_size(tn, dtype):
+    """B=1, 9 q heads / 3 kv heads, D=64, S=2048, causal,
+    Q/K/V ~ N(0,1), scale 1/8."""
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((1, 9, 2048, 64))
+    k = rng.standard_normal((1, 3, 2048, 64))
+    v = rng.standard_normal((1, 3, 2048, 64))
+    worst = _check(tn, dtype, q, k, v, True)
+    print(f"config 2 {dtype}: worst error {worst:.3f} of the bound", flush=True)
+
+
+def test_default_scale_and_explicit_scale_agree(tn):
+    rng = np.random.default_rng(5)
+    q, k, v = (tn.tensor(rng.standard_normal(s).astype(np.float32), device="hip")
+               for s in ((1, 2, 16, 64), (1, 2, 16, 64), (1, 2, 16, 64)))
+    a, la = tn._aten_dispatch(OP, q, k, v, 0.0, False)
+    b, lb = tn._aten_dispatch(OP, q, k, v, 0.0, False, scale=1.0 / math.sqrt(64))
+    assert np.array_equal(a.numpy(), b.numpy()) and np.array_equal(la.numpy(), lb.numpy())
+
+
+def test_gqa_is_indexed_not_tiled(tn):
+    """Query head i reads kv head i // n_rep: equal to running each head alone."""
+    rng = np.random.default_rng(6)
+    q = rng.standard_normal((1, 6, 20, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 20, 64)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 20, 64)).astype(np.float32)
+    o, _ = tn._aten_dispatch(OP, *(tn.tensor(a, device="hip") for a in (q, k, v)), 0.0, True)
+    full = o.numpy()
+    for h in range(6):
+        kh = h // 3
+        oh, _ = tn._aten_dispatch(OP, tn.tensor(q[:, h:h + 1], device="hip"), tn.tensor(k[:, kh:kh + 1], device="hip"),
+                                  tn.tensor(v[:, kh:kh + 1], device="hip"), 0.0, True)
+        assert np.array_equal(oh.numpy()[:, 0], full[:, h])
+
+
+def _decode_case(tn, B, Hq, Hkv, D, lens, cap, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float32)
+    kc = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+    vc = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+    qb = tn.tensor(q, dtype="bfloat16", device="hip")
+    kb = tn.tensor(kc, dtype="bfloat16", device="hip")
+    vb = tn.tensor(vc, dtype="bfloat16", device="hip")
+    ln = tn.tensor(np.asarray(lens, np.int32), device="hip")
+    o, lse = tn.sdpa_decode(qb, kb, vb, ln, max(lens))
+    got = o.numpy().astype(np.float64)
+    glse = lse.numpy().astype(np.float64)
+    qw, kw, vw = qb.numpy(), kb.numpy(), vb.numpy()
+    worst = 0.0
+    for b in range(B):
+        L = lens[b]
+        args = (qw[b:b + 1, :, None, :], kw[b:b + 1, :, :L], vw[b:b + 1, :, :L])
+        r32, l32 = O.sdpa(*args)
+        r64, l64 = O.sdpa(*args, dtype=np.float64)
+        pav, _ = O.sdpa(args[0], args[1], np.abs(args[2]), dtype=np.float64)
+        ref = O.bf16_to_f32(O.bf16_from_f32(r32)).astype(np.float64)
+        tol = _bound(r32, r64, pav, bf16=True, got=got[b:b + 1, :, None, :])
+        err = np.abs(got[b:b + 1, :, None, :] - ref)
+        worst = max(worst, float(np.max(err / tol)))
+        lt = _bound(l32, l64)
+        assert float(np.max(np.abs(glse[b:b + 1, :, None] - l32) / lt)) <= 1.0
+    assert worst <= 1.0, worst
+    return worst
+
+
+def test_decode_small_and_ragged(tn):
+    _decode_case(tn, 3, 8, 2, 128, [1, 77, 300], 320, 7)
+    _decode_case(tn, 2, 4, 4, 64, [129, 64], 200, 8)
+    _decode_case(tn, 2, 16, 1, 128, [513, 5], 600, 9)
+
+
+def test_config4_decode_attention_at_full_size(tn):
+    """B=16, 32 q heads / 8 kv heads, D=128, bf16, cache
+    lengths uniform in [512, 4096]."""
+    rng = np.random.default_rng(4)
+    lens = [int(x) for x in rng.integers(512, 4097, size=16)]
+    worst = _decode_case(tn, 16, 32, 8, 128, lens, 4096, 44)
+    print(f"config 4: worst error {worst:.3f} of the bound", flush=True)

@@ -1,0 +1,112 @@
+"""ctypes binding of libtnhip.so (the C ABI declared in include/tnhip.h).
+
+The library is required: if it is not built, importing a compute entry point
+raises, naming the build command. Nothing here falls back to the host.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtnhip.so")
+
+TN_OK, TN_EINVAL, TN_ENOTIMPL, TN_EHIP, TN_EVALUE = 0, 1, 2, 3, 4
+TN_F32, TN_BF16, TN_F16, TN_F64 = 0, 1, 2, 3
+
+# every symbol include/tnhip.h declares, with (restype, argtypes)
+_P, _I64, _I, _D, _SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double, ctypes.c_size_t
+
+
+class Counters(ctypes.Structure):
+    _fields_ = [
+        ("dispatches", ctypes.c_uint64),
+        ("bytes_uploaded", ctypes.c_uint64),
+        ("host_downloads", ctypes.c_uint64),
+        ("bytes_downloaded", ctypes.c_uint64),
+        ("refusals", ctypes.c_uint64),
+        ("workspace_bytes", ctypes.c_uint64),
+    ]
+
+
+SIGNATURES = {
+    "tn_last_error": (ctypes.c_char_p, []),
+    "tn_abi_version": (_I, []),
+    "tn_probe": (_I, [ctypes.c_char_p, _SZ]),
+    "tn_counters": (_I, [ctypes.POINTER(Counters)]),
+    "tn_counters_reset": (_I, []),
+    "tn_ops": (ctypes.c_char_p, []),
+    "tn_device_count": (_I, [ctypes.POINTER(_I)]),
+    "tn_set_device": (_I, [_I]),
+    "tn_get_device": (_I, [ctypes.POINTER(_I)]),
+    "tn_malloc": (_I, [ctypes.POINTER(_P), _SZ]),
+    "tn_free": (_I, [_P]),
+    "tn_memcpy_h2d": (_I, [_P, _P, _SZ, _P]),
+    "tn_memcpy_d2h": (_I, [_P, _P, _SZ, _P]),
+    "tn_memcpy_d2d": (_I, [_P, _P, _SZ, _P]),
+    "tn_memset": (_I, [_P, _I, _SZ, _P]),
+    "tn_stream_create": (_I, [ctypes.POINTER(_P)]),
+    "tn_stream_destroy": (_I, [_P]),
+    "tn_stream_synchronize": (_I, [_P]),
+    "tn_device_synchronize": (_I, []),
+    "tn_event_create": (_I, [ctypes.POINTER(_P)]),
+    "tn_event_destroy": (_I, [_P]),
+    "tn_event_record": (_I, [_P, _P]),
+    "tn_event_synchronize": (_I, [_P]),
+    "tn_event_elapsed_ms": (_I, [ctypes.POINTER(ctypes.c_float), _P, _P]),
+    "tn_q4_0_from_blob": (_I, [_P, _P, _I64, _I64, _P, _P]),
+    "tn_q4_0_to_blob": (_I, [_P, _P, _P, _I64, _I64, _P]),
+    "tn_q4_0_quantize": (_I, [_P, _P, _I64, _I64, _P, _P]),
+    "tn_q4_0_dequantize": (_I, [_P, _P, _P, _I64, _I64, _P]),
+    "tn_q4_0_linear": (_I, [_P, _P, _I, _I64, _I64, _P, _P, _I64, _P, _P, _I]),
+    "tn_sdpa_fwd": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I, _I, _D, _P, _P]),
+    "tn_sdpa_decode": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _D, _P, _P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class HipLibraryMissing(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded libtnhip.so. Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise HipLibraryMissing(
+                f"torchnative_amd: {LIB_PATH} is not built; run `python -m torchnative_amd.build` "
+                "(hipcc --offload-arch=gfx950). There is no host fallback."
+            )
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().tn_last_error()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def check(status: int) -> None:
+    """Map a tn_status onto the exception the reference raises (err.rs:11-28)."""
+    if status == TN_OK:
+        return
+    msg = last_error()
+    if status == TN_ENOTIMPL:
+        raise NotImplementedError(msg)
+    if status == TN_EVALUE:
+        raise ValueError(msg)
+    raise RuntimeError(msg)

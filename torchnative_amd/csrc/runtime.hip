@@ -1,0 +1,258 @@
+// tnhip runtime: errors, probe, counters, device memory, streams, events and
+// the per-(device, stream) workspace.
+//
+// The error/refusal convention follows torchnative's err.rs:11-28 (refusals
+// are NotImplementedError naming the reason; runtime failures RuntimeError),
+// the probe/counter shape follows device.rs:1671-1708 and vulkan.rs:2138-2268.
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "tn_common.h"
+
+namespace tn {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+tn_status fail(tn_status code, const std::string& msg) {
+    g_last_error = msg;
+    if (code == TN_ENOTIMPL) counters().refusals.fetch_add(1);
+    return code;
+}
+
+tn_status hip_fail(hipError_t e, const char* what) {
+    char buf[512];
+    std::snprintf(buf, sizeof buf, "tnhip: HIP error %d (%s) in %s", (int)e, hipGetErrorString(e), what);
+    return fail(TN_EHIP, buf);
+}
+
+Counters& counters() {
+    static Counters c;
+    return c;
+}
+
+namespace {
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+}  // namespace
+
+tn_status workspace(hipStream_t stream, size_t bytes, void** out) {
+    int dev = 0;
+    TN_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace& w = g_ws[{dev, stream}];
+    if (w.bytes < bytes) {
+        size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+        want = (want + 4095) & ~(size_t)4095;
+        if (w.ptr) {
+            // the old buffer may still be read by work queued on this stream
+            TN_HIP(hipStreamSynchronize(stream));
+            TN_HIP(hipFree(w.ptr));
+            counters().workspace_bytes.fetch_sub(w.bytes);
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        TN_HIP(hipMalloc(&w.ptr, want));
+        w.bytes = want;
+        counters().workspace_bytes.fetch_add(want);
+    }
+    *out = w.ptr;
+    return TN_OK;
+}
+
+}  // namespace tn
+
+using namespace tn;
+
+extern "C" {
+
+const char* tn_last_error(void) { return g_last_error.c_str(); }
+
+int tn_abi_version(void) { return TN_ABI_VERSION; }
+
+const char* tn_ops(void) {
+    return "torch._C._quantize(q4_0),torch._C._dequantize(q4_0),torch._C._quantized_linear(q4_0),"
+           "torch._C._quantized_to,torch._C._quantized_blob,"
+           "aten._scaled_dot_product_flash_attention_for_cpu.default,sdpa_decode";
+}
+
+tn_status tn_probe(char* buf, size_t len) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0)
+        return fail(TN_ENOTIMPL, e != hipSuccess
+                                     ? std::string("tnhip: no_driver: hipGetDeviceCount failed: ") + hipGetErrorString(e)
+                                     : std::string("tnhip: no_device: the HIP runtime sees no GPU"));
+    int dev = 0;
+    TN_HIP(hipGetDevice(&dev));
+    hipDeviceProp_t p;
+    TN_HIP(hipGetDeviceProperties(&p, dev));
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(TN_ENOTIMPL, std::string("tnhip: wrong_arch: this library is built for gfx950 (MI355X), "
+                                             "the current device is ") + p.gcnArchName);
+    if (buf && len) {
+        std::snprintf(buf, len, "name=%s;arch=%s;cus=%d;hbm_bytes=%zu;clock_khz=%d;devices=%d;device=%d",
+                      p.name, p.gcnArchName, p.multiProcessorCount, (size_t)p.totalGlobalMem, p.clockRate, n,
+                      dev);
+    }
+    return TN_OK;
+}
+
+tn_status tn_counters(tn_counters_t* out) {
+    if (!out) return fail(TN_EVALUE, "tn_counters: null output");
+    Counters& c = counters();
+    out->dispatches = c.dispatches.load();
+    out->bytes_uploaded = c.bytes_uploaded.load();
+    out->host_downloads = c.host_downloads.load();
+    out->bytes_downloaded = c.bytes_downloaded.load();
+    out->refusals = c.refusals.load();
+    out->workspace_bytes = c.workspace_bytes.load();
+    return TN_OK;
+}
+
+tn_status tn_counters_reset(void) {
+    Counters& c = counters();
+    c.dispatches = 0;
+    c.bytes_uploaded = 0;
+    c.host_downloads = 0;
+    c.bytes_downloaded = 0;
+    c.refusals = 0;
+    return TN_OK;
+}
+
+tn_status tn_device_count(int* n) {
+    hipError_t e = hipGetDeviceCount(n);
+    if (e == hipErrorNoDevice) {
+        *n = 0;
+        return TN_OK;
+    }
+    TN_HIP(e);
+    return TN_OK;
+}
+
+tn_status tn_set_device(int ordinal) {
+    TN_HIP(hipSetDevice(ordinal));
+    return TN_OK;
+}
+
+tn_status tn_get_device(int* ordinal) {
+    TN_HIP(hipGetDevice(ordinal));
+    return TN_OK;
+}
+
+tn_status tn_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(TN_EVALUE, "tn_malloc: null output");
+    *ptr = nullptr;
+    if (bytes == 0) return TN_OK;
+    TN_HIP(hipMalloc(ptr, bytes));
+    return TN_OK;
+}
+
+tn_status tn_free(void* ptr) {
+    if (ptr) TN_HIP(hipFree(ptr));
+    return TN_OK;
+}
+
+tn_status tn_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (!bytes) return TN_OK;
+    TN_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+    TN_HIP(hipStreamSynchronize((hipStream_t)stream));  // the host buffer may be freed on return
+    counters().bytes_uploaded.fetch_add(bytes);
+    return TN_OK;
+}
+
+tn_status tn_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+    counters().host_downloads.fetch_add(1);
+    if (!bytes) return TN_OK;
+    TN_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    TN_HIP(hipStreamSynchronize((hipStream_t)stream));
+    counters().bytes_downloaded.fetch_add(bytes);
+    return TN_OK;
+}
+
+tn_status tn_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (!bytes) return TN_OK;
+    TN_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    return TN_OK;
+}
+
+tn_status tn_memset(void* dst, int value, size_t bytes, void* stream) {
+    if (!bytes) return TN_OK;
+    TN_HIP(hipMemsetAsync(dst, value, bytes, (hipStream_t)stream));
+    return TN_OK;
+}
+
+tn_status tn_stream_create(void** stream) {
+    hipStream_t s;
+    TN_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return TN_OK;
+}
+
+tn_status tn_stream_destroy(void* stream) {
+    if (stream) {
+        {
+            int dev = 0;
+            TN_HIP(hipGetDevice(&dev));
+            std::lock_guard<std::mutex> lock(g_ws_mu);
+            auto it = g_ws.find({dev, (hipStream_t)stream});
+            if (it != g_ws.end()) {
+                TN_HIP(hipStreamSynchronize((hipStream_t)stream));
+                if (it->second.ptr) {
+                    TN_HIP(hipFree(it->second.ptr));
+                    counters().workspace_bytes.fetch_sub(it->second.bytes);
+                }
+                g_ws.erase(it);
+            }
+        }
+        TN_HIP(hipStreamDestroy((hipStream_t)stream));
+    }
+    return TN_OK;
+}
+
+tn_status tn_stream_synchronize(void* stream) {
+    TN_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return TN_OK;
+}
+
+tn_status tn_device_synchronize(void) {
+    TN_HIP(hipDeviceSynchronize());
+    return TN_OK;
+}
+
+tn_status tn_event_create(void** event) {
+    hipEvent_t e;
+    TN_HIP(hipEventCreate(&e));
+    *event = e;
+    return TN_OK;
+}
+
+tn_status tn_event_destroy(void* event) {
+    if (event) TN_HIP(hipEventDestroy((hipEvent_t)event));
+    return TN_OK;
+}
+
+tn_status tn_event_record(void* event, void* stream) {
+    TN_HIP(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+    return TN_OK;
+}
+
+tn_status tn_event_synchronize(void* event) {
+    TN_HIP(hipEventSynchronize((hipEvent_t)event));
+    return TN_OK;
+}
+
+tn_status tn_event_elapsed_ms(float* ms, void* start, void* end) {
+    TN_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
+    return TN_OK;
+}
+
+}  // extern "C"
