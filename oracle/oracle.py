@@ -339,11 +339,11 @@ def sdpa_tolerance(ref32, ref64, kind="float32", p=None, got=None):
 
     The rule (docs/numerics/AGREE.md section 2 of the reference, applied per
     tensor): 4x the reference's own fp32-vs-fp64 distance, floored at 10 ulp
-    (1.186e-6) of the tensor's scale. For a bf16 output add one bf16 ulp of
-    |ref| (both sides round to bf16) and, when ``p``/``v_abs`` are given, the
-    P-narrowing term 2^-9 * sum_j P_ij |V_jd| (pass ``p`` = that sum). The
-    bf16 spacing is taken at max(|ref|, |got|): a value just under a power of
-    two may round up across it."""
+    (1.186e-6) of the tensor's scale. For a bf16 output add one bf16 ulp
+    (both sides round to bf16; the spacing is taken at max(|ref|, |got|), as a
+    value just under a power of two may round up across it) and, when ``p`` is
+    given, the P-narrowing term u * sum_j P_ij |V_jd| with u = 2^-8, bf16's
+    unit roundoff (pass ``p`` = that sum: the attention output with |V|)."""
     ref32 = np.asarray(ref32, np.float64)
     ref64 = np.asarray(ref64, np.float64)
     fin = np.isfinite(ref64)
@@ -356,5 +356,5 @@ def sdpa_tolerance(ref32, ref64, kind="float32", p=None, got=None):
         e = np.floor(np.log2(np.where(mag > 0, mag, 1e-38)))
         tol = tol + np.where(mag > 0, 2.0 ** (e - 7), 2.0 ** -133)
         if p is not None:
-            tol = tol + 2.0 ** -9 * p
+            tol = tol + 2.0 ** -8 * np.asarray(p, np.float64)
     return tol

@@ -3,10 +3,10 @@
 Tolerance (written out in `_bound`): per output tensor, 4x the reference's own
 fp32-vs-fp64 distance on the same inputs, floored at 1.186e-6 of the tensor's
 scale (the reference's docs/numerics/AGREE.md section 2 rule). A bf16 run adds
-one bf16 ulp of |ref| (both sides round to bf16) and the P-narrowing term
-2^-9 * sum_j P_ij |V_jd| (upstream's blocked kernel narrows P to bf16 between
-the products, flash.rs:503-516). The lse is compared in f32 with the same
-base rule.
+one bf16 ulp of max(|ref|, |gpu|) (both sides round to bf16) and the
+P-narrowing term u * sum_j P_ij |V_jd| with u = 2^-8, bf16's unit roundoff
+(upstream's blocked kernel narrows P to bf16 between the products,
+flash.rs:503-516). The lse is compared in f32 with the same base rule.
 """
 
 import math
@@ -33,16 +33,7 @@ def _det(shape, seed):
 
 
 def _bound(ref32, ref64, pav=None, bf16=False, got=None):
-    own = float(np.max(np.abs(ref32.astype(np.float64) - ref64)))
-    scale = float(np.max(np.abs(ref64)))
-    tol = np.full(ref64.shape, max(4.0 * own, 1.186e-6 * scale))
-    if bf16:
-        # both sides round to bf16: half a spacing each, taken at the larger
-        # magnitude (a value just under a power of two may round up across it)
-        mag = np.abs(ref64) if got is None else np.maximum(np.abs(ref64), np.abs(got))
-        e = np.floor(np.log2(np.where(mag > 0, mag, 2.0 ** -126)))
-        tol = tol + 2.0 ** (e - 7) + 2.0 ** -9 * pav
-    return tol
+    return O.sdpa_tolerance(ref32, ref64, "bfloat16" if bf16 else "float32", p=pav, got=got)
 
 
 def _run(tn, dtype, q, k, v, causal, threads=16):

@@ -155,6 +155,8 @@ constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_ITEMS = 4;  // (row, block) items per thread
 constexpr int GEMV_MAX_M = 4;
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 __device__ inline int dot_block(uint4 w, const int* __restrict__ xw) {
     // xw: the 32 int8 codes of the block as 8 dwords, natural element order.
     // w dword j holds bytes 4j..4j+3: low nibbles = elements 4j..4j+3, high
@@ -205,51 +207,73 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
     }
     __syncthreads();
 
-    // phase 2: stream the weight
-    const int64_t row0 = (int64_t)blockIdx.x * rows;
-    const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
-    const int total = nrows * nb;
-    const uint8_t* qbase = qs + row0 * nb * 16;
-    const uint16_t* dbase = dw + row0 * nb;
-    uint4 wv[GEMV_ITEMS];
-    uint16_t dv[GEMV_ITEMS];
+    // phase 2/3, persistent over row tiles: the next tile's weight loads are in
+    // flight while this tile's terms are computed and summed; the terms live
+    // in two LDS buffers, so one barrier per tile suffices
+    const int ntiles = (N + rows - 1) / rows;
+    const int tstride = (int)gridDim.x;
+    uint4 wv[GEMV_ITEMS], wn[GEMV_ITEMS];
+    uint16_t dv[GEMV_ITEMS], dn[GEMV_ITEMS];
+    auto gload = [&](int tile, uint4* wr, uint16_t* dr) {
+        const int64_t row0 = (int64_t)tile * rows;
+        const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
+        const int total = nrows * nb;
+        const uint4* qbase = reinterpret_cast<const uint4*>(qs) + row0 * nb;
+        const uint16_t* dbase = dw + row0 * nb;
 #pragma unroll
-    for (int it = 0; it < GEMV_ITEMS; it++) {
-        const int g = tid + it * GEMV_THREADS;
-        if (g < total) {
-            wv[it] = reinterpret_cast<const uint4*>(qbase)[g];
-            dv[it] = dbase[g];
-        }
-    }
-#pragma unroll
-    for (int it = 0; it < GEMV_ITEMS; it++) {
-        const int g = tid + it * GEMV_THREADS;
-        if (g < total) {
-            const int r = g / nb, b = g - r * nb;
-            const float dwf = f16_to_f32(dv[it]);
-#pragma unroll
-            for (int mr = 0; mr < MR; mr++) {
-                int s = dot_block(wv[it], xq + mr * (K / 4) + b * 8) - 8 * sxs[mr * nb + b];
-                float t = (float)s * dwf;
-                t = t * dxs[mr * nb + b];
-                terms[(r * MR + mr) * nb + b] = t;
+        for (int it = 0; it < GEMV_ITEMS; it++) {
+            const int g = tid + it * GEMV_THREADS;
+            if (g < total) {
+                // streamed once: a non-temporal load keeps it from evicting x and the terms
+                const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(qbase + g));
+                wr[it] = make_uint4(v[0], v[1], v[2], v[3]);
+                dr[it] = dbase[g];
             }
         }
-    }
-    __syncthreads();
-
-    // phase 3: each output's terms in block order
-    for (int o = tid; o < nrows * MR; o += GEMV_THREADS) {
-        const int r = o / MR, mr = o - r * MR;
-        const float* tr = terms + (r * MR + mr) * nb;
-        float acc = 0.0f;
-        for (int b = 0; b < nb; b++) acc = acc + tr[b];
-        const int64_t n = row0 + r;
-        if (bias) acc = acc + bias[n];
-        if (y_bf16)
-            reinterpret_cast<uint16_t*>(y)[(int64_t)mr * N + n] = bf16_from_f32(acc);
-        else
-            reinterpret_cast<float*>(y)[(int64_t)mr * N + n] = acc;
+    };
+    int tile = (int)blockIdx.x;
+    if (tile < ntiles) gload(tile, wv, dv);
+    for (int buf = 0; tile < ntiles; tile += tstride, buf ^= 1) {
+        const int next = tile + tstride;
+        if (next < ntiles) gload(next, wn, dn);
+        const int64_t row0 = (int64_t)tile * rows;
+        const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
+        const int total = nrows * nb;
+        float* tb = terms + buf * rows * MR * nb;
+#pragma unroll
+        for (int it = 0; it < GEMV_ITEMS; it++) {
+            const int g = tid + it * GEMV_THREADS;
+            if (g < total) {
+                const int r = g / nb, b = g - r * nb;
+                const float dwf = f16_to_f32(dv[it]);
+#pragma unroll
+                for (int mr = 0; mr < MR; mr++) {
+                    int s = dot_block(wv[it], xq + mr * (K / 4) + b * 8) - 8 * sxs[mr * nb + b];
+                    float t = (float)s * dwf;
+                    t = t * dxs[mr * nb + b];
+                    tb[(r * MR + mr) * nb + b] = t;
+                }
+            }
+        }
+        __syncthreads();
+        // each output's terms in block order
+        for (int o = tid; o < nrows * MR; o += GEMV_THREADS) {
+            const int r = o / MR, mr = o - r * MR;
+            const float* tr = tb + (r * MR + mr) * nb;
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) acc = acc + tr[b];
+            const int64_t n = row0 + r;
+            if (bias) acc = acc + bias[n];
+            if (y_bf16)
+                reinterpret_cast<uint16_t*>(y)[(int64_t)mr * N + n] = bf16_from_f32(acc);
+            else
+                reinterpret_cast<float*>(y)[(int64_t)mr * N + n] = acc;
+        }
+#pragma unroll
+        for (int it = 0; it < GEMV_ITEMS; it++) {
+            wv[it] = wn[it];
+            dv[it] = dn[it];
+        }
     }
 }
 
@@ -261,20 +285,33 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
 //
 // Main kernel: a 128x128 output tile per workgroup, four waves as 2x2, each
 // wave 64x64 = 4x4 tiles of v_mfma_f32_16x16x32_bf16. The K loop walks blocks
-// in order. One MFMA over one 32-element block, started from a zero
-// accumulator, yields the block's integer dot exactly: products are at most
-// 8*127 and the 32-term sum at most 32512 < 2^24. The weight nibbles are
-// widened to bf16 codes (nib - 8) once per workgroup in LDS.
+// in order, double-buffered in LDS: the next block's loads are issued into
+// registers before the current block is computed.
+//
+// Exactness. The weight codes enter the MFMA as bf16(128 + nib), built by one
+// byte permute per two nibbles (the bf16 bit pattern of 128 + n is 0x4300 | n),
+// and the accumulator starts at -136 * sum_j(x codes) for the row, so the MFMA
+// returns sum_j (nib_j - 8) * q_j = the block's integer dot S_b exactly: every
+// product (<= 143*127), every partial sum and the start value stay below 2^24
+// in magnitude, so no fp32 step rounds. S_b then gets the reference's two
+// roundings, (S_b * d_w) * d_x, and one addition into the running sum, in
+// block order.
 //
 // K-slot order: MFMA lane group g (lanes 16g..16g+15) holds 8 of the 32 block
 // elements, {4g..4g+3, 16+4g..16+4g+3}: the low and high nibbles of weight
 // bytes 4g..4g+3. The activation codes are stored in the same order, so the
 // two operands agree element for element.
+//
+// Tile order is XCD-aware: consecutive workgroups go to different XCDs, so the
+// workgroup index is remapped such that each XCD works on a contiguous range
+// of weight columns and reads those columns into its own L2 once for all the
+// row tiles.
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int GM_BM = 128, GM_BN = 128, GM_THREADS = 256;
+constexpr int NUM_XCD = 8;
 
 __device__ inline int kslot_of_element(int e) {  // element (0..31) -> K slot
     return e < 16 ? 8 * (e >> 2) + (e & 3) : 8 * ((e - 16) >> 2) + 4 + (e & 3);
@@ -282,7 +319,8 @@ __device__ inline int kslot_of_element(int e) {  // element (0..31) -> K slot
 
 template <typename XT>
 __global__ __launch_bounds__(256) void k_q8_rows(const XT* __restrict__ x, int M, int M_pad, int K, int nb,
-                                               uint16_t* __restrict__ xc, float* __restrict__ dxT) {
+                                               uint16_t* __restrict__ xc, float* __restrict__ dxT,
+                                               float* __restrict__ corrT) {
     // one 32-lane group per (row, block); rows >= M become zero codes, zero scale
     const int64_t blk = (int64_t)blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5);
     const int lane = threadIdx.x & 31;
@@ -294,35 +332,48 @@ __global__ __launch_bounds__(256) void k_q8_rows(const XT* __restrict__ x, int M
         float v = load_x<XT>(x + (int64_t)row * K + b * QK + lane);
         q = q8_0_lane(v, &dx);
     }
+    int s = q;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off, 32);
     xc[blk * QK + kslot_of_element(lane)] = (uint16_t)(__builtin_bit_cast(uint32_t, (float)q) >> 16);
-    if (lane == 0) dxT[(int64_t)b * M_pad + row] = dx;
+    if (lane == 0) {
+        dxT[(int64_t)b * M_pad + row] = dx;
+        corrT[(int64_t)b * M_pad + row] = (float)(-136 * s);
+    }
 }
 
-__device__ inline uint32_t pack_bf16_codes(uint32_t n0, uint32_t n1) {
-    // two nibbles -> bf16(n0 - 8) | bf16(n1 - 8) << 16 (small integers: exact,
-    // the low 16 bits of the f32 are zero)
-    uint32_t a = __builtin_bit_cast(uint32_t, (float)((int)n0 - 8));
-    uint32_t b = __builtin_bit_cast(uint32_t, (float)((int)n1 - 8));
-    return (a >> 16) | (b & 0xffff0000u);
-}
+// bytes 0,1 (or 2,3) of x -> the bf16 pair (128 + byte0, 128 + byte1): the
+// high byte of each half comes from the constant 0x43
+__device__ inline uint32_t codes_pair01(uint32_t x) { return __builtin_amdgcn_perm(0x43434343u, x, 0x04010400u); }
+__device__ inline uint32_t codes_pair23(uint32_t x) { return __builtin_amdgcn_perm(0x43434343u, x, 0x04030402u); }
+
+constexpr int GM_AS = QK + 8;  // LDS row stride (bf16) of the code tiles: 80 B, conflict-free b128 reads
 
 __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict__ xc,
-                                                    const float* __restrict__ dxT, int M, int M_pad, int nb,
+                                                    const float* __restrict__ dxT,
+                                                    const float* __restrict__ corrT, int M, int M_pad, int nb,
                                                     const uint8_t* __restrict__ qs,
                                                     const uint16_t* __restrict__ dw, int N,
                                                     const float* __restrict__ bias, void* __restrict__ y,
                                                     int y_bf16) {
-    // LDS: A codes [128][32] bf16 (64 B rows), B codes [128][32] bf16, dx[128], dw[128]
-    __shared__ __align__(16) uint16_t sA[GM_BM * QK];
-    __shared__ __align__(16) uint16_t sB[GM_BN * QK];
-    __shared__ float sdx[GM_BM];
-    __shared__ float sdw[GM_BN];
+    __shared__ __align__(16) uint16_t sA[2][GM_BM * GM_AS];
+    __shared__ __align__(16) uint16_t sB[2][GM_BN * GM_AS];
+    __shared__ __align__(16) float sdx[2][GM_BM];
+    __shared__ __align__(16) float scr[2][GM_BM];
+    __shared__ __align__(16) float sdw[2][GM_BN];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;  // wave's 64x64 sub-tile
-    const int m0 = blockIdx.y * GM_BM, n0 = blockIdx.x * GM_BN;
     const int lrow = lane & 15, lgrp = lane >> 4;
+
+    // XCD-aware tile order: workgroup id -> (row tile, column tile)
+    const int mt = (int)gridDim.y;              // row tiles
+    const int ntot = (int)(gridDim.x * gridDim.y);
+    const int id = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    int tile = id;
+    if (ntot % NUM_XCD == 0) tile = (id % NUM_XCD) * (ntot / NUM_XCD) + id / NUM_XCD;
+    const int m0 = (tile % mt) * GM_BM, n0 = (tile / mt) * GM_BN;
 
     f32x4 acc[4][4];
 #pragma unroll
@@ -330,64 +381,82 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    for (int b = 0; b < nb; b++) {
-        // stage A: 128 rows x 64 B = 512 chunks of 16 B, two per thread
+    // per-thread staging registers
+    uint4 ra[2];
+    uint2 rb;
+    float rs0 = 0.0f, rs1 = 0.0f;
+    uint16_t rdw = 0;
+    const int bcol = tid >> 1, bhalf = tid & 1;
+    auto gload = [&](int b) {
 #pragma unroll
         for (int c = 0; c < 2; c++) {
             const int chunk = tid + c * GM_THREADS;
             const int r = chunk >> 2, part = chunk & 3;
-            const uint4 v = *reinterpret_cast<const uint4*>(xc + ((int64_t)(m0 + r) * nb + b) * QK + part * 8);
-            *reinterpret_cast<uint4*>(sA + r * QK + part * 8) = v;
+            ra[c] = *reinterpret_cast<const uint4*>(xc + ((int64_t)(m0 + r) * nb + b) * QK + part * 8);
         }
-        // stage B: threads 0..127 widen one column's block; 128..255 load scales
-        if (tid < GM_BN) {
-            const int n = n0 + tid;
-            uint4 w = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-            if (n < N) w = *reinterpret_cast<const uint4*>(qs + ((int64_t)n * nb + b) * 16);
-            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-            uint32_t out[16];
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const uint32_t v = ws[g];
-                // K slots 8g..8g+3 <- low nibbles of bytes 0..3, 8g+4..8g+7 <- high nibbles
-                out[4 * g + 0] = pack_bf16_codes(v & 0xf, (v >> 8) & 0xf);
-                out[4 * g + 1] = pack_bf16_codes((v >> 16) & 0xf, (v >> 24) & 0xf);
-                out[4 * g + 2] = pack_bf16_codes((v >> 4) & 0xf, (v >> 12) & 0xf);
-                out[4 * g + 3] = pack_bf16_codes((v >> 20) & 0xf, (v >> 28) & 0xf);
-            }
-            uint4* dst = reinterpret_cast<uint4*>(sB + tid * QK);
-#pragma unroll
-            for (int q = 0; q < 4; q++) dst[q] = make_uint4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
+        rb = make_uint2(0x88888888u, 0x88888888u);
+        if (n0 + bcol < N) rb = *reinterpret_cast<const uint2*>(qs + ((int64_t)(n0 + bcol) * nb + b) * 16 + bhalf * 8);
+        if (tid < GM_BM) {
+            rs0 = dxT[(int64_t)b * M_pad + m0 + tid];
+            rs1 = corrT[(int64_t)b * M_pad + m0 + tid];
         } else {
-            const int t = tid - GM_BN;  // 0..127
-            const int n = n0 + t;
-            sdw[t] = (n < N) ? f16_to_f32(dw[(int64_t)n * nb + b]) : 0.0f;
-            sdx[t] = dxT[(int64_t)b * M_pad + m0 + t];
+            const int n = n0 + tid - GM_BM;
+            rdw = (n < N) ? dw[(int64_t)n * nb + b] : (uint16_t)0;
         }
-        __syncthreads();
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int chunk = tid + c * GM_THREADS;
+            const int r = chunk >> 2, part = chunk & 3;
+            *reinterpret_cast<uint4*>(&sA[buf][r * GM_AS + part * 8]) = ra[c];
+        }
+        // weight dwords g = 2*bhalf, 2*bhalf+1 -> K slots 8g..8g+7 each
+        const uint32_t w0 = rb.x, w1 = rb.y;
+        const uint32_t lo0 = w0 & 0x0f0f0f0fu, hi0 = (w0 >> 4) & 0x0f0f0f0fu;
+        const uint32_t lo1 = w1 & 0x0f0f0f0fu, hi1 = (w1 >> 4) & 0x0f0f0f0fu;
+        uint4* dst = reinterpret_cast<uint4*>(&sB[buf][bcol * GM_AS + bhalf * 16]);
+        dst[0] = make_uint4(codes_pair01(lo0), codes_pair23(lo0), codes_pair01(hi0), codes_pair23(hi0));
+        dst[1] = make_uint4(codes_pair01(lo1), codes_pair23(lo1), codes_pair01(hi1), codes_pair23(hi1));
+        if (tid < GM_BM) {
+            sdx[buf][tid] = rs0;
+            scr[buf][tid] = rs1;
+        } else {
+            sdw[buf][tid - GM_BM] = f16_to_f32(rdw);
+        }
+    };
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int b = 0; b < nb; b++) {
+        const int buf = b & 1;
+        if (b + 1 < nb) gload(b + 1);
 
         bf16x8 afr[4], bfr[4];
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            afr[i] = *reinterpret_cast<const bf16x8*>(sA + (wm * 64 + i * 16 + lrow) * QK + lgrp * 8);
+            afr[i] = *reinterpret_cast<const bf16x8*>(&sA[buf][(wm * 64 + i * 16 + lrow) * GM_AS + lgrp * 8]);
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            bfr[j] = *reinterpret_cast<const bf16x8*>(sB + (wn * 64 + j * 16 + lrow) * QK + lgrp * 8);
+            bfr[j] = *reinterpret_cast<const bf16x8*>(&sB[buf][(wn * 64 + j * 16 + lrow) * GM_AS + lgrp * 8]);
         float dwv[4];
-        f32x4 dxv[4];
+        f32x4 dxv[4], crv[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) dwv[j] = sdw[wn * 64 + j * 16 + lrow];
+        for (int j = 0; j < 4; j++) dwv[j] = sdw[buf][wn * 64 + j * 16 + lrow];
 #pragma unroll
-        for (int i = 0; i < 4; i++) dxv[i] = *reinterpret_cast<const f32x4*>(sdx + wm * 64 + i * 16 + lgrp * 4);
+        for (int i = 0; i < 4; i++) {
+            dxv[i] = *reinterpret_cast<const f32x4*>(&sdx[buf][wm * 64 + i * 16 + lgrp * 4]);
+            crv[i] = *reinterpret_cast<const f32x4*>(&scr[buf][wm * 64 + i * 16 + lgrp * 4]);
+        }
 
 #pragma unroll
         for (int i = 0; i < 4; i++) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-                // C[row][col]: col = lane & 15 (weight column), row = 4*(lane>>4) + r
-                // A = activation rows, B = weight columns
-                f32x4 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[i], bfr[j], zero, 0, 0, 0);
+                // C[row][col]: col = lane & 15 (weight column), row = 4*(lane>>4) + r;
+                // A = activation rows, B = weight columns; C starts at -136*sum(x codes)
+                const f32x4 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[i], bfr[j], crv[i], 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     float t = s[r] * dwv[j];
@@ -396,6 +465,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
                 }
             }
         }
+        if (b + 1 < nb) lstore(buf ^ 1);
         __syncthreads();
     }
 
@@ -438,18 +508,26 @@ template <int MR, typename XT>
 tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, const uint16_t* dw, int N,
                       const float* bias, void* y, int y_bf16) {
     const int nb = K / QK;
+    // rows per tile: as many as GEMV_ITEMS items per thread allow, but no more
+    // than it takes to give every CU a tile of a small matrix
     int rows = (GEMV_THREADS * GEMV_ITEMS) / nb;
+    const int spread = (int)cdiv(N, 256);
+    if (rows > spread) rows = spread;
     if (rows < 1) rows = 1;
     if (rows > N) rows = N;
-    size_t lds = (size_t)MR * K + (size_t)MR * nb * 8 + (size_t)rows * MR * nb * 4;
+    // two term buffers (double-buffered across tiles)
+    auto lds_of = [&](int r) { return (size_t)MR * K + (size_t)MR * nb * 8 + 2 * (size_t)r * MR * nb * 4; };
+    size_t lds = lds_of(rows);
     while (rows > 1 && lds > 64 * 1024) {
         rows >>= 1;
-        lds = (size_t)MR * K + (size_t)MR * nb * 8 + (size_t)rows * MR * nb * 4;
+        lds = lds_of(rows);
     }
-    if (lds > 64 * 1024) return TN_ENOTIMPL;  // caller chunks rows / refuses
+    if (lds > 64 * 1024) return TN_ENOTIMPL;  // caller falls through to the GEMM path
     // (row, block) items must fit GEMV_ITEMS per thread
     if ((int64_t)rows * nb > GEMV_THREADS * GEMV_ITEMS) return TN_ENOTIMPL;
-    const unsigned grid = (unsigned)cdiv(N, rows);
+    const int64_t ntiles = cdiv(N, rows);
+    // persistent: about 8 resident workgroups per CU on 256 CUs
+    const unsigned grid = (unsigned)(ntiles < 2048 ? ntiles : 2048);
     hipLaunchKernelGGL((k_gemv<MR, XT>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N, rows,
                        bias, y, y_bf16);
     TN_LAUNCHED();
@@ -489,20 +567,21 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
     const size_t xc_bytes = (size_t)M_pad * k * 2;
     const size_t dx_bytes = (size_t)M_pad * nb * 4;
     void* ws = nullptr;
-    tn_status s = workspace(st, xc_bytes + dx_bytes, &ws);
+    tn_status s = workspace(st, xc_bytes + 2 * dx_bytes, &ws);
     if (s != TN_OK) return s;
     uint16_t* xc = static_cast<uint16_t*>(ws);
     float* dxT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes);
+    float* corrT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes + dx_bytes);
     {
         const int64_t blocks = M_pad * nb;
         const unsigned grid = (unsigned)cdiv(blocks, 8);
         hipLaunchKernelGGL((k_q8_rows<XT>), dim3(grid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
-                           dxT);
+                           dxT, corrT);
         TN_LAUNCHED();
     }
     dim3 grid((unsigned)cdiv(n, GM_BN), (unsigned)(M_pad / GM_BM));
-    hipLaunchKernelGGL(k_gemm, grid, dim3(GM_THREADS), 0, st, xc, dxT, (int)m, (int)M_pad, nb, qs, d, (int)n, bias,
-                       y, y_bf16);
+    hipLaunchKernelGGL(k_gemm, grid, dim3(GM_THREADS), 0, st, xc, dxT, corrT, (int)m, (int)M_pad, nb, qs, d, (int)n,
+                       bias, y, y_bf16);
     TN_LAUNCHED();
     return TN_OK;
 }
