@@ -20,10 +20,13 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -fhip-fp32-correctly-rounded-divide-sqrt: Q8_0's d = amax/127 and 1/d must be
 #   IEEE divisions (the default, stated explicitly).
 # -packed-fp32-ops disabled: no v_pk_*_f32 from the compiler.
+# -amdgpu-mfma-vgpr-form: MFMA accumulators in ordinary VGPRs, so the softmax
+#   and the rescales read them without v_accvgpr_read/write copies.
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -62,242 +62,410 @@ __device__ inline uint32_t pack2_bf16(float a, float b) {
     return (uint32_t)bf16_from_f32(a) | ((uint32_t)bf16_from_f32(b) << 16);
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// (i % 4) of the 8-byte rows that lanes i/4, 4 + i/4, 8 + i/4 and 12 + i/4
+// point at -- a 4-key x 16-column block read out column-wise.
+__device__ inline uint2 lds_read_tr16(const uint16_t* p) {
+#if __HIP_DEVICE_COMPILE__
+    typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p)));
+#else
+    (void)p;
+    return make_uint2(0, 0);
+#endif
+}
+
+// s_waitcnt vmcnt(n) for a compile-time n (expcnt and lgkmcnt left open)
+template <int N>
+__device__ inline void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// max / sum of a value over lanes l and l ^ 32 (v_permlane32_swap: one VALU
+// op, no LDS round trip); both lanes get the same result
+__device__ inline float xor32_max(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+__device__ inline float xor32_sum(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// Raw buffer descriptor over `bytes` bytes at `base`: offsets at or past the
+// end read as zero. Word 3 selects a 32-bit data format (any non-zero format
+// enables the access); all else is zero.
+#if __HIP_DEVICE_COMPILE__
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
+#else
+typedef struct { uint32_t w[4]; } buf_rsrc;  // the host pass never emits kernel code
+#endif
+
+__device__ inline buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+#else
+    (void)base;
+    (void)bytes;
+    return buf_rsrc{};
+#endif
+}
+
+// 16 bytes per lane from a raw buffer straight into LDS (buffer_load_dwordx4
+// ... lds): lane l's bytes land at lds_wave_base + 16*l, which must be
+// wave-uniform.
+__device__ inline void lds_direct16(buf_rsrc rsrc, uint32_t voffset, void* lds_wave_base) {
+#if __HIP_DEVICE_COMPILE__
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds_wave_base, 16,
+                                             voffset, 0, 0, 0);
+#else
+    (void)rsrc;
+    (void)voffset;
+    (void)lds_wave_base;
+#endif
+}
+
 // ---------------------------------------------------------------------------
-// bf16 prefill. Workgroup = 4 waves = 64 queries of one (batch, head); each
-// wave owns 16 queries. K/V tiles of 64 keys are staged in LDS (K as is, V
-// transposed), double-buffered: the next tile's global loads are issued into
-// registers before the current tile is computed and stored to the other LDS
-// buffer after it. Per tile and wave:
-//   S^T  : 4 key-tiles x D/32 MFMA 16x16x32 (A = K rows, B = Q^T in registers)
-//   P    : exp2(S * scale*log2e - m), narrowed to bf16
-//   O^T += D/16 d-tiles x 2 MFMA 16x16x32 (A = V^T rows, B = P^T)
-// MFMA K-slot order for a 32-key chunk u: lane group g holds keys
-// {32u + 4g + r, 32u + 16 + 4g + r : r = 0..3}, which is where S^T put them.
+// bf16 prefill on v_mfma_f32_32x32x16_bf16 (the full-rate bf16 MFMA shape).
 //
-// Long causal rows are split over `nsplit` workgroups (blockIdx.x encodes the
-// (query block, split) pair); a split writes unnormalised (m, l, O) partials
-// that k_prefill_combine merges. Rows that fit one split write the output
-// directly.
+// Workgroup = 2*KG waves over 64 queries of one (batch, head): wave w takes
+// query half qw = w & 1 (32 queries) and key group kg = w >> 1. K and V
+// stream through a two-stage LDS ring whose stages hold KG*BKW consecutive
+// keys; key group kg computes the stage's BKW-key tile kg, so the KG groups
+// split the row's keys among themselves and merge through LDS at the end (a
+// log2(KG)-round tree). Two waves per SIMD hide each other's MFMA -> softmax
+// -> MFMA latency, and a query block's keys are covered KG tiles at a time
+// without any traffic outside the CU. Stages are filled with
+// buffer_load ... lds: no registers are involved, so the next stage is in
+// flight while one is computed, and the stage's position is a scalar buffer
+// descriptor, so a stage costs no vector address arithmetic (keys past the
+// end read as zero). Rows are stored in 16-byte chunks XOR-swizzled by row so
+// that the MFMA operand reads are bank-conflict free. Per tile and wave:
+//   S^T = K . Q^T : BKW/32 key halves x D/16 MFMA (A = K rows from LDS, B =
+//                   Q^T in registers); lane l owns query l&31, 16 keys per half;
+//   P             : exp2(S * scale*log2e - m), narrowed to bf16 (v_cvt_pk_bf16_f32);
+//   O^T += V^T P^T: D/32 x BKW/16 MFMA; the V^T operand is read column-wise
+//                   from the natural-layout V tile with ds_read_b64_tr_b16.
+// K-slot order of a 16-key MFMA step j of key half s: lane half h holds keys
+// {32s + 16j + 4h + e, 32s + 16j + 8 + 4h + e : e = 0..3}, which is where the
+// 32x32 result layout (lane l holds rows 8(r/4) + 4(l>>5) + r%4) put them.
+//
+// When the grid would not fill the device, long rows are also split across
+// workgroups into items of `tiles_per` 64-key tiles; a split writes
+// unnormalised (m, l, O) partials that k_prefill_combine merges. (A merge
+// inside this kernel would take a device-scope release per workgroup, which
+// writes back the XCD's whole L2 and serialises there.)
 // ---------------------------------------------------------------------------
 
-constexpr int PF_BQ = 64, PF_BK = 64;
+constexpr int F3_BQ = 64, F3_BK = 64;  // queries per workgroup; key tile of the host-side split unit
+
+// v_max3_f32 (IEEE maxNum twice): written out because fmaxf on values the
+// compiler cannot prove quiet costs an extra canonicalising v_max per operand
+__device__ inline float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// key groups and keys per wave tile by head dim: both stage 32 KB of K and V
+// per ring stage (64 KB of LDS), so two 4-wave workgroups share a CU. (One
+// 8-wave workgroup per CU measured slower: its single barrier keeps the two
+// waves of each SIMD in the same phase, MFMA against MFMA and softmax
+// against softmax, where two workgroups drift apart and overlap.)
+template <int D>
+struct FlashCfg {
+    static constexpr int KG = 2;
+    static constexpr int BKW = D == 64 ? 64 : 32;
+};
 
 template <int D>
-__global__ __launch_bounds__(256) void k_fa_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kg,
-                                               const uint16_t* __restrict__ Vg, int Hq, int Hkv, int L, int S,
-                                               float sl2, int causal, int tiles_per, int nsplit,
-                                               uint16_t* __restrict__ Og, float* __restrict__ lse,
-                                               float* __restrict__ part_o, float2* __restrict__ part_ml) {
-    constexpr int BQ = PF_BQ, BK = PF_BK;
-    constexpr int KS = D + 8;   // K tile row stride (bf16)
-    constexpr int VS = BK + 8;  // V^T tile row stride (bf16)
-    constexpr int KCH = (BK * D / 8) / 256;   // 16-byte K chunks per thread
-    constexpr int VBL = (BK * D / 16) / 256;  // 4-key x 4-d V blocks per thread
-    __shared__ __align__(16) uint16_t sK[2][BK * KS];
-    __shared__ __align__(16) uint16_t sVt[2][D * VS];
+__global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
+    const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kg, const uint16_t* __restrict__ Vg, int Hq,
+    int Hkv, int L, int S, float sl2, int causal, int tiles_per, int nsplit, uint16_t* __restrict__ Og,
+    float* __restrict__ lse, float* __restrict__ part_o, float2* __restrict__ part_ml) {
+    constexpr int KG = FlashCfg<D>::KG;        // key groups
+    constexpr int BKW = FlashCfg<D>::BKW;      // keys per wave tile
+    constexpr int NH = BKW / 32;               // 32-key halves per wave tile
+    constexpr int NW = 2 * KG;                 // waves
+    constexpr int NT = 64 * NW;                // threads
+    constexpr int ROWS = KG * BKW;             // keys per ring stage
+    constexpr int STAGE = ROWS * D;            // elements of one K (or V) stage
+    constexpr int CPR = D / 8;                 // 16-byte chunks per row
+    constexpr int LPT = ROWS * CPR / NT;       // 16-byte loads per thread per stage, for K and for V each
+    static_assert(LPT * NT == ROWS * CPR, "stage must split evenly over the threads");
+    // one LDS object per ring stage: with the stage known at compile time the
+    // compiler can prove a read of stage s does not alias the loads still
+    // landing in the other stage, and inserts no blanket vmcnt(0)
+    __shared__ __align__(16) uint16_t sK0[STAGE], sK1[STAGE];
+    __shared__ __align__(16) uint16_t sV0[STAGE], sV1[STAGE];
+    __shared__ float2 s_ml[KG / 2][2][64];
+    auto stK = [&](auto sc) -> uint16_t* {
+        if constexpr (decltype(sc)::value == 0) return sK0; else return sK1;
+    };
+    auto stV = [&](auto sc) -> uint16_t* {
+        if constexpr (decltype(sc)::value == 0) return sV0; else return sV1;
+    };
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int lq = lane & 15, g = lane >> 4;
-    // work decode: heaviest query blocks first, then their splits
-    const int nqb = (L + BQ - 1) / BQ;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, kept in a scalar register
+    const int qw = w & 1, kg = w >> 1;                       // query half, key group
+    const int lq = lane & 31, hh = lane >> 5;
+    const int nqb = (L + F3_BQ - 1) / F3_BQ;
     const int item = (int)blockIdx.x;
-    const int qt = nqb - 1 - item / nsplit;
+    const int qt = nqb - 1 - item / nsplit;  // heaviest query blocks first
     const int split = item % nsplit;
     const int h = blockIdx.y, b = blockIdx.z;
     const int kvh = h / (Hq / Hkv);
-    const int q0 = qt * BQ;
-    const int qi = q0 + w * 16 + lq;
-    const int kend = causal ? min(S, q0 + BQ) : S;
-    const int ntiles_row = (kend + BK - 1) / BK;
+    const int q0 = qt * F3_BQ;
+    const int qw0 = q0 + qw * 32;            // first query of this wave
+    const int qi = qw0 + lq;
+    const int kend = causal ? min(S, q0 + F3_BQ) : S;
+    const int ntiles_row = (kend + F3_BK - 1) / F3_BK;
     const int nsplit_row = (ntiles_row + tiles_per - 1) / tiles_per;
     if (split >= nsplit_row) return;  // uniform over the workgroup
-    const int t_begin = split * tiles_per;
-    const int t_end = min(ntiles_row, t_begin + tiles_per);
+    const int k_lo = split * tiles_per * F3_BK;                       // this item's keys: [k_lo, k_hi)
+    const int k_hi = min(kend, (split + 1) * tiles_per * F3_BK);
+    const int nst = (k_hi - k_lo + ROWS - 1) / ROWS;                  // ring stages of this item
 
     const uint16_t* qp = Qg + ((int64_t)b * Hq + h) * L * D;
     const uint16_t* kp = Kg + ((int64_t)b * Hkv + kvh) * S * D;
     const uint16_t* vp = Vg + ((int64_t)b * Hkv + kvh) * S * D;
 
-    bf16x8 qf[D / 32];
+    // physical 16-byte chunk of logical chunk c in row r (an involution; it
+    // depends on r mod 16 only, so a tile's rows and the stage's rows agree)
+    auto swz = [](int r, int c) { return D == 64 ? (c ^ ((r >> 1) & 7)) : (c ^ (r & 15)); };
+
+    bf16x8 qf[D / 16];
 #pragma unroll
-    for (int c = 0; c < D / 32; c++) {
+    for (int c = 0; c < D / 16; c++) {
         uint4 v = make_uint4(0, 0, 0, 0);
-        if (qi < L) v = *reinterpret_cast<const uint4*>(qp + (int64_t)qi * D + 32 * c + 8 * g);
+        if (qi < L) v = *reinterpret_cast<const uint4*>(qp + (int64_t)qi * D + 16 * c + 8 * hh);
         qf[c] = __builtin_bit_cast(bf16x8, v);
     }
-    // o[0 .. D/16-1]: O^T tiles; o[D/16]: the row sums, accumulated by one more
-    // MFMA against a tile of ones so that the normaliser sums exactly the
-    // bf16 probabilities the numerator used (every element of it holds l)
-    f32x4 o[D / 16 + 1];
-#pragma unroll
-    for (int i = 0; i <= D / 16; i++) o[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    float m = -INFINITY;
-    const bf16x8 ones = __builtin_bit_cast(bf16x8, make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
 
-    uint4 kr[KCH];
-    uint2 vr[VBL][4];
-    // the (key, column) each thread moves is fixed; only the tile base moves
-    auto gload = [&](int k0) {
-        const uint16_t* kb = kp + (int64_t)k0 * D;
-        const uint16_t* vb = vp + (int64_t)k0 * D;
-        if (k0 + BK <= S) {
+    // this lane's byte offset in a stage for its i-th 16-byte load: LDS
+    // position p = tid + NT*i (wave w's i-th load covers positions
+    // (w + NW*i)*64 .. +63) holds logical chunk swz(row, p % CPR) of row p / CPR
+    uint32_t voff[LPT];
 #pragma unroll
-            for (int it = 0; it < KCH; it++) {
-                const int c = tid + it * 256;
-                kr[it] = *reinterpret_cast<const uint4*>(kb + (c / (D / 8)) * D + (c % (D / 8)) * 8);
-            }
+    for (int i = 0; i < LPT; i++) {
+        const int p = tid + NT * i;
+        const int row = p / CPR;
+        voff[i] = (uint32_t)(row * D + swz(row, p % CPR) * 8) * 2u;
+    }
+    auto issue = [&](auto sc, int st) {
+        const int k0 = k_lo + st * ROWS;
+        const uint32_t bytes = (uint32_t)(S - k0) * (uint32_t)(D * 2);  // keys k0 .. S-1
+        const buf_rsrc rk = make_rsrc(kp + (int64_t)k0 * D, bytes);
+        const buf_rsrc rv = make_rsrc(vp + (int64_t)k0 * D, bytes);
+        uint16_t* dK = stK(sc);
+        uint16_t* dV = stV(sc);
 #pragma unroll
-            for (int it = 0; it < VBL; it++) {
-                const int idx = tid + it * 256;
-                const uint16_t* src = vb + (4 * (idx / (D / 4))) * D + 4 * (idx % (D / 4));
-#pragma unroll
-                for (int i = 0; i < 4; i++) vr[it][i] = *reinterpret_cast<const uint2*>(src + i * D);
-            }
-        } else {
-#pragma unroll
-            for (int it = 0; it < KCH; it++) {
-                const int c = tid + it * 256;
-                const int r = c / (D / 8), part = c % (D / 8);
-                kr[it] = make_uint4(0, 0, 0, 0);
-                if (k0 + r < S) kr[it] = *reinterpret_cast<const uint4*>(kb + r * D + part * 8);
-            }
-#pragma unroll
-            for (int it = 0; it < VBL; it++) {
-                const int idx = tid + it * 256;
-                const int dg = idx % (D / 4), kg = idx / (D / 4);
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    vr[it][i] = make_uint2(0, 0);
-                    if (k0 + 4 * kg + i < S) vr[it][i] = *reinterpret_cast<const uint2*>(vb + (4 * kg + i) * D + 4 * dg);
-                }
-            }
-        }
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int it = 0; it < KCH; it++) {
-            const int c = tid + it * 256;
-            const int r = c / (D / 8), part = c % (D / 8);
-            *reinterpret_cast<uint4*>(&sK[buf][r * KS + part * 8]) = kr[it];
-        }
-#pragma unroll
-        for (int it = 0; it < VBL; it++) {
-            const int idx = tid + it * 256;
-            const int dg = idx % (D / 4), kg = idx / (D / 4);
-            // 4 keys x 4 d -> 4 d-rows x 4 keys (v_perm picks 16-bit halves)
-            const uint2* rw = vr[it];
-            const uint32_t c0 = __builtin_amdgcn_perm(rw[1].x, rw[0].x, 0x05040100u);
-            const uint32_t c1 = __builtin_amdgcn_perm(rw[3].x, rw[2].x, 0x05040100u);
-            const uint32_t c2 = __builtin_amdgcn_perm(rw[1].x, rw[0].x, 0x07060302u);
-            const uint32_t c3 = __builtin_amdgcn_perm(rw[3].x, rw[2].x, 0x07060302u);
-            const uint32_t c4 = __builtin_amdgcn_perm(rw[1].y, rw[0].y, 0x05040100u);
-            const uint32_t c5 = __builtin_amdgcn_perm(rw[3].y, rw[2].y, 0x05040100u);
-            const uint32_t c6 = __builtin_amdgcn_perm(rw[1].y, rw[0].y, 0x07060302u);
-            const uint32_t c7 = __builtin_amdgcn_perm(rw[3].y, rw[2].y, 0x07060302u);
-            uint16_t* base = &sVt[buf][(4 * dg) * VS + 4 * kg];
-            *reinterpret_cast<uint2*>(base) = make_uint2(c0, c1);
-            *reinterpret_cast<uint2*>(base + VS) = make_uint2(c2, c3);
-            *reinterpret_cast<uint2*>(base + 2 * VS) = make_uint2(c4, c5);
-            *reinterpret_cast<uint2*>(base + 3 * VS) = make_uint2(c6, c7);
+        for (int i = 0; i < LPT; i++) {
+            lds_direct16(rk, voff[i], dK + (w + NW * i) * 64 * 8);
+            lds_direct16(rv, voff[i], dV + (w + NW * i) * 64 * 8);
         }
     };
 
-    gload(t_begin * BK);
-    lstore(0);
-    __syncthreads();
-    for (int t = t_begin; t < t_end; t++) {
-        const int buf = (t - t_begin) & 1;
-        const int k0 = t * BK;
-        if (t + 1 < t_end) gload(k0 + BK);
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[i][r] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
 
-        // S^T for 64 keys x this wave's 16 queries
-        f32x4 s[4];
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    issue(I0{}, 0);  // nst >= 1: every item has at least one key
+
+    // ring stage sc holds stage st: wait for it, open the other stage (read in
+    // the previous step) to the next stage's loads, compute this wave's tile
+    auto step = [&](auto sc, int st) {
+        wait_vmcnt<0>();  // the only loads in flight are this stage's
+        // a bare barrier (no fence: a fence would also wait for the scalar
+        // loads); the empty asm statements keep the compiler from moving LDS
+        // accesses across it
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (st + 1 < nst) issue(std::integral_constant<int, 1 - decltype(sc)::value>{}, st + 1);
+
+        const int k0 = k_lo + st * ROWS + kg * BKW;
+        // past the item's keys, or every query of the wave precedes the tile
+        if (k0 >= k_hi || (causal && qw0 + 31 < k0)) return;
+        // this wave's tile is rows BKW*kg .. BKW*kg + BKW-1 of the stage; the
+        // key group enters through the row index (not the pointer), which
+        // keeps the reads attributable to their stage's LDS object, so the
+        // compiler does not make them wait for the other stage's loads
+        const uint16_t* tK = stK(sc);
+        const uint16_t* tV = stV(sc);
+        const int kr = BKW * kg;
+
+        float sv[NH][16];
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-            s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int s2 = 0; s2 < NH; s2++) {
+            f32x16 acc;
 #pragma unroll
-            for (int c = 0; c < D / 32; c++) {
-                const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&sK[buf][(16 * kt + lq) * KS + 32 * c + 8 * g]);
-                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[c], s[kt], 0, 0, 0);
+            for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+            const int row = kr + 32 * s2 + lq;
+#pragma unroll
+            for (int c = 0; c < D / 16; c++) {
+                const bf16x8 ka = *reinterpret_cast<const bf16x8*>(tK + row * D + swz(row, 2 * c + hh) * 8);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[c], acc, 0, 0, 0);
             }
+#pragma unroll
+            for (int r = 0; r < 16; r++) sv[s2][r] = acc[r];
         }
-        if (k0 + BK > S || (causal && k0 + BK - 1 > q0 + w * 16)) {
+        if (k0 + BKW > S || (causal && k0 + BKW - 1 > qw0)) {
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++)
+            for (int s2 = 0; s2 < NH; s2++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int key = k0 + 16 * kt + 4 * g + r;
-                    if (key >= S || (causal && key > qi)) s[kt][r] = -INFINITY;
+                for (int r = 0; r < 16; r++) {
+                    const int key = k0 + 32 * s2 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    if (key >= S || (causal && key > qi)) sv[s2][r] = -INFINITY;
                 }
         }
-        float mx = -INFINITY;
+        // row maximum: independent max3 chains over 8 scores each
+        float mq[2 * NH];
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++)
-            mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
-        mx = wave_xor_max(mx) * sl2;
+        for (int g = 0; g < 2 * NH; g++) {
+            const float* v = &sv[g >> 1][8 * (g & 1)];
+            float a = max3f(v[0], v[1], v[2]);
+            a = max3f(a, v[3], v[4]);
+            a = max3f(a, v[5], v[6]);
+            mq[g] = max3f(a, v[7], v[7]);
+        }
+        float mx = NH == 2 ? max3f(max3f(mq[0], mq[1], mq[2]), mq[2 * NH - 1], mq[2 * NH - 1])
+                           : max3f(mq[0], mq[2 * NH - 1], mq[2 * NH - 1]);
+        mx = xor32_max(mx) * sl2;
         const bool need = mx > m + RESCALE_SLACK;
         if (__any(need)) {
             const float mn = need ? mx : m;
             const float alpha = __builtin_amdgcn_exp2f(m - mn);
+            l = l * alpha;
 #pragma unroll
-            for (int i = 0; i <= D / 16; i++) o[i] = o[i] * alpha;
+            for (int i = 0; i < D / 32; i++) o[i] = o[i] * alpha;
             m = mn;
         }
         const float mu = (m == -INFINITY) ? 0.0f : m;
-        bf16x8 pf[2];
+        bf16x8 pf[NH][2];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            float p[8];
+        for (int s2 = 0; s2 < NH; s2++) {
+            float p[16];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * u][r], sl2, -mu));
-                p[4 + r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * u + 1][r], sl2, -mu));
-            }
-            uint4 pk;
-            pk.x = pack2_bf16_hw(p[0], p[1]);
-            pk.y = pack2_bf16_hw(p[2], p[3]);
-            pk.z = pack2_bf16_hw(p[4], p[5]);
-            pk.w = pack2_bf16_hw(p[6], p[7]);
-            pf[u] = __builtin_bit_cast(bf16x8, pk);
+            for (int r = 0; r < 16; r++) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[s2][r], sl2, -mu));
+            float ps = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r += 4) ps = ps + ((p[r] + p[r + 1]) + (p[r + 2] + p[r + 3]));
+            l = l + ps;
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                pf[s2][j] = __builtin_bit_cast(
+                    bf16x8, make_uint4(pack2_bf16_hw(p[8 * j], p[8 * j + 1]), pack2_bf16_hw(p[8 * j + 2], p[8 * j + 3]),
+                                       pack2_bf16_hw(p[8 * j + 4], p[8 * j + 5]),
+                                       pack2_bf16_hw(p[8 * j + 6], p[8 * j + 7])));
         }
+        // V^T operand rows for this lane's 16-lane group: d = 32dt + 16*((lane>>4)&1) + (lane&15)
+        const int gi = lane & 15;
+        const int dcol = 16 * ((lane >> 4) & 1) + 4 * (gi & 3);  // source lane's 4 columns
 #pragma unroll
-        for (int dt = 0; dt < D / 16; dt++) {
+        for (int dt = 0; dt < D / 32; dt++) {
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const uint16_t* row = &sVt[buf][(16 * dt + lq) * VS + 32 * u + 4 * g];
-                const uint2 lo = *reinterpret_cast<const uint2*>(row);
-                const uint2 hi = *reinterpret_cast<const uint2*>(row + 16);
-                const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[u], o[dt], 0, 0, 0);
+            for (int s2 = 0; s2 < NH; s2++) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int r0 = kr + 32 * s2 + 16 * j + 4 * hh + (gi >> 2);
+                    const int r1 = r0 + 8;
+                    const int col = 32 * dt + dcol;
+                    const uint2 lo = lds_read_tr16(tV + r0 * D + swz(r0, col >> 3) * 8 + (col & 7));
+                    const uint2 hi = lds_read_tr16(tV + r1 * D + swz(r1, col >> 3) * 8 + (col & 7));
+                    const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[s2][j], o[dt], 0, 0, 0);
+                }
             }
         }
-#pragma unroll
-        for (int u = 0; u < 2; u++) o[D / 16] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[u], o[D / 16], 0, 0, 0);
-        if (t + 1 < t_end) lstore(buf ^ 1);
-        __syncthreads();
+    };
+    // the ring unrolled so that every stage index is a constant
+    for (int st = 0; st < nst; st += 2) {
+        step(I0{}, st);
+        if (st + 1 < nst) step(I1{}, st + 1);
     }
 
-    const float l = o[D / 16][0];
-    if (qi >= L) return;
+    l = xor32_sum(l);
+    // Tree merge of the key groups through LDS: in the round of width `half`,
+    // group kg + half hands its (m, l, O) to group kg. Lane l of wave (qw, g)
+    // holds the same (query, d) entries for every g. The O buffers of a round
+    // take 2*half wave slots of D*128 bytes, laid over the ring arrays (every
+    // load has landed and been read once the first barrier has passed).
+    constexpr int WSLOT = D / 32 * 16 * 64;        // floats per wave slot
+    constexpr int PER_ARR = STAGE / 2 / WSLOT;     // wave slots per ring array
+    static_assert(PER_ARR >= 1 && KG <= 4 * PER_ARR, "merge slots must fit in the ring");
+#pragma unroll
+    for (int half = KG / 2; half >= 1; half /= 2) {
+        __syncthreads();
+        if (kg >= half && kg < 2 * half) {
+            const int x = (kg - half) * 2 + qw;  // wave slot
+            float* arr = reinterpret_cast<float*>(x / PER_ARR == 0 ? sK0 : x / PER_ARR == 1 ? sK1
+                                                  : x / PER_ARR == 2 ? sV0 : sV1);
+            float* xo = arr + (x % PER_ARR) * WSLOT;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) xo[(dt * 16 + r) * 64 + lane] = o[dt][r];
+            s_ml[kg - half][qw][lane] = make_float2(m, l);
+        }
+        __syncthreads();
+        if (kg < half) {
+            const int x = kg * 2 + qw;
+            const float* arr = reinterpret_cast<const float*>(x / PER_ARR == 0 ? sK0 : x / PER_ARR == 1 ? sK1
+                                                              : x / PER_ARR == 2 ? sV0 : sV1);
+            const float* xo = arr + (x % PER_ARR) * WSLOT;
+            const float2 ml1 = s_ml[kg][qw][lane];
+            const float mm = fmaxf(m, ml1.x);
+            const float mu = (mm == -INFINITY) ? 0.0f : mm;
+            const float a0 = __builtin_amdgcn_exp2f(m - mu);
+            const float a1 = __builtin_amdgcn_exp2f(ml1.x - mu);
+            l = l * a0 + ml1.y * a1;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[dt][r] = o[dt][r] * a0 + xo[(dt * 16 + r) * 64 + lane] * a1;
+            m = mm;
+        }
+    }
+    if (kg != 0 || qi >= L) return;
     const int64_t row = ((int64_t)b * Hq + h) * L + qi;
     if (nsplit_row == 1) {
         const float inv = 1.0f / l;
         uint16_t* op = Og + row * D;
 #pragma unroll
-        for (int dt = 0; dt < D / 16; dt++) {
-            // O^T[d = 16dt + 4g + r][q = lq]
-            *reinterpret_cast<uint2*>(op + 16 * dt + 4 * g) =
-                make_uint2(pack2_bf16(o[dt][0] * inv, o[dt][1] * inv), pack2_bf16(o[dt][2] * inv, o[dt][3] * inv));
-        }
-        if (lse && g == 0) lse[row] = m * LN2 + logf(l);
-    } else {
-        float* po = part_o + (row * nsplit + split) * D;
+        for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
-        for (int dt = 0; dt < D / 16; dt++)
-            *reinterpret_cast<float4*>(po + 16 * dt + 4 * g) = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
-        if (g == 0) part_ml[row * nsplit + split] = make_float2(m, l);
+            for (int g4 = 0; g4 < 4; g4++)
+                // O^T[d = 32dt + 8g4 + 4hh + e][q = lq]
+                *reinterpret_cast<uint2*>(op + 32 * dt + 8 * g4 + 4 * hh) =
+                    make_uint2(pack2_bf16(o[dt][4 * g4] * inv, o[dt][4 * g4 + 1] * inv),
+                               pack2_bf16(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv));
+        if (lse && hh == 0) lse[row] = m * LN2 + logf(l);
+        return;
     }
+    float* po = part_o + (row * nsplit + split) * D;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++)
+            *reinterpret_cast<float4*>(po + 32 * dt + 8 * g4 + 4 * hh) =
+                make_float4(o[dt][4 * g4], o[dt][4 * g4 + 1], o[dt][4 * g4 + 2], o[dt][4 * g4 + 3]);
+    if (hh == 0) part_ml[row * nsplit + split] = make_float2(m, l);
 }
+
+constexpr int PF_BQ = 64, PF_BK = 64;
+
 
 // ---------------------------------------------------------------------------
 // f32 prefill: the same decomposition on v_mfma_f32_16x16x4_f32 (K = 4 per op).
@@ -453,14 +621,14 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
 template <int D, typename OT>
 __global__ __launch_bounds__(256) void k_prefill_combine(const float* __restrict__ part_o,
                                                        const float2* __restrict__ part_ml, int L, int S, int causal,
-                                                       int bk, int tiles_per, int nsplit, int64_t rows,
+                                                       int bq, int bk, int tiles_per, int nsplit, int64_t rows,
                                                        OT* __restrict__ out, float* __restrict__ lse) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const int qi = (int)(row % L);
-    const int q0 = qi / PF_BQ * PF_BQ;
-    const int kend = causal ? min(S, q0 + PF_BQ) : S;
+    const int q0 = qi / bq * bq;
+    const int kend = causal ? min(S, q0 + bq) : S;
     const int ntiles_row = (kend + bk - 1) / bk;
     const int ns = (ntiles_row + tiles_per - 1) / tiles_per;
     if (ns <= 1) return;  // written directly by the prefill kernel
@@ -697,6 +865,21 @@ int prefill_tiles_per_split(int64_t B, int64_t Hq, int64_t L, int64_t S, int cau
     return (int)std::max<int64_t>(8, (ntiles + 3) / 4);
 }
 
+// 64-key tiles per work item of the bf16 prefill. Rows stay whole once the
+// query blocks alone give every CU (256) a workgroup; below that, rows are
+// split into items of at least 16 tiles (a split costs a workgroup's fixed
+// start-up, about 2 us, and the partials it writes) so that the items about
+// fill the device once.
+int flash_tiles_per_split(int64_t B, int64_t Hq, int64_t L, int64_t S, int causal) {
+    const int64_t nqb = cdiv(L, F3_BQ);
+    const int64_t row_tiles = cdiv(causal ? std::min<int64_t>(S, nqb * F3_BQ) : S, F3_BK);
+    if (B * Hq * nqb >= 256) return (int)std::min<int64_t>(row_tiles, INT32_MAX);
+    int64_t total = 0;  // tiles over all query blocks of one head
+    for (int64_t qb = 0; qb < nqb; qb++) total += cdiv(causal ? std::min<int64_t>(S, (qb + 1) * F3_BQ) : S, F3_BK);
+    total *= B * Hq;
+    return (int)std::min<int64_t>(std::max<int64_t>(16, cdiv(total, 256)), INT32_MAX);
+}
+
 }  // namespace
 }  // namespace tn
 
@@ -746,14 +929,57 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     const float sl2 = (float)sc * LOG2E;
     hipStream_t st = (hipStream_t)stream;
     const int c = is_causal ? 1 : 0;
-    const int bk = (dtype == TN_F32 && D == 128) ? 32 : PF_BK;
+    const int64_t rows = B * Hq * L;
+    if (dtype == TN_BF16) {
+        // the key/value buffer descriptors cover one head's S*D elements
+        if (S * D * 2 > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": key length too large");
+        const int64_t nqb = cdiv(L, F3_BQ);
+        const int tiles_per = flash_tiles_per_split(B, Hq, L, S, c);
+        const int64_t kend_max = is_causal ? std::min<int64_t>(S, nqb * F3_BQ) : S;
+        const int nsplit = (int)cdiv(cdiv(kend_max, F3_BK), tiles_per);
+        float* part_o = nullptr;
+        float2* part_ml = nullptr;
+        if (nsplit > 1) {
+            const size_t po = (size_t)rows * nsplit * D * sizeof(float);
+            const size_t pm = (size_t)rows * nsplit * sizeof(float2);
+            void* ws = nullptr;
+            tn_status s = workspace(st, po + pm, &ws);
+            if (s != TN_OK) return s;
+            part_o = static_cast<float*>(ws);
+            part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + po);
+        }
+        if (nqb * nsplit > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": shape too large");
+        dim3 grid((unsigned)(nqb * nsplit), (unsigned)Hq, (unsigned)B);
+        auto qq = static_cast<const uint16_t*>(q);
+        auto kk = static_cast<const uint16_t*>(k);
+        auto vv = static_cast<const uint16_t*>(v);
+        auto oo = static_cast<uint16_t*>(out);
+        if (D == 64)
+            hipLaunchKernelGGL(k_flash_bf16<64>, grid, dim3(128 * FlashCfg<64>::KG), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
+                               (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml);
+        else
+            hipLaunchKernelGGL(k_flash_bf16<128>, grid, dim3(128 * FlashCfg<128>::KG), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
+                               (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml);
+        TN_LAUNCHED();
+        if (nsplit > 1) {
+            const unsigned g2 = (unsigned)cdiv(rows, 4);
+            if (D == 64)
+                hipLaunchKernelGGL((k_prefill_combine<64, uint16_t>), dim3(g2), dim3(256), 0, st, part_o, part_ml,
+                                   (int)L, (int)S, c, F3_BQ, F3_BK, tiles_per, nsplit, rows, oo, lse);
+            else
+                hipLaunchKernelGGL((k_prefill_combine<128, uint16_t>), dim3(g2), dim3(256), 0, st, part_o,
+                                   part_ml, (int)L, (int)S, c, F3_BQ, F3_BK, tiles_per, nsplit, rows, oo, lse);
+            TN_LAUNCHED();
+        }
+        return TN_OK;
+    }
+    const int bk = (D == 128) ? 32 : PF_BK;
     const int64_t nqb = cdiv(L, PF_BQ);
     const int64_t kend_max = is_causal ? std::min<int64_t>(S, nqb * PF_BQ) : S;
     const int tiles_per = prefill_tiles_per_split(B, Hq, L, S, c, bk);
     const int nsplit = (int)cdiv(cdiv(kend_max, bk), tiles_per);
     float* part_o = nullptr;
     float2* part_ml = nullptr;
-    const int64_t rows = B * Hq * L;
     if (nsplit > 1) {
         const size_t po = (size_t)rows * nsplit * D * sizeof(float);
         const size_t pm = (size_t)rows * nsplit * sizeof(float2);
@@ -765,29 +991,7 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     }
     if (nqb * nsplit > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": shape too large");
     dim3 grid((unsigned)(nqb * nsplit), (unsigned)Hq, (unsigned)B);
-    if (dtype == TN_BF16) {
-        auto qq = static_cast<const uint16_t*>(q);
-        auto kk = static_cast<const uint16_t*>(k);
-        auto vv = static_cast<const uint16_t*>(v);
-        auto oo = static_cast<uint16_t*>(out);
-        if (D == 64)
-            hipLaunchKernelGGL(k_fa_bf16<64>, grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L, (int)S,
-                               sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml);
-        else
-            hipLaunchKernelGGL(k_fa_bf16<128>, grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
-                               (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml);
-        TN_LAUNCHED();
-        if (nsplit > 1) {
-            const unsigned g2 = (unsigned)cdiv(rows, 4);
-            if (D == 64)
-                hipLaunchKernelGGL((k_prefill_combine<64, uint16_t>), dim3(g2), dim3(256), 0, st, part_o, part_ml,
-                                   (int)L, (int)S, c, bk, tiles_per, nsplit, rows, oo, lse);
-            else
-                hipLaunchKernelGGL((k_prefill_combine<128, uint16_t>), dim3(g2), dim3(256), 0, st, part_o, part_ml,
-                                   (int)L, (int)S, c, bk, tiles_per, nsplit, rows, oo, lse);
-            TN_LAUNCHED();
-        }
-    } else {
+    {
         auto qq = static_cast<const float*>(q);
         auto kk = static_cast<const float*>(k);
         auto vv = static_cast<const float*>(v);
@@ -803,10 +1007,10 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
             const unsigned g2 = (unsigned)cdiv(rows, 4);
             if (D == 64)
                 hipLaunchKernelGGL((k_prefill_combine<64, float>), dim3(g2), dim3(256), 0, st, part_o, part_ml,
-                                   (int)L, (int)S, c, bk, tiles_per, nsplit, rows, oo, lse);
+                                   (int)L, (int)S, c, PF_BQ, bk, tiles_per, nsplit, rows, oo, lse);
             else
                 hipLaunchKernelGGL((k_prefill_combine<128, float>), dim3(g2), dim3(256), 0, st, part_o, part_ml,
-                                   (int)L, (int)S, c, bk, tiles_per, nsplit, rows, oo, lse);
+                                   (int)L, (int)S, c, PF_BQ, bk, tiles_per, nsplit, rows, oo, lse);
             TN_LAUNCHED();
         }
     }
