@@ -24,6 +24,8 @@
 // is the same softmax; only the common factor differs until the end.
 #include <algorithm>
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 #include "tn_common.h"
 
@@ -155,11 +157,11 @@ __device__ inline void lds_direct16(buf_rsrc rsrc, uint32_t voffset, void* lds_w
 // {32s + 16j + 4h + e, 32s + 16j + 8 + 4h + e : e = 0..3}, which is where the
 // 32x32 result layout (lane l holds rows 8(r/4) + 4(l>>5) + r%4) put them.
 //
-// When the grid would not fill the device, long rows are also split across
-// workgroups into items of `tiles_per` 64-key tiles; a split writes
-// unnormalised (m, l, O) partials that k_prefill_combine merges. (A merge
-// inside this kernel would take a device-scope release per workgroup, which
-// writes back the XCD's whole L2 and serialises there.)
+// Long rows are also split across workgroups (the work list, FlashWork,
+// balances the items); a split writes unnormalised (m, l, O) partials that
+// k_prefill_combine merges. (A merge inside this kernel would take a
+// device-scope release per workgroup, which writes back the XCD's whole L2
+// and serialises there.)
 // ---------------------------------------------------------------------------
 
 constexpr int F3_BQ = 64, F3_BK = 64;  // queries per workgroup; key tile of the host-side split unit
@@ -183,10 +185,29 @@ struct FlashCfg {
     static constexpr int BKW = D == 64 ? 64 : 32;
 };
 
+// A row of n key tiles is cut into row_splits(n, target) items; item s covers
+// tiles [s*n/ns, (s+1)*n/ns), so the items differ in size by at most one tile
+// and none is empty.
+__host__ __device__ inline int row_splits(int n, int target) { return n <= target ? 1 : (n + target - 1) / target; }
+
+// The prefill's work list, passed by value: item classes (query block qt,
+// split s) sorted by decreasing size, each class repeated for every (batch,
+// head). Workgroup i takes class i / bh, (batch, head) i % bh; consecutive
+// workgroups go to the eight XCDs in turn, so every XCD receives the same mix
+// of long and short items and the longest start first. ncls = 0: no row is
+// split and class c is query block nqb-1-c.
+constexpr int FLASH_MAX_CLS = 768;
+struct FlashWork {
+    int target;   // tiles per item
+    int bh;       // B * Hq
+    int ncls;
+    uint32_t cls[FLASH_MAX_CLS];  // qt | split << 16
+};
+
 template <int D>
 __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
     const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kg, const uint16_t* __restrict__ Vg, int Hq,
-    int Hkv, int L, int S, float sl2, int causal, int tiles_per, int nsplit, uint16_t* __restrict__ Og,
+    int Hkv, int L, int S, float sl2, int causal, const FlashWork work, int nsplit, uint16_t* __restrict__ Og,
     float* __restrict__ lse, float* __restrict__ part_o, float2* __restrict__ part_ml) {
     constexpr int KG = FlashCfg<D>::KG;        // key groups
     constexpr int BKW = FlashCfg<D>::BKW;      // keys per wave tile
@@ -216,20 +237,20 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
     const int qw = w & 1, kg = w >> 1;                       // query half, key group
     const int lq = lane & 31, hh = lane >> 5;
     const int nqb = (L + F3_BQ - 1) / F3_BQ;
-    const int item = (int)blockIdx.x;
-    const int qt = nqb - 1 - item / nsplit;  // heaviest query blocks first
-    const int split = item % nsplit;
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int cidx = (int)blockIdx.x / work.bh;
+    const int bh = (int)blockIdx.x % work.bh;
+    const uint32_t cl = work.ncls ? work.cls[cidx] : (uint32_t)(nqb - 1 - cidx);
+    const int qt = (int)(cl & 0xffffu), split = (int)(cl >> 16);
+    const int h = bh % Hq, b = bh / Hq;
     const int kvh = h / (Hq / Hkv);
     const int q0 = qt * F3_BQ;
     const int qw0 = q0 + qw * 32;            // first query of this wave
     const int qi = qw0 + lq;
     const int kend = causal ? min(S, q0 + F3_BQ) : S;
     const int ntiles_row = (kend + F3_BK - 1) / F3_BK;
-    const int nsplit_row = (ntiles_row + tiles_per - 1) / tiles_per;
-    if (split >= nsplit_row) return;  // uniform over the workgroup
-    const int k_lo = split * tiles_per * F3_BK;                       // this item's keys: [k_lo, k_hi)
-    const int k_hi = min(kend, (split + 1) * tiles_per * F3_BK);
+    const int nsplit_row = row_splits(ntiles_row, work.target);
+    const int k_lo = split * ntiles_row / nsplit_row * F3_BK;         // this item's keys: [k_lo, k_hi)
+    const int k_hi = min(kend, (split + 1) * ntiles_row / nsplit_row * F3_BK);
     const int nst = (k_hi - k_lo + ROWS - 1) / ROWS;                  // ring stages of this item
 
     const uint16_t* qp = Qg + ((int64_t)b * Hq + h) * L * D;
@@ -500,10 +521,10 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
     const int qi = q0 + w * 16 + lq;
     const int kend = causal ? min(S, q0 + BQ) : S;
     const int ntiles_row = (kend + BK - 1) / BK;
-    const int nsplit_row = (ntiles_row + tiles_per - 1) / tiles_per;
+    const int nsplit_row = row_splits(ntiles_row, tiles_per);
     if (split >= nsplit_row) return;
-    const int t_begin = split * tiles_per;
-    const int t_end = min(ntiles_row, t_begin + tiles_per);
+    const int t_begin = split * ntiles_row / nsplit_row;
+    const int t_end = (split + 1) * ntiles_row / nsplit_row;
 
     const float* qp = Qg + ((int64_t)b * Hq + h) * L * D;
     const float* kp = Kg + ((int64_t)b * Hkv + kvh) * S * D;
@@ -616,47 +637,66 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
     }
 }
 
-// Merge the split partials of the rows whose KV range was split: one wave
-// per (row, head); lane covers D/64 output elements.
+// Merge the partials of the rows whose key range was split. 1-D grid over
+// (row block, batch*head) for query rows row_lo .. L-1 (a causal row's tile
+// count grows with its query block, so the split rows are the last ones);
+// D/4 threads per row, each merging four output columns of every split with
+// float4 loads.
 template <int D, typename OT>
 __global__ __launch_bounds__(256) void k_prefill_combine(const float* __restrict__ part_o,
                                                        const float2* __restrict__ part_ml, int L, int S, int causal,
-                                                       int bq, int bk, int tiles_per, int nsplit, int64_t rows,
-                                                       OT* __restrict__ out, float* __restrict__ lse) {
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const int qi = (int)(row % L);
+                                                       int bq, int bk, int target, int nsplit, int row_lo,
+                                                       int nrb, OT* __restrict__ out, float* __restrict__ lse) {
+    constexpr int TPR = D / 4;      // threads per row
+    constexpr int RPB = 256 / TPR;  // rows per workgroup
+    const int rb = (int)(blockIdx.x % (unsigned)nrb);
+    const int64_t bh = blockIdx.x / (unsigned)nrb;
+    const int qi = row_lo + rb * RPB + (int)threadIdx.x / TPR;
+    const int c4 = ((int)threadIdx.x % TPR) * 4;
+    if (qi >= L) return;
     const int q0 = qi / bq * bq;
     const int kend = causal ? min(S, q0 + bq) : S;
-    const int ntiles_row = (kend + bk - 1) / bk;
-    const int ns = (ntiles_row + tiles_per - 1) / tiles_per;
+    const int ns = row_splits((kend + bk - 1) / bk, target);
     if (ns <= 1) return;  // written directly by the prefill kernel
+    const int64_t row = bh * L + qi;
     const float2* ml = part_ml + row * nsplit;
+    const float* pr = part_o + row * nsplit * D + c4;
+    // the first CMAX splits' partials are all requested before any is used
+    // (one memory round trip); rows with more splits loop for the rest
+    constexpr int CMAX = 4;
+    float2 mlv[CMAX];
+    float4 pv[CMAX];
+#pragma unroll
+    for (int s = 0; s < CMAX; s++) {
+        mlv[s] = s < ns ? ml[s] : make_float2(-INFINITY, 0.0f);
+        pv[s] = s < ns ? *reinterpret_cast<const float4*>(pr + s * D) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     float mm = -INFINITY;
-    for (int s = 0; s < ns; s++) mm = fmaxf(mm, ml[s].x);
+#pragma unroll
+    for (int s = 0; s < CMAX; s++) mm = fmaxf(mm, mlv[s].x);  // absent splits hold -inf
+    for (int s = CMAX; s < ns; s++) mm = fmaxf(mm, ml[s].x);
     const float mu = (mm == -INFINITY) ? 0.0f : mm;
     float tl = 0.0f;
-    float acc[D / 64];
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    auto add = [&](float2 m_l, float4 v) {
+        const float f = exp2f(m_l.x - mu);
+        tl = tl + m_l.y * f;
+        a0 = a0 + v.x * f;
+        a1 = a1 + v.y * f;
+        a2 = a2 + v.z * f;
+        a3 = a3 + v.w * f;
+    };
 #pragma unroll
-    for (int e = 0; e < D / 64; e++) acc[e] = 0.0f;
-    for (int s = 0; s < ns; s++) {
-        const float f = exp2f(ml[s].x - mu);
-        tl = tl + ml[s].y * f;
-        const float* po = part_o + (row * nsplit + s) * D;
-#pragma unroll
-        for (int e = 0; e < D / 64; e++) acc[e] = acc[e] + po[lane + 64 * e] * f;
-    }
+    for (int s = 0; s < CMAX; s++)
+        if (s < ns) add(mlv[s], pv[s]);
+    for (int s = CMAX; s < ns; s++) add(ml[s], *reinterpret_cast<const float4*>(pr + s * D));
     const float inv = 1.0f / tl;
-#pragma unroll
-    for (int e = 0; e < D / 64; e++) {
-        const float v = acc[e] * inv;
-        if constexpr (sizeof(OT) == 2)
-            out[row * D + lane + 64 * e] = bf16_from_f32(v);
-        else
-            out[row * D + lane + 64 * e] = v;
-    }
-    if (lse && lane == 0) lse[row] = mu * LN2 + logf(tl);
+    if constexpr (sizeof(OT) == 2)
+        *reinterpret_cast<uint2*>(out + row * D + c4) = make_uint2(pack2_bf16(a0 * inv, a1 * inv),
+                                                                   pack2_bf16(a2 * inv, a3 * inv));
+    else
+        *reinterpret_cast<float4*>(out + row * D + c4) = make_float4(a0 * inv, a1 * inv, a2 * inv, a3 * inv);
+    if (lse && c4 == 0) lse[row] = mu * LN2 + logf(tl);
 }
 
 // ---------------------------------------------------------------------------
@@ -865,19 +905,59 @@ int prefill_tiles_per_split(int64_t B, int64_t Hq, int64_t L, int64_t S, int cau
     return (int)std::max<int64_t>(8, (ntiles + 3) / 4);
 }
 
-// 64-key tiles per work item of the bf16 prefill. Rows stay whole once the
-// query blocks alone give every CU (256) a workgroup; below that, rows are
-// split into items of at least 16 tiles (a split costs a workgroup's fixed
-// start-up, about 2 us, and the partials it writes) so that the items about
-// fill the device once.
-int flash_tiles_per_split(int64_t B, int64_t Hq, int64_t L, int64_t S, int causal) {
+// First query row of the query blocks whose rows are split (L when none is):
+// a causal row's tile count grows with its block, so they are the last ones.
+int64_t first_split_row(int64_t L, int64_t S, int causal, int bq, int bk, int target) {
+    const int64_t nqb = cdiv(L, bq);
+    for (int64_t qt = 0; qt < nqb; qt++)
+        if (row_splits((int)cdiv(causal ? std::min<int64_t>(S, (qt + 1) * bq) : S, bk), target) > 1) return qt * bq;
+    return L;
+}
+
+// Work list of the bf16 prefill (see FlashWork). Items aim at the tiles of
+// the whole call spread over 512 workgroups (two per CU), at least 16 tiles
+// each: a split costs a workgroup's start-up, about 2 us, and the partials it
+// writes and merges (measured on config 2: 16-tile items beat 8 to 12 and
+// whole rows), so rows that fit stay whole. Returns the number of workgroups
+// and the largest split count (the partial layout's stride).
+int64_t flash_work(int64_t B, int64_t Hq, int64_t L, int64_t S, int causal, FlashWork& w, int& nsplit) {
     const int64_t nqb = cdiv(L, F3_BQ);
-    const int64_t row_tiles = cdiv(causal ? std::min<int64_t>(S, nqb * F3_BQ) : S, F3_BK);
-    if (B * Hq * nqb >= 256) return (int)std::min<int64_t>(row_tiles, INT32_MAX);
-    int64_t total = 0;  // tiles over all query blocks of one head
-    for (int64_t qb = 0; qb < nqb; qb++) total += cdiv(causal ? std::min<int64_t>(S, (qb + 1) * F3_BQ) : S, F3_BK);
-    total *= B * Hq;
-    return (int)std::min<int64_t>(std::max<int64_t>(16, cdiv(total, 256)), INT32_MAX);
+    auto ntiles = [&](int64_t qt) {
+        return (int)cdiv(causal ? std::min<int64_t>(S, (qt + 1) * F3_BQ) : S, F3_BK);
+    };
+    int row_max = 0;
+    int64_t total = 0;  // tiles of one head
+    for (int64_t qt = 0; qt < nqb; qt++) {
+        row_max = std::max(row_max, ntiles(qt));
+        total += ntiles(qt);
+    }
+    w.bh = (int)(B * Hq);
+    int target = (int)std::min<int64_t>(row_max, std::max<int64_t>(16, cdiv(total * B * Hq, 512)));
+    std::vector<std::pair<int, uint32_t>> cls;  // (tiles, qt | split << 16)
+    for (;;) {
+        cls.clear();
+        for (int64_t qt = nqb - 1; qt >= 0 && (int64_t)cls.size() <= FLASH_MAX_CLS; qt--) {
+            const int n = ntiles(qt), ns = row_splits(n, target);
+            for (int s = 0; s < ns; s++)
+                cls.emplace_back((s + 1) * n / ns - s * n / ns, (uint32_t)qt | ((uint32_t)s << 16));
+        }
+        if (target >= row_max || (int64_t)cls.size() <= FLASH_MAX_CLS) break;
+        target = std::min(row_max, target * 2);  // too many classes for the table: coarser items
+    }
+    w.target = target;
+    if (target >= row_max) {  // nothing split: class c is query block nqb-1-c
+        w.ncls = 0;
+        nsplit = 1;
+        return nqb * B * Hq;
+    }
+    std::stable_sort(cls.begin(), cls.end(), [](const auto& a, const auto& b) { return a.first > b.first; });
+    w.ncls = (int)cls.size();
+    nsplit = 1;
+    for (size_t i = 0; i < cls.size(); i++) {
+        w.cls[i] = cls[i].second;
+        nsplit = std::max(nsplit, (int)(cls[i].second >> 16) + 1);
+    }
+    return (int64_t)w.ncls * B * Hq;
 }
 
 }  // namespace
@@ -933,10 +1013,10 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     if (dtype == TN_BF16) {
         // the key/value buffer descriptors cover one head's S*D elements
         if (S * D * 2 > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": key length too large");
-        const int64_t nqb = cdiv(L, F3_BQ);
-        const int tiles_per = flash_tiles_per_split(B, Hq, L, S, c);
-        const int64_t kend_max = is_causal ? std::min<int64_t>(S, nqb * F3_BQ) : S;
-        const int nsplit = (int)cdiv(cdiv(kend_max, F3_BK), tiles_per);
+        FlashWork work;
+        int nsplit = 1;
+        const int64_t nitems = flash_work(B, Hq, L, S, c, work, nsplit);
+        if (nitems > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": shape too large");
         float* part_o = nullptr;
         float2* part_ml = nullptr;
         if (nsplit > 1) {
@@ -948,27 +1028,29 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
             part_o = static_cast<float*>(ws);
             part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + po);
         }
-        if (nqb * nsplit > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": shape too large");
-        dim3 grid((unsigned)(nqb * nsplit), (unsigned)Hq, (unsigned)B);
         auto qq = static_cast<const uint16_t*>(q);
         auto kk = static_cast<const uint16_t*>(k);
         auto vv = static_cast<const uint16_t*>(v);
         auto oo = static_cast<uint16_t*>(out);
         if (D == 64)
-            hipLaunchKernelGGL(k_flash_bf16<64>, grid, dim3(128 * FlashCfg<64>::KG), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
-                               (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml);
+            hipLaunchKernelGGL(k_flash_bf16<64>, dim3((unsigned)nitems), dim3(128 * FlashCfg<64>::KG), 0, st, qq, kk,
+                               vv, (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, work, nsplit, oo, lse, part_o, part_ml);
         else
-            hipLaunchKernelGGL(k_flash_bf16<128>, grid, dim3(128 * FlashCfg<128>::KG), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
-                               (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml);
+            hipLaunchKernelGGL(k_flash_bf16<128>, dim3((unsigned)nitems), dim3(128 * FlashCfg<128>::KG), 0, st, qq,
+                               kk, vv, (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, work, nsplit, oo, lse, part_o,
+                               part_ml);
         TN_LAUNCHED();
         if (nsplit > 1) {
-            const unsigned g2 = (unsigned)cdiv(rows, 4);
+            const int64_t row_lo = first_split_row(L, S, c, F3_BQ, F3_BK, work.target);
+            const int64_t nrb = cdiv(L - row_lo, 256 / (D / 4));
+            if (nrb * B * Hq > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": shape too large");
+            const dim3 g2((unsigned)(nrb * B * Hq));
             if (D == 64)
-                hipLaunchKernelGGL((k_prefill_combine<64, uint16_t>), dim3(g2), dim3(256), 0, st, part_o, part_ml,
-                                   (int)L, (int)S, c, F3_BQ, F3_BK, tiles_per, nsplit, rows, oo, lse);
+                hipLaunchKernelGGL((k_prefill_combine<64, uint16_t>), g2, dim3(256), 0, st, part_o, part_ml, (int)L,
+                                   (int)S, c, F3_BQ, F3_BK, work.target, nsplit, (int)row_lo, (int)nrb, oo, lse);
             else
-                hipLaunchKernelGGL((k_prefill_combine<128, uint16_t>), dim3(g2), dim3(256), 0, st, part_o,
-                                   part_ml, (int)L, (int)S, c, F3_BQ, F3_BK, tiles_per, nsplit, rows, oo, lse);
+                hipLaunchKernelGGL((k_prefill_combine<128, uint16_t>), g2, dim3(256), 0, st, part_o, part_ml, (int)L,
+                                   (int)S, c, F3_BQ, F3_BK, work.target, nsplit, (int)row_lo, (int)nrb, oo, lse);
             TN_LAUNCHED();
         }
         return TN_OK;
@@ -1004,13 +1086,16 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
                                (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml);
         TN_LAUNCHED();
         if (nsplit > 1) {
-            const unsigned g2 = (unsigned)cdiv(rows, 4);
+            const int64_t row_lo = first_split_row(L, S, c, PF_BQ, bk, tiles_per);
+            const int64_t nrb = cdiv(L - row_lo, 256 / (D / 4));
+            if (nrb * B * Hq > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": shape too large");
+            const dim3 g2((unsigned)(nrb * B * Hq));
             if (D == 64)
-                hipLaunchKernelGGL((k_prefill_combine<64, float>), dim3(g2), dim3(256), 0, st, part_o, part_ml,
-                                   (int)L, (int)S, c, PF_BQ, bk, tiles_per, nsplit, rows, oo, lse);
+                hipLaunchKernelGGL((k_prefill_combine<64, float>), g2, dim3(256), 0, st, part_o, part_ml, (int)L,
+                                   (int)S, c, PF_BQ, bk, tiles_per, nsplit, (int)row_lo, (int)nrb, oo, lse);
             else
-                hipLaunchKernelGGL((k_prefill_combine<128, float>), dim3(g2), dim3(256), 0, st, part_o, part_ml,
-                                   (int)L, (int)S, c, PF_BQ, bk, tiles_per, nsplit, rows, oo, lse);
+                hipLaunchKernelGGL((k_prefill_combine<128, float>), g2, dim3(256), 0, st, part_o, part_ml, (int)L,
+                                   (int)S, c, PF_BQ, bk, tiles_per, nsplit, (int)row_lo, (int)nrb, oo, lse);
             TN_LAUNCHED();
         }
     }
