@@ -526,8 +526,13 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     // (row, block) items must fit GEMV_ITEMS per thread
     if ((int64_t)rows * nb > GEMV_THREADS * GEMV_ITEMS) return TN_ENOTIMPL;
     const int64_t ntiles = cdiv(N, rows);
-    // persistent: about 8 resident workgroups per CU on 256 CUs
-    const unsigned grid = (unsigned)(ntiles < 2048 ? ntiles : 2048);
+    // persistent: exactly as many workgroups as the device holds at once (a
+    // workgroup that had to wait for a slot would start its whole share of
+    // tiles late)
+    int resident = 0;
+    tn_status s = resident_workgroups(reinterpret_cast<const void*>(&k_gemv<MR, XT>), GEMV_THREADS, lds, &resident);
+    if (s != TN_OK) return s;
+    const unsigned grid = (unsigned)(ntiles < resident ? ntiles : resident);
     hipLaunchKernelGGL((k_gemv<MR, XT>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N, rows,
                        bias, y, y_bf16);
     TN_LAUNCHED();

@@ -68,6 +68,45 @@ tn_status workspace(hipStream_t stream, size_t bytes, void** out) {
     return TN_OK;
 }
 
+namespace {
+struct OccKey {
+    int dev;
+    const void* kernel;
+    int block;
+    size_t lds;
+    bool operator<(const OccKey& o) const {
+        if (dev != o.dev) return dev < o.dev;
+        if (kernel != o.kernel) return kernel < o.kernel;
+        if (block != o.block) return block < o.block;
+        return lds < o.lds;
+    }
+};
+std::mutex g_occ_mu;
+std::map<OccKey, int> g_occ;
+}  // namespace
+
+tn_status resident_workgroups(const void* kernel, int block, size_t lds, int* out) {
+    int dev = 0;
+    TN_HIP(hipGetDevice(&dev));
+    const OccKey key{dev, kernel, block, lds};
+    {
+        std::lock_guard<std::mutex> lock(g_occ_mu);
+        auto it = g_occ.find(key);
+        if (it != g_occ.end()) {
+            *out = it->second;
+            return TN_OK;
+        }
+    }
+    int per_cu = 0, cus = 0;
+    TN_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds));
+    TN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int n = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    std::lock_guard<std::mutex> lock(g_occ_mu);
+    g_occ[key] = n;
+    *out = n;
+    return TN_OK;
+}
+
 }  // namespace tn
 
 using namespace tn;

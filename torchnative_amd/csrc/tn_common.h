@@ -33,6 +33,11 @@ Counters& counters();
 // Grow-only device workspace, one per (device, stream). Calls on one stream
 // are ordered, so reuse across them is safe.
 tn_status workspace(hipStream_t stream, size_t bytes, void** out);
+// Workgroups of `kernel` (block threads, lds dynamic bytes) that the current
+// device holds at once: the size of a persistent grid, all of whose
+// workgroups must be resident from the start. Cached per (device, kernel,
+// block, lds).
+tn_status resident_workgroups(const void* kernel, int block, size_t lds, int* out);
 
 #define TN_HIP(call)                                              \
     do {                                                          \
