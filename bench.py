@@ -213,27 +213,65 @@ def bench_decode(tn, L, steps, warmup, sets=3):
                          "frac": ach / HBM_PEAK_GBS, "traffic": None}}
 
 
-def cpu_baseline_sdpa(threads):
+def cpu_baseline_sdpa(threads, seconds=10.0):
     """The oracle's restatement of the reference's default SDPA path (f32
-    body, bf16 in/out) on config 2 -- 4 of the 9 query heads (with their 2 KV
-    heads), scaled to the full workload's TFLOP/s."""
+    body, bf16 in/out) on the full config 2 (9/3 heads, causal, S=2048),
+    repeated until about `seconds` of wall time have passed, in TFLOP/s of the
+    same algorithmic flop count as the GPU line."""
     import oracle as O
 
     rng = np.random.default_rng(2)
-    S, D = 2048, 64
-    hq, hkv = 3, 1  # one GQA group; x3 for the 9/3-head workload
+    S, D, hq, hkv = 2048, 64, 9, 3
     q = O.bf16_to_f32(O.bf16_from_f32(rng.standard_normal((1, hq, S, D)).astype(np.float32)))
     k = O.bf16_to_f32(O.bf16_from_f32(rng.standard_normal((1, hkv, S, D)).astype(np.float32)))
     v = O.bf16_to_f32(O.bf16_from_f32(rng.standard_normal((1, hkv, S, D)).astype(np.float32)))
     O.sdpa(q[:, :, :64], k, v, is_causal=True, threads=threads)  # warm
+    reps = 0
     t0 = time.perf_counter()
-    out, _ = O.sdpa(q, k, v, is_causal=True, threads=threads)
-    O.bf16_from_f32(out)
-    sec = time.perf_counter() - t0
-    flops = 4.0 * D * hq * S * (S + 1) / 2  # the same algorithmic flop count as the GPU line
+    while True:
+        out, _ = O.sdpa(q, k, v, is_causal=True, threads=threads)
+        O.bf16_from_f32(out)
+        reps += 1
+        sec = time.perf_counter() - t0
+        if sec >= seconds:
+            break
+    flops = 4.0 * D * hq * S * (S + 1) / 2 * reps
     return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"config 2 restricted to one GQA group (3 of 9 query heads, 1 of 3 KV heads), causal, "
-                      f"bf16 inputs widened to f32; {sec:.2f} s for {flops / 1e9:.2f} GFLOP"}
+            "sample": f"config 2 in full (9 q heads / 3 kv heads, causal, S=2048, bf16 inputs widened to f32, "
+                      f"output narrowed to bf16) x {reps} repetitions: {sec:.1f} s for {flops / 1e9:.1f} GFLOP"}
+
+
+# The copy kernel that scales the PMC byte counters: tn_q4_0_from_blob over a
+# 288 MiB blob reads and writes each of its bytes exactly once.
+COPY_CAL_BLOCKS = 16 * 1024 * 1024
+
+
+def calibrate_copy(tn, L, steps):
+    lib = L.lib()
+    nbytes = COPY_CAL_BLOCKS * 18
+    blob = tn.empty((nbytes,), "uint8", "hip")
+    blob.zero_()
+    qs = tn.empty((COPY_CAL_BLOCKS * 16,), "uint8", "hip")
+    d = tn.empty((COPY_CAL_BLOCKS,), "float16", "hip")  # the f16 scale plane
+    for _ in range(steps):
+        L.check(lib.tn_q4_0_from_blob(None, blob.data_ptr(), COPY_CAL_BLOCKS, 32, qs.data_ptr(), d.data_ptr()))
+    tn.synchronize()
+    print(json.dumps({"copy_kernel": "tn_q4_0_from_blob", "read_bytes": nbytes, "write_bytes": nbytes,
+                      "launches": steps}))
+
+
+def profiled_traffic(name):
+    """HBM bytes per launch of the headline kernel, as committed in
+    profiles/<name> (line `traffic_bytes_per_launch: N`), or None."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
 
 
 def cpu_threads():
@@ -248,6 +286,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c3,c4)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only the copy kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} asked); the path would shard by "
@@ -259,6 +299,9 @@ def main():
     from torchnative_amd import _lib as L
 
     info = tn._hip_probe()
+    if args.calibrate_copy:
+        calibrate_copy(tn, L, args.steps)
+        return
     only = set(filter(None, args.only.split(",")))
     want = (lambda p: not only or p in only)
     parts = {}
@@ -276,6 +319,7 @@ def main():
         parts["c4_decode_attention"] = bench_decode(tn, L, args.steps, args.warmup)
     print("bench: c2 SDPA prefill bf16 (headline)", file=sys.stderr, flush=True)
     head = bench_sdpa(tn, L, "bfloat16", args.steps, args.warmup)
+    head["roofline"]["traffic"] = profiled_traffic("flash_bf16_c2_traffic.md")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -300,7 +344,7 @@ def main():
                    "flops_per_step": head["flops"]},
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
-        "device": info.get("name"),
+        "device": info.get("name") or info.get("arch"),
         "parts": parts,
     }
     print(json.dumps(line))
