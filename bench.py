@@ -13,7 +13,9 @@ configs are measured in the same run and reported under "parts":
   c2  SDPA prefill, bf16 (headline) and fp32;
   c3  q4_0 prefill GEMM x bf16 [512,4096] x W [14336,4096]^T, bf16 out;
   c4  decode attention, B=16, 32/8 heads, D=128, bf16, lens ~ U[512,4096],
-      rotated over 3 KV sets (> MALL).
+      rotated over 3 KV sets (> MALL);
+  c5  greedy decode of the random-init 30-layer q4_0 Llama, 256-token prompt,
+      128 new tokens, tokens/s over the steps after the prompt.
 
 Kernel time comes from HIP events on the stream the kernels run on; the
 step time from the host clock around synchronised regions. The CPU baseline
@@ -213,6 +215,63 @@ def bench_decode(tn, L, steps, warmup, sets=3):
                          "frac": ach / HBM_PEAK_GBS, "traffic": None}}
 
 
+def bench_e2e(tn, L, prompt_len=256, n_new=128, seed=5):
+    """greedy decode of the random-init 30-layer q4_0
+    Llama (hidden 576, 9/3 heads, MLP 1536, vocab 49152). As the reference's
+    bench does (tests/bench/bench_llama_cpp.py:540-569), the prompt yields
+    the first token and the next n_new - 1 steps are timed: tokens/s =
+    (n_new - 1) / seconds. The timed steps run as one captured HIP graph;
+    the same steps issued one call at a time are reported beside it."""
+    from torchnative_amd.decoder import LlamaConfig, Q4Llama
+
+    cfg = LlamaConfig()
+    model = Q4Llama(cfg, seed=0, cap=prompt_len + n_new)
+    prompt = np.random.default_rng(seed).integers(0, cfg.vocab, prompt_len).astype(np.int32)
+    s = ctypes.c_void_p()
+    L.check(L.lib().tn_stream_create(ctypes.byref(s)))
+    st = s.value
+    lib = L.lib()
+
+    def run_prompt():
+        model.start(prompt)
+        for _ in range(prompt_len):
+            model.step(st)
+        L.check(lib.tn_stream_synchronize(st))
+
+    try:
+        run_prompt()
+        graph = model.capture(n_new - 1, st)
+        graph.launch(st)  # warm: the first launch uploads the graph
+        L.check(lib.tn_stream_synchronize(st))
+        warm_tokens = model.generated(prompt_len, n_new)
+        run_prompt()
+        t0 = time.perf_counter()
+        graph.launch(st)
+        L.check(lib.tn_stream_synchronize(st))
+        graph_s = time.perf_counter() - t0
+        tokens = model.generated(prompt_len, n_new)
+        graph.close()
+        run_prompt()
+        t0 = time.perf_counter()
+        for _ in range(n_new - 1):
+            model.step(st)
+        L.check(lib.tn_stream_synchronize(st))
+        eager_s = time.perf_counter() - t0
+        eager_tokens = model.generated(prompt_len, n_new)
+    finally:
+        L.check(lib.tn_stream_destroy(st))
+    weight_bytes = cfg.n_layers * ((cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim * cfg.hidden
+                                   + cfg.hidden * cfg.n_heads * cfg.head_dim + 3 * cfg.inter * cfg.hidden)
+    weight_bytes = (weight_bytes + cfg.vocab * cfg.hidden) // 32 * 18
+    tps = (n_new - 1) / graph_s
+    return {"tokens_per_s": tps, "ms_per_token": graph_s * 1e3 / (n_new - 1),
+            "eager_tokens_per_s": (n_new - 1) / eager_s, "prompt_tokens": prompt_len, "new_tokens": n_new,
+            "q4_weight_bytes_per_token": weight_bytes,
+            "weight_stream_gbs": weight_bytes * tps / 1e9,
+            "same_tokens_graph_eager_warm": tokens == eager_tokens == warm_tokens,
+            "first_tokens": tokens[:16]}
+
+
 def cpu_baseline_sdpa(threads, seconds=10.0):
     """The oracle's restatement of the reference's default SDPA path (f32
     body, bf16 in/out) on the full config 2 (9/3 heads, causal, S=2048),
@@ -285,7 +344,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c3,c4)")
+    ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c3,c4,c5)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the copy kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
@@ -317,6 +376,9 @@ def main():
     if want("c4"):
         print("bench: c4 decode attention", file=sys.stderr, flush=True)
         parts["c4_decode_attention"] = bench_decode(tn, L, args.steps, args.warmup)
+    if want("c5"):
+        print("bench: c5 end-to-end greedy decode", file=sys.stderr, flush=True)
+        parts["c5_e2e_decode"] = bench_e2e(tn, L)
     print("bench: c2 SDPA prefill bf16 (headline)", file=sys.stderr, flush=True)
     head = bench_sdpa(tn, L, "bfloat16", args.steps, args.warmup)
     head["roofline"]["traffic"] = profiled_traffic("flash_bf16_c2_traffic.md")

@@ -165,14 +165,129 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
  * [B, Hkv, cap, D] with head stride cap*D, sequence b using keys 0..lens[b]-1.
  * Equals tn_sdpa_fwd with L = 1, non-causal, on the view k[:, :, :lens[b]]
  * (the reference passes attn_mask=None at L=1, sdpa_metal.rs:23-30).
- *   q [B, Hq, D], out [B, Hq, D] in `dtype`; lens: device int32 [B], each in
- *   [1, cap]; max_len: host upper bound of lens (sizes the split-KV grid);
+ *   q [B, Hq, D], out [B, Hq, D] and the caches in `dtype` (TN_BF16, or
+ *   TN_F32 for an f32 model); lens: device int32 [B], each in [1, cap];
+ *   max_len: host upper bound of lens (sizes the split-KV grid);
  *   lse nullable f32 [B, Hq].
  * Split-KV with a combine pass; the partials live in the library workspace. */
 tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_cache,
                          const void* v_cache, int64_t B, int64_t Hq, int64_t Hkv, int64_t cap,
                          int64_t D, const int32_t* lens, int64_t max_len, double scale,
                          void* out, float* lse);
+
+/* ---- decode-step ops ----
+ * The per-token aten ops around the linear and the attention in a Llama-style
+ * decoder step, f32, as the reference runs them for an f32 model
+ * (`transformers`' LlamaForCausalLM over torch._C; the op census of a decode
+ * step in profile_llama_cpp.json). All tensors are dense row-major device
+ * memory; positions and token ids are device int32, so a sequence of steps
+ * can be captured as a graph once and replayed. */
+
+/* `aten.embedding.default` (aten.rs:11980-12040): out[i, :] = table[ids[i], :]
+ * for an f32 table [vocab, dim] and device int32 ids [m]. An id outside
+ * [0, vocab) gives a row of NaN (a device id cannot be checked on the host
+ * without a synchronisation). */
+tn_status tn_embedding(void* stream, const int32_t* ids, int64_t m, const float* table, int64_t vocab,
+                       int64_t dim, float* out);
+
+/* LlamaRMSNorm in f32 through the reference's ops: pow(x, 2) (aten.rs:4656),
+ * mean over the row = sum then divide (aten.rs:15812), + eps, rsqrt = sqrt
+ * then reciprocal (aten.rs:11112-11133), x * r, then weight * that.
+ * x, y [m, n]; weight [n]; y may alias x. The row sum is a tree, not the
+ * reference's order: equal within the f32 tolerance, not bitwise. */
+tn_status tn_rmsnorm(void* stream, const float* x, int64_t m, int64_t n, const float* weight, double eps,
+                     float* y);
+
+/* Rotary embedding in place (LlamaRotaryEmbedding + apply_rotary_pos_emb:
+ * x * cos + rotate_half(x) * sin, cos/sin of pos * inv_freq in f32, the
+ * angle table duplicated over the two halves). x [m, heads, d]; token t is
+ * at position pos[t] (device int32 [m]); inv_freq f32 [d/2]
+ * (1 / theta^(2i/d), computed by the caller as the model does). */
+tn_status tn_rope(void* stream, float* x, int64_t m, int64_t heads, int64_t d, const float* inv_freq,
+                  const int32_t* pos);
+
+/* silu(gate) * up: candle's silu x / (1 + exp(-x)) (candle-core op.rs:782-784,
+ * aten.rs:15360-15384), then aten.mul.Tensor. out may alias gate or up. */
+tn_status tn_silu_mul(void* stream, const float* gate, const float* up, int64_t n, float* out);
+
+/* `aten.add.Tensor` on f32 vectors: out = a + b; out may alias a or b. */
+tn_status tn_add(void* stream, const float* a, const float* b, int64_t n, float* out);
+
+/* `aten.argmax.default` over the last dim of x [m, n] f32 (aten.rs:11927-11975
+ * with first_extremum_index, aten.rs:16705-16741): the first maximal index,
+ * or the first NaN's if the row holds one. out: device int32 [m]. */
+tn_status tn_argmax(void* stream, const float* x, int64_t m, int64_t n, int32_t* out);
+
+/* KV-cache append (PreallocatedLayer.update, kernels/kv_cache.py:92-114):
+ * rows k, v [m, hkv, d] f32 go to k_cache, v_cache [hkv, cap, d] at positions
+ * pos0[0] + i. Positions at or past cap are not written (the caller sizes
+ * the cache). */
+tn_status tn_kv_append(void* stream, const float* k, const float* v, int64_t m, int64_t hkv, int64_t d,
+                       float* k_cache, float* v_cache, int64_t cap, const int32_t* pos0);
+
+/* ---- greedy decode of a q4_0 Llama-style decoder ----
+ * No single reference function: the reference runs this step as
+ * transformers' LlamaForCausalLM.forward over its torch._C ops, with every
+ * nn.Linear swapped for QuantizedLinear (quant/__init__.py:100-365), then
+ * the greedy argmax of generate(). tn_llama_step launches one whole step of
+ * that on the device, from the ops above, tn_q4_0_linear and the f32 decode
+ * attention, so that a caller (or a captured graph) pays one call per token:
+ *   h = embed[token]; per layer: x = rmsnorm(h, ln1); qkv = x W_qkv^T;
+ *   rope(q, k at pos); append k, v; a = attention(q, cache[0..pos]);
+ *   h += a W_o^T; x = rmsnorm(h, ln2); gu = x W_gate_up^T;
+ *   h += (silu(gate) * up) W_down^T; then logits = rmsnorm(h, norm) W_lm^T,
+ *   next = argmax(logits).
+ * The projections are stacked row-wise (q|k|v and gate|up): each output
+ * row of the q4 linear is computed on its own, so stacking changes no bit.
+ * Step state lives on the device in `state` (int32 [4]): [0] the position
+ * of the token being processed, [1] = [0] + 1 (the KV length), [2] that
+ * token's id, [3] the argmax of the step. After the step [0] and [1]
+ * advance by one and [2] becomes the next input: prompt[[0]] while the
+ * prompt lasts, else the argmax; it is also stored in tokens[[0]] (the
+ * caller writes tokens[0]). */
+typedef struct tn_q4_weight {
+    const uint8_t* qs; /* [n][k/32][16] nibble bytes */
+    const uint16_t* d; /* [n][k/32] f16 scales */
+} tn_q4_weight;
+
+typedef struct tn_llama_layer {
+    tn_q4_weight qkv;     /* [(n_heads + 2 n_kv_heads) head_dim, hidden] */
+    tn_q4_weight o;       /* [hidden, n_heads head_dim] */
+    tn_q4_weight gate_up; /* [2 inter, hidden]: gate rows, then up rows */
+    tn_q4_weight down;    /* [hidden, inter] */
+    const float* ln1;     /* input_layernorm weight [hidden] */
+    const float* ln2;     /* post_attention_layernorm weight [hidden] */
+    float* k_cache;       /* [n_kv_heads, cap, head_dim] f32 */
+    float* v_cache;
+} tn_llama_layer;
+
+typedef struct tn_llama {
+    int64_t n_layers, hidden, n_heads, n_kv_heads, head_dim, inter, vocab;
+    int64_t cap;        /* KV capacity = the longest sequence (prompt + generated) */
+    double eps;         /* RMSNorm epsilon */
+    const float* embed; /* [vocab, hidden] */
+    const float* norm;  /* final norm weight [hidden] */
+    tn_q4_weight lm_head;   /* [vocab, hidden] */
+    const float* inv_freq;  /* [head_dim / 2] */
+    const tn_llama_layer* layers; /* host array [n_layers] */
+    const int32_t* prompt;  /* device [prompt_len] */
+    int64_t prompt_len;
+    int32_t* state;     /* device [4], see above */
+    int32_t* tokens;    /* device [cap]: tokens[p] = the input token at position p */
+    float* logits;      /* device [vocab], the last step's logits */
+    float* work;        /* device scratch, tn_llama_work_floats() floats */
+} tn_llama;
+
+/* Floats of device scratch tn_llama_step needs for this model. */
+int64_t tn_llama_work_floats(const tn_llama* model);
+/* One decode step of `model` on `stream` (see above). Allocates nothing. */
+tn_status tn_llama_step(void* stream, const tn_llama* model);
+/* Captures `steps` consecutive calls of tn_llama_step into a HIP graph
+ * (hipGraphExec_t returned in *graph) for replay with tn_graph_launch. The
+ * model's buffers must stay valid while the graph lives. */
+tn_status tn_llama_capture(void* stream, const tn_llama* model, int64_t steps, void** graph);
+tn_status tn_graph_launch(void* stream, void* graph);
+tn_status tn_graph_destroy(void* graph);
 
 #ifdef __cplusplus
 }

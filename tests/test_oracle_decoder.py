@@ -1,0 +1,107 @@
+"""The oracle's decode-step restatement (oracle/decoder.py), pinned by what
+the mathematics fixes rather than by retyping its formulas: rotation
+identities for RoPE, the odd-part identity of SiLU, closed forms and scale
+invariance for RMSNorm, argmax's documented tie and NaN rules, a one-key
+attention, and the float32 run's agreement with the float64 one."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from oracle import decoder as OD
+
+CFG = OD.LlamaConfig()
+
+
+def test_inv_freq_is_one_over_theta_to_the_2i_over_d():
+    f = OD.inv_freq(CFG)
+    assert f.dtype == np.float32 and f.shape == (32,)
+    assert f[0] == 1.0
+    exact = 1.0 / (1e5 ** (np.arange(0, 64, 2) / 64.0))
+    assert np.max(np.abs(f - exact) / exact) < 4e-7  # float32 rounding of pow and of the division
+
+
+def test_rope_is_a_rotation_by_pos_times_the_frequency():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((3, 64))
+    f = OD.inv_freq(CFG).astype(np.float64)
+    assert np.array_equal(OD.rope(x, 0, f, np.float64), x)  # position 0
+    for pos in (1, 17, 300):
+        y = OD.rope(x, pos, f, np.float64)
+        # the complex-number form: (x1 + i x2) * exp(i pos f)
+        z = (x[:, :32] + 1j * x[:, 32:]) * np.exp(1j * pos * f)
+        assert np.allclose(y[:, :32], z.real, rtol=0, atol=1e-12)
+        assert np.allclose(y[:, 32:], z.imag, rtol=0, atol=1e-12)
+        # pairs keep their length, and rotations compose
+        assert np.allclose(np.hypot(y[:, :32], y[:, 32:]), np.hypot(x[:, :32], x[:, 32:]), atol=1e-12)
+        assert np.allclose(OD.rope(OD.rope(x, 5, f, np.float64), pos, f, np.float64),
+                           OD.rope(x, 5 + pos, f, np.float64), atol=1e-11)
+
+
+def test_silu_odd_part_identity():
+    x = np.linspace(-20, 20, 4001)
+    one = np.ones_like(x)
+    s = OD.silu_mul(x, one, np.float64)
+    # x * sigmoid(x) - (-x) * sigmoid(-x) = x, and silu(0) = 0
+    assert np.allclose(s - OD.silu_mul(-x, one, np.float64), x, atol=1e-12)
+    assert OD.silu_mul(np.array([0.0]), np.array([1.0]), np.float64)[0] == 0.0
+
+
+def test_rmsnorm_closed_form_and_scale_invariance():
+    c = 3.0
+    y = OD.rmsnorm(np.full(576, c), np.ones(576), 1e-5, np.float64)
+    assert np.allclose(y, c / np.sqrt(c * c + 1e-5), rtol=1e-15)
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(576).astype(np.float32)
+    w = rng.standard_normal(576).astype(np.float32)
+    # eps = 0: scaling the row by a power of two changes no bit
+    assert np.array_equal(OD.rmsnorm(x, w, 0.0), OD.rmsnorm(x * np.float32(8), w, 0.0))
+    # and the weight multiplies the normalised row
+    assert np.array_equal(OD.rmsnorm(x, w, 1e-5), w * OD.rmsnorm(x, np.ones(576, np.float32), 1e-5))
+
+
+def test_argmax_rules():
+    assert OD.argmax([1.0, 3.0, 3.0, 2.0]) == 1
+    assert OD.argmax([-np.inf, -np.inf]) == 0
+    assert OD.argmax([1.0, np.nan, np.inf, np.nan]) == 1
+
+
+def test_one_key_attention_returns_v():
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((1, 9, 1, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 3, 1, 64)).astype(np.float32)
+    v = rng.standard_normal((1, 3, 1, 64)).astype(np.float32)
+    out, _ = O.sdpa(q, k, v)
+    assert np.array_equal(out[0, :, 0], np.repeat(v[0, :, 0], 3, axis=0))
+
+
+SMALL = OD.LlamaConfig(n_layers=2, hidden=128, n_heads=2, n_kv_heads=1, head_dim=64, inter=256, vocab=512)
+
+
+def test_decoder_float32_run_tracks_the_float64_run():
+    r32 = OD.Decoder(SMALL, 3, 8, np.float32)
+    r64 = OD.Decoder(SMALL, 3, 8, np.float64)
+    for pos, tok in enumerate([7, 300, 2, 511]):
+        a, b = r32.step(tok, pos), r64.step(tok, pos)
+        assert a.dtype == np.float32 and a.shape == (SMALL.vocab,)
+        assert np.max(np.abs(a - b)) < 1e-3 * np.max(np.abs(b)), pos
+
+
+def test_stacked_projections_equal_separate_ones():
+    """Stacking q|k|v (and gate|up) row-wise changes no bit of the quantised
+    linear: each output row is its own recurrence."""
+    w = OD.layer_weights(SMALL, 0, 4)
+    x = np.random.default_rng(5).standard_normal((1, SMALL.hidden)).astype(np.float32)
+    blob = O.q4_0_quantize(w["qkv"])
+    full = O.q4_0_linear(x, blob, w["qkv"].shape[0])
+    q = w["qkv"][:128]
+    assert np.array_equal(full[:, :128], O.q4_0_linear(x, O.q4_0_quantize(q), 128))
+
+
+@pytest.mark.parametrize("n", [1, 5])
+def test_model_weights_are_deterministic(n):
+    a = OD.layer_weights(SMALL, n, 9)
+    b = OD.layer_weights(SMALL, n, 9)
+    assert all(np.array_equal(a[k], b[k]) for k in a)
+    c = OD.layer_weights(SMALL, n, 10)
+    assert not np.array_equal(a["qkv"], c["qkv"])

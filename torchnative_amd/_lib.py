@@ -31,6 +31,31 @@ class Counters(ctypes.Structure):
     ]
 
 
+class Q4Weight(ctypes.Structure):
+    _fields_ = [("qs", ctypes.c_void_p), ("d", ctypes.c_void_p)]
+
+
+class LlamaLayer(ctypes.Structure):
+    _fields_ = [
+        ("qkv", Q4Weight), ("o", Q4Weight), ("gate_up", Q4Weight), ("down", Q4Weight),
+        ("ln1", ctypes.c_void_p), ("ln2", ctypes.c_void_p),
+        ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+    ]
+
+
+class Llama(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", ctypes.c_int64), ("hidden", ctypes.c_int64), ("n_heads", ctypes.c_int64),
+        ("n_kv_heads", ctypes.c_int64), ("head_dim", ctypes.c_int64), ("inter", ctypes.c_int64),
+        ("vocab", ctypes.c_int64), ("cap", ctypes.c_int64), ("eps", ctypes.c_double),
+        ("embed", ctypes.c_void_p), ("norm", ctypes.c_void_p), ("lm_head", Q4Weight),
+        ("inv_freq", ctypes.c_void_p), ("layers", ctypes.POINTER(LlamaLayer)),
+        ("prompt", ctypes.c_void_p), ("prompt_len", ctypes.c_int64),
+        ("state", ctypes.c_void_p), ("tokens", ctypes.c_void_p), ("logits", ctypes.c_void_p),
+        ("work", ctypes.c_void_p),
+    ]
+
+
 SIGNATURES = {
     "tn_last_error": (ctypes.c_char_p, []),
     "tn_abi_version": (_I, []),
@@ -63,6 +88,18 @@ SIGNATURES = {
     "tn_q4_0_linear": (_I, [_P, _P, _I, _I64, _I64, _P, _P, _I64, _P, _P, _I]),
     "tn_sdpa_fwd": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I, _I, _D, _P, _P]),
     "tn_sdpa_decode": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _D, _P, _P]),
+    "tn_embedding": (_I, [_P, _P, _I64, _P, _I64, _I64, _P]),
+    "tn_rmsnorm": (_I, [_P, _P, _I64, _I64, _P, _D, _P]),
+    "tn_rope": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
+    "tn_silu_mul": (_I, [_P, _P, _P, _I64, _P]),
+    "tn_add": (_I, [_P, _P, _P, _I64, _P]),
+    "tn_argmax": (_I, [_P, _P, _I64, _I64, _P]),
+    "tn_kv_append": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P]),
+    "tn_llama_work_floats": (_I64, [ctypes.POINTER(Llama)]),
+    "tn_llama_step": (_I, [_P, ctypes.POINTER(Llama)]),
+    "tn_llama_capture": (_I, [_P, ctypes.POINTER(Llama), _I64, ctypes.POINTER(_P)]),
+    "tn_graph_launch": (_I, [_P, _P]),
+    "tn_graph_destroy": (_I, [_P]),
 }
 
 _lib = None

@@ -716,6 +716,7 @@ __global__ __launch_bounds__(256) void k_prefill_combine(const float* __restrict
 
 constexpr int DEC_WAVE_KEYS = 64;
 constexpr int DEC_SPLIT = 4 * DEC_WAVE_KEYS;  // keys per workgroup
+static_assert(DEC_SPLIT == DECODE_SPLIT_KEYS, "the decode step sizes its partials with this");
 
 template <int D, int NR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
@@ -858,11 +859,86 @@ void k_decode_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restrict__
     }
 }
 
+// Decode, f32 (the precision the reference runs an f32 model in). Grid
+// (splits of 256 keys, Hq, B); thread t of a workgroup scores key t of the
+// split (a sequential f32 dot over D), the workgroup reduces max and sum,
+// then D-wide thread groups accumulate P.V over interleaved keys with
+// coalesced V rows and merge in LDS. Writes the same (m, l, O) partial per
+// split as the bf16 kernel.
 template <int D>
+__global__ __launch_bounds__(256) void k_decode_f32(const float* __restrict__ Qg, const float* __restrict__ Kc,
+                                                  const float* __restrict__ Vc, int Hq, int Hkv, int nrep, int cap,
+                                                  const int32_t* __restrict__ lens, int nsplit, float sl2,
+                                                  float* __restrict__ part_o, float2* __restrict__ part_ml) {
+    constexpr int G = 256 / D;  // key groups in P.V
+    __shared__ __align__(16) float sq[D];
+    __shared__ float sp[DEC_SPLIT];
+    __shared__ float sred[2][4];
+    __shared__ float so[G][D];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / nrep;
+    int len = lens[b];
+    len = len < 0 ? 0 : (len > cap ? cap : len);
+    if (split * DEC_SPLIT >= len) return;  // uniform over the workgroup
+    const int k0 = split * DEC_SPLIT;
+    const int nk = min(len - k0, DEC_SPLIT);
+    const float* kp = Kc + ((int64_t)b * Hkv + kvh) * cap * D;
+    const float* vp = Vc + ((int64_t)b * Hkv + kvh) * cap * D;
+    if (tid < D) sq[tid] = Qg[((int64_t)b * Hq + h) * D + tid];
+    __syncthreads();
+
+    float s = -INFINITY;
+    if (tid < nk) {
+        const float4* kr = reinterpret_cast<const float4*>(kp + (int64_t)(k0 + tid) * D);
+        const float4* qr = reinterpret_cast<const float4*>(sq);
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < D / 4; c++) {
+            const float4 kv = kr[c], qv = qr[c];
+            acc = acc + qv.x * kv.x;
+            acc = acc + qv.y * kv.y;
+            acc = acc + qv.z * kv.z;
+            acc = acc + qv.w * kv.w;
+        }
+        s = acc * sl2;
+    }
+    float mx = s;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) sred[0][w] = mx;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(sred[0][0], sred[0][1]), fmaxf(sred[0][2], sred[0][3]));
+    const float mu = (m == -INFINITY) ? 0.0f : m;
+    const float p = (tid < nk) ? exp2f(s - mu) : 0.0f;
+    sp[tid] = p;
+    float l = p;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) l = l + __shfl_xor(l, off);
+    if (lane == 0) sred[1][w] = l;
+    __syncthreads();
+    l = (sred[1][0] + sred[1][1]) + (sred[1][2] + sred[1][3]);
+
+    const int d = tid % D, g = tid / D;
+    float acc = 0.0f;
+    for (int t = g; t < nk; t += G) acc = acc + sp[t] * vp[(int64_t)(k0 + t) * D + d];
+    so[g][d] = acc;
+    __syncthreads();
+    if (tid < D) {
+        float o = so[0][tid];
+#pragma unroll
+        for (int gg = 1; gg < G; gg++) o = o + so[gg][tid];
+        const int64_t prow = ((int64_t)b * Hq + h) * nsplit + split;
+        part_o[prow * D + tid] = o;
+        if (tid == 0) part_ml[prow] = make_float2(m, l);
+    }
+}
+
+template <int D, typename OT>
 __global__ __launch_bounds__(D) void k_decode_combine(const float* __restrict__ part_o,
                                                     const float2* __restrict__ part_ml,
                                                     const int32_t* __restrict__ lens, int Hq, int cap, int nsplit,
-                                                    uint16_t* __restrict__ out, float* __restrict__ lse) {
+                                                    OT* __restrict__ out, float* __restrict__ lse) {
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     int len = lens[b];
     len = len < 0 ? 0 : (len > cap ? cap : len);
@@ -879,11 +955,112 @@ __global__ __launch_bounds__(D) void k_decode_combine(const float* __restrict__ 
         tl = tl + ml.y * f;
         acc = acc + part_o[(base + s) * D + d] * f;
     }
-    out[((int64_t)b * Hq + h) * D + d] = bf16_from_f32(acc / tl);
+    if constexpr (sizeof(OT) == 2)
+        out[((int64_t)b * Hq + h) * D + d] = bf16_from_f32(acc / tl);
+    else
+        out[((int64_t)b * Hq + h) * D + d] = acc / tl;
     if (lse && d == 0) lse[(int64_t)b * Hq + h] = mu * LN2 + logf(tl);
 }
 
 const char* OP = "aten._scaled_dot_product_flash_attention_for_cpu.default";
+
+}  // namespace
+
+// Argument checks of the decode attention (shared with the decode step).
+tn_status decode_check(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, int64_t max_len) {
+    if (dtype != TN_BF16 && dtype != TN_F32)
+        return fail(TN_ENOTIMPL, "sdpa_decode: only float32 and bfloat16 KV caches are implemented on the hip device");
+    if (B < 0 || Hq < 0 || Hkv <= 0 || cap <= 0 || D <= 0 || max_len < 1 || max_len > cap)
+        return fail(TN_EINVAL, "sdpa_decode: need Hkv > 0, cap > 0 and 1 <= max_len <= cap");
+    if (Hq % Hkv != 0) {
+        char buf[256];
+        std::snprintf(buf, sizeof buf,
+                      "sdpa_decode: grouped-query attention with %lld query heads and %lld key/value heads -- the "
+                      "head counts do not divide",
+                      (long long)Hq, (long long)Hkv);
+        return fail(TN_ENOTIMPL, buf);
+    }
+    if (D != 64 && D != 128) {
+        char buf[256];
+        std::snprintf(buf, sizeof buf,
+                      "sdpa_decode: head_dim %lld is not implemented on the hip device (kernels exist for 64 and 128)",
+                      (long long)D);
+        return fail(TN_ENOTIMPL, buf);
+    }
+    if (B > 65535 || Hq > 65535 || cap > INT32_MAX) return fail(TN_EVALUE, "sdpa_decode: shape too large");
+    return TN_OK;
+}
+
+// Split-KV decode attention with caller-provided partial buffers (B*Hq*
+// ceil(max_len/256) rows of D floats, and as many (m, l) pairs): the grid is
+// sized by max_len, each workgroup reads its sequence's length on the device,
+// so the launch stays valid for every length up to max_len.
+tn_status decode_launch(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens,
+                        int64_t max_len, double scale, void* out, float* lse, float* part_o, float2* part_ml) {
+    const int nrep = (int)(Hq / Hkv);
+    const int nsplit = (int)cdiv(max_len, DEC_SPLIT);
+    const double sc = std::isnan(scale) ? 1.0 / std::sqrt((double)D) : scale;
+    const float sl2 = (float)sc * LOG2E;
+    if (dtype == TN_F32) {
+        auto qq = static_cast<const float*>(q);
+        auto kk = static_cast<const float*>(k_cache);
+        auto vv = static_cast<const float*>(v_cache);
+        auto oo = static_cast<float*>(out);
+        const dim3 grid((unsigned)nsplit, (unsigned)Hq, (unsigned)B);
+        if (D == 128)
+            hipLaunchKernelGGL(k_decode_f32<128>, grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, nrep,
+                               (int)cap, lens, nsplit, sl2, part_o, part_ml);
+        else
+            hipLaunchKernelGGL(k_decode_f32<64>, grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, nrep,
+                               (int)cap, lens, nsplit, sl2, part_o, part_ml);
+        TN_LAUNCHED();
+        if (D == 128)
+            hipLaunchKernelGGL((k_decode_combine<128, float>), dim3((unsigned)Hq, (unsigned)B), dim3(128), 0, st,
+                               part_o, part_ml, lens, (int)Hq, (int)cap, nsplit, oo, lse);
+        else
+            hipLaunchKernelGGL((k_decode_combine<64, float>), dim3((unsigned)Hq, (unsigned)B), dim3(64), 0, st,
+                               part_o, part_ml, lens, (int)Hq, (int)cap, nsplit, oo, lse);
+        TN_LAUNCHED();
+        return TN_OK;
+    }
+    // query heads per workgroup: the largest of 8, 4, 3, 2, 1 that divides the group
+    const int nr = nrep % 8 == 0 ? 8 : nrep % 4 == 0 ? 4 : nrep % 3 == 0 ? 3 : nrep % 2 == 0 ? 2 : 1;
+    auto qq = static_cast<const uint16_t*>(q);
+    auto kk = static_cast<const uint16_t*>(k_cache);
+    auto vv = static_cast<const uint16_t*>(v_cache);
+    dim3 grid((unsigned)nsplit, (unsigned)(Hkv * (nrep / nr)), (unsigned)B);
+#define TN_DEC(DD, NR)                                                                                            \
+    hipLaunchKernelGGL((k_decode_bf16<DD, NR>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, nrep,      \
+                       (int)cap, lens, nsplit, sl2, part_o, part_ml)
+#define TN_DEC_D(DD)                       \
+    switch (nr) {                          \
+        case 8: TN_DEC(DD, 8); break;      \
+        case 4: TN_DEC(DD, 4); break;      \
+        case 3: TN_DEC(DD, 3); break;      \
+        case 2: TN_DEC(DD, 2); break;      \
+        default: TN_DEC(DD, 1); break;     \
+    }
+    if (D == 128) {
+        TN_DEC_D(128)
+    } else {
+        TN_DEC_D(64)
+    }
+#undef TN_DEC_D
+#undef TN_DEC
+    TN_LAUNCHED();
+    auto oo = static_cast<uint16_t*>(out);
+    if (D == 128)
+        hipLaunchKernelGGL((k_decode_combine<128, uint16_t>), dim3((unsigned)Hq, (unsigned)B), dim3(128), 0, st,
+                           part_o, part_ml, lens, (int)Hq, (int)cap, nsplit, oo, lse);
+    else
+        hipLaunchKernelGGL((k_decode_combine<64, uint16_t>), dim3((unsigned)Hq, (unsigned)B), dim3(64), 0, st,
+                           part_o, part_ml, lens, (int)Hq, (int)cap, nsplit, oo, lse);
+    TN_LAUNCHED();
+    return TN_OK;
+}
+
+namespace {
 
 tn_status refuse_head_dim(int64_t D) {
     char buf[256];
@@ -1105,68 +1282,18 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
 tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_cache, const void* v_cache, int64_t B,
                          int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens, int64_t max_len,
                          double scale, void* out, float* lse) {
-    if (dtype != TN_BF16)
-        return fail(TN_ENOTIMPL, "sdpa_decode: only bfloat16 KV caches are implemented on the hip device");
-    if (B < 0 || Hq < 0 || Hkv <= 0 || cap <= 0 || D <= 0 || max_len < 1 || max_len > cap)
-        return fail(TN_EINVAL, "sdpa_decode: need Hkv > 0, cap > 0 and 1 <= max_len <= cap");
-    if (Hq % Hkv != 0) {
-        char buf[256];
-        std::snprintf(buf, sizeof buf,
-                      "sdpa_decode: grouped-query attention with %lld query heads and %lld key/value heads -- the "
-                      "head counts do not divide",
-                      (long long)Hq, (long long)Hkv);
-        return fail(TN_ENOTIMPL, buf);
-    }
-    if (D != 64 && D != 128) return refuse_head_dim(D);
-    if (B == 0 || Hq == 0) return TN_OK;
+    tn_status s = decode_check(dtype, B, Hq, Hkv, cap, D, max_len);
+    if (s != TN_OK || B == 0 || Hq == 0) return s;
     if (!q || !k_cache || !v_cache || !out || !lens) return fail(TN_EVALUE, "sdpa_decode: null pointer");
-    if (B > 65535 || Hq > 65535 || cap > INT32_MAX) return fail(TN_EVALUE, "sdpa_decode: shape too large");
-    const int nrep = (int)(Hq / Hkv);
-    // query heads per workgroup: the largest of 8, 4, 3, 2, 1 that divides the group
-    const int nr = nrep % 8 == 0 ? 8 : nrep % 4 == 0 ? 4 : nrep % 3 == 0 ? 3 : nrep % 2 == 0 ? 2 : 1;
-    const int nsplit = (int)cdiv(max_len, DEC_SPLIT);
+    const int64_t nsplit = cdiv(max_len, DEC_SPLIT);
     const size_t po = (size_t)B * Hq * nsplit * D * sizeof(float);
     const size_t pm = (size_t)B * Hq * nsplit * sizeof(float2);
     void* ws = nullptr;
     hipStream_t st = (hipStream_t)stream;
-    tn_status s = workspace(st, po + pm, &ws);
+    s = workspace(st, po + pm, &ws);
     if (s != TN_OK) return s;
-    float* part_o = static_cast<float*>(ws);
-    float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + po);
-    const double sc = std::isnan(scale) ? 1.0 / std::sqrt((double)D) : scale;
-    const float sl2 = (float)sc * LOG2E;
-    auto qq = static_cast<const uint16_t*>(q);
-    auto kk = static_cast<const uint16_t*>(k_cache);
-    auto vv = static_cast<const uint16_t*>(v_cache);
-    dim3 grid((unsigned)nsplit, (unsigned)(Hkv * (nrep / nr)), (unsigned)B);
-#define TN_DEC(DD, NR)                                                                                            \
-    hipLaunchKernelGGL((k_decode_bf16<DD, NR>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, nrep,      \
-                       (int)cap, lens, nsplit, sl2, part_o, part_ml)
-#define TN_DEC_D(DD)                       \
-    switch (nr) {                          \
-        case 8: TN_DEC(DD, 8); break;      \
-        case 4: TN_DEC(DD, 4); break;      \
-        case 3: TN_DEC(DD, 3); break;      \
-        case 2: TN_DEC(DD, 2); break;      \
-        default: TN_DEC(DD, 1); break;     \
-    }
-    if (D == 128) {
-        TN_DEC_D(128)
-    } else {
-        TN_DEC_D(64)
-    }
-#undef TN_DEC_D
-#undef TN_DEC
-    TN_LAUNCHED();
-    auto oo = static_cast<uint16_t*>(out);
-    if (D == 128)
-        hipLaunchKernelGGL(k_decode_combine<128>, dim3((unsigned)Hq, (unsigned)B), dim3(128), 0, st, part_o, part_ml,
-                           lens, (int)Hq, (int)cap, nsplit, oo, lse);
-    else
-        hipLaunchKernelGGL(k_decode_combine<64>, dim3((unsigned)Hq, (unsigned)B), dim3(64), 0, st, part_o, part_ml,
-                           lens, (int)Hq, (int)cap, nsplit, oo, lse);
-    TN_LAUNCHED();
-    return TN_OK;
+    return decode_launch(st, dtype, q, k_cache, v_cache, B, Hq, Hkv, cap, D, lens, max_len, scale, out, lse,
+                         static_cast<float*>(ws), reinterpret_cast<float2*>(static_cast<char*>(ws) + po));
 }
 
 }  // extern "C"

@@ -39,6 +39,16 @@ tn_status workspace(hipStream_t stream, size_t bytes, void** out);
 // block, lds).
 tn_status resident_workgroups(const void* kernel, int block, size_t lds, int* out);
 
+// Decode attention (sdpa.hip), shared with the decode step: argument checks,
+// and the launch with caller-provided split partials (B*Hq*ceil(max_len/256)
+// rows of D floats and as many (m, l) pairs). The grid depends on max_len
+// only; each workgroup reads its sequence's length from `lens` on the device.
+tn_status decode_check(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, int64_t max_len);
+tn_status decode_launch(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens,
+                        int64_t max_len, double scale, void* out, float* lse, float* part_o, float2* part_ml);
+constexpr int DECODE_SPLIT_KEYS = 256;  // keys per split of the decode attention
+
 #define TN_HIP(call)                                              \
     do {                                                          \
         hipError_t e_ = (call);                                   \
