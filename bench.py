@@ -215,7 +215,7 @@ def bench_decode(tn, L, steps, warmup, sets=3):
                          "frac": ach / HBM_PEAK_GBS, "traffic": None}}
 
 
-def bench_e2e(tn, L, prompt_len=256, n_new=128, seed=5):
+def bench_e2e(tn, L, prompt_len=256, n_new=128, seed=5, graph=True):
     """greedy decode of the random-init 30-layer q4_0
     Llama (hidden 576, 9/3 heads, MLP 1536, vocab 49152). As the reference's
     bench does (tests/bench/bench_llama_cpp.py:540-569), the prompt yields
@@ -238,19 +238,21 @@ def bench_e2e(tn, L, prompt_len=256, n_new=128, seed=5):
             model.step(st)
         L.check(lib.tn_stream_synchronize(st))
 
+    graph_s = tokens = warm_tokens = None
     try:
-        run_prompt()
-        graph = model.capture(n_new - 1, st)
-        graph.launch(st)  # warm: the first launch uploads the graph
-        L.check(lib.tn_stream_synchronize(st))
-        warm_tokens = model.generated(prompt_len, n_new)
-        run_prompt()
-        t0 = time.perf_counter()
-        graph.launch(st)
-        L.check(lib.tn_stream_synchronize(st))
-        graph_s = time.perf_counter() - t0
-        tokens = model.generated(prompt_len, n_new)
-        graph.close()
+        if graph:
+            run_prompt()
+            g = model.capture(n_new - 1, st)
+            g.launch(st)  # warm: the first launch uploads the graph
+            L.check(lib.tn_stream_synchronize(st))
+            warm_tokens = model.generated(prompt_len, n_new)
+            run_prompt()
+            t0 = time.perf_counter()
+            g.launch(st)
+            L.check(lib.tn_stream_synchronize(st))
+            graph_s = time.perf_counter() - t0
+            tokens = model.generated(prompt_len, n_new)
+            g.close()
         run_prompt()
         t0 = time.perf_counter()
         for _ in range(n_new - 1):
@@ -263,13 +265,14 @@ def bench_e2e(tn, L, prompt_len=256, n_new=128, seed=5):
     weight_bytes = cfg.n_layers * ((cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim * cfg.hidden
                                    + cfg.hidden * cfg.n_heads * cfg.head_dim + 3 * cfg.inter * cfg.hidden)
     weight_bytes = (weight_bytes + cfg.vocab * cfg.hidden) // 32 * 18
-    tps = (n_new - 1) / graph_s
-    return {"tokens_per_s": tps, "ms_per_token": graph_s * 1e3 / (n_new - 1),
+    timed_s = graph_s if graph else eager_s
+    tps = (n_new - 1) / timed_s
+    return {"tokens_per_s": tps, "ms_per_token": timed_s * 1e3 / (n_new - 1), "graph": graph,
             "eager_tokens_per_s": (n_new - 1) / eager_s, "prompt_tokens": prompt_len, "new_tokens": n_new,
             "q4_weight_bytes_per_token": weight_bytes,
             "weight_stream_gbs": weight_bytes * tps / 1e9,
-            "same_tokens_graph_eager_warm": tokens == eager_tokens == warm_tokens,
-            "first_tokens": tokens[:16]}
+            "same_tokens_graph_eager_warm": (tokens == eager_tokens == warm_tokens) if graph else None,
+            "first_tokens": (tokens if graph else eager_tokens)[:16]}
 
 
 def cpu_baseline_sdpa(threads, seconds=10.0):
@@ -345,6 +348,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c3,c4,c5)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="c5: time the decode steps as separate launches only (no HIP graph)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the copy kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
@@ -378,7 +383,7 @@ def main():
         parts["c4_decode_attention"] = bench_decode(tn, L, args.steps, args.warmup)
     if want("c5"):
         print("bench: c5 end-to-end greedy decode", file=sys.stderr, flush=True)
-        parts["c5_e2e_decode"] = bench_e2e(tn, L)
+        parts["c5_e2e_decode"] = bench_e2e(tn, L, graph=not args.no_graph)
     print("bench: c2 SDPA prefill bf16 (headline)", file=sys.stderr, flush=True)
     head = bench_sdpa(tn, L, "bfloat16", args.steps, args.warmup)
     head["roofline"]["traffic"] = profiled_traffic("flash_bf16_c2_traffic.md")

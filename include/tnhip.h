@@ -225,13 +225,34 @@ tn_status tn_argmax(void* stream, const float* x, int64_t m, int64_t n, int32_t*
 tn_status tn_kv_append(void* stream, const float* k, const float* v, int64_t m, int64_t hkv, int64_t d,
                        float* k_cache, float* v_cache, int64_t cap, const int32_t* pos0);
 
+/* One f32 activation row through a q4_0 linear with the decode step's
+ * neighbouring ops fused in, bit-identical to running them separately:
+ *   prologue TN_PRO_NONE     x [k]
+ *            TN_PRO_RMSNORM  x [k] -> tn_rmsnorm(x, prologue_w [k], eps)
+ *            TN_PRO_SILU     x [2k] = gate | up -> tn_silu_mul(gate, up)
+ *   then y [n] = tn_q4_0_linear of that row (no bias),
+ *   then, if resid is non-null, y = tn_add(resid [n], y).
+ * The reference runs these as separate ops (LlamaRMSNorm, the SiLU-gated
+ * MLP and the residual adds of modeling_llama.py around
+ * `_quantized_linear`, quant.rs:286-369); the fusion saves the launches and
+ * the round trips of the intermediate rows. y may alias resid (the decoder's
+ * in-place residual), never x. k must be a multiple of 32, at most 32768. */
+#define TN_PRO_NONE 0
+#define TN_PRO_RMSNORM 1
+#define TN_PRO_SILU 2
+tn_status tn_q4_0_linear_decode(void* stream, const float* x, int64_t k, int prologue, const float* prologue_w,
+                                double eps, const uint8_t* qs, const uint16_t* d, int64_t n, const float* resid,
+                                float* y);
+
 /* ---- greedy decode of a q4_0 Llama-style decoder ----
  * No single reference function: the reference runs this step as
  * transformers' LlamaForCausalLM.forward over its torch._C ops, with every
  * nn.Linear swapped for QuantizedLinear (quant/__init__.py:100-365), then
  * the greedy argmax of generate(). tn_llama_step launches one whole step of
- * that on the device, from the ops above, tn_q4_0_linear and the f32 decode
- * attention, so that a caller (or a captured graph) pays one call per token:
+ * that on the device -- five launches per layer: tn_q4_0_linear_decode with
+ * the norms, SiLU and residual adds fused in, one RoPE + KV-append kernel,
+ * and the f32 decode attention -- so that a caller (or a captured graph)
+ * pays one call per token:
  *   h = embed[token]; per layer: x = rmsnorm(h, ln1); qkv = x W_qkv^T;
  *   rope(q, k at pos); append k, v; a = attention(q, cache[0..pos]);
  *   h += a W_o^T; x = rmsnorm(h, ln2); gu = x W_gate_up^T;

@@ -128,3 +128,16 @@ def test_bf16_host_conversion_is_round_to_nearest_even():
     x = np.concatenate([rng.standard_normal(10000).astype(np.float32),
                         np.array([1.00390625, 1.005859375, np.inf, -np.inf, 0.0, -0.0], np.float32)])
     assert np.array_equal(bf16_bits_from_f32(x), O.bf16_from_f32(x))
+
+
+def test_fused_decode_linear_refusals(L):
+    from torchnative_amd import _lib
+
+    # checked on the host before anything reaches a device
+    st = L.tn_q4_0_linear_decode(None, 4096, 64, 7, None, 0.0, 8192, 8192, 8, None, 16384)
+    assert st == _lib.TN_EINVAL and "unknown prologue" in _lib.last_error()
+    st = L.tn_q4_0_linear_decode(None, 4096, 64, _lib.TN_PRO_RMSNORM, None, 1e-5, 8192, 8192, 8, None, 16384)
+    assert st == _lib.TN_EVALUE and "null pointer" in _lib.last_error()
+    # y overlapping x ([gate | up] is 2k floats under the SiLU prologue)
+    st = L.tn_q4_0_linear_decode(None, 4096, 64, _lib.TN_PRO_SILU, None, 0.0, 8192, 8192, 8, None, 4096 + 4 * 100)
+    assert st == _lib.TN_EINVAL and "overlaps" in _lib.last_error()

@@ -139,7 +139,9 @@ def test_kv_append_writes_at_the_device_position(tn):
     assert not gk[:, :8].any() and not gv[:, :8].any()
 
 
-@pytest.mark.parametrize("D,hq,hkv,lens,cap", [(64, 9, 3, [1, 200, 300], 320), (128, 8, 2, [513, 17], 600)])
+# max_len <= 1024 runs the single-pass kernel, above it the split-KV one
+@pytest.mark.parametrize("D,hq,hkv,lens,cap", [(64, 9, 3, [1, 200, 300], 320), (128, 8, 2, [513, 17], 600),
+                                              (64, 4, 2, [1500, 1, 1025], 1600), (128, 2, 1, [1024, 257], 1024)])
 def test_f32_decode_attention_within_the_derived_bound(tn, D, hq, hkv, lens, cap):
     L = _lib()
     B = len(lens)
@@ -163,10 +165,61 @@ def test_f32_decode_attention_within_the_derived_bound(tn, D, hq, hkv, lens, cap
         _within(gl[b][None, :, None], l32.astype(np.float64), l64)
 
 
+@pytest.mark.parametrize("k,n", [(576, 960), (1536, 576), (64, 3), (2304, 70)])
+def test_fused_decode_linear_equals_the_separate_ops(tn, k, n):
+    """tn_q4_0_linear_decode against tn_rmsnorm / tn_silu_mul, then
+    tn_q4_0_linear, then tn_add: bit for bit, including y aliasing the
+    residual. k = 2304 takes two batches of the activation loads."""
+    from torchnative_amd import _C
+
+    L = _lib()
+    f = L.lib()
+    rng = np.random.default_rng(k * 7 + n)
+    w = _dev(tn, (rng.standard_normal((n, k)) * 0.05).astype(np.float32))
+    q = _C._quantize(w, "q4_0")
+    qs, d = q._qs.data_ptr(), q._d.data_ptr()
+    x = _dev(tn, (rng.standard_normal(2 * k) * 2).astype(np.float32))
+    g = _dev(tn, rng.standard_normal(k).astype(np.float32))
+    res = rng.standard_normal(n).astype(np.float32)
+    d_res = _dev(tn, res)
+    t = tn.empty((k,), "float32", "hip")
+    ref, got = tn.empty((n,), "float32", "hip"), tn.empty((n,), "float32", "hip")
+
+    def lin(src, out):
+        L.check(f.tn_q4_0_linear(None, src, L.TN_F32, 1, k, qs, d, n, None, out.data_ptr(), L.TN_F32))
+
+    L.check(f.tn_rmsnorm(None, x.data_ptr(), 1, k, g.data_ptr(), 1e-5, t.data_ptr()))
+    lin(t.data_ptr(), ref)
+    L.check(f.tn_q4_0_linear_decode(None, x.data_ptr(), k, L.TN_PRO_RMSNORM, g.data_ptr(), 1e-5, qs, d, n, None,
+                                    got.data_ptr()))
+    assert np.array_equal(got.numpy(), ref.numpy())
+
+    L.check(f.tn_silu_mul(None, x.data_ptr(), x.data_ptr() + 4 * k, k, t.data_ptr()))
+    lin(t.data_ptr(), ref)
+    L.check(f.tn_q4_0_linear_decode(None, x.data_ptr(), k, L.TN_PRO_SILU, None, 0.0, qs, d, n, None,
+                                    got.data_ptr()))
+    assert np.array_equal(got.numpy(), ref.numpy())
+
+    # residual epilogue, in place on the residual (the decoder's h += ...)
+    lin(x.data_ptr(), ref)
+    L.check(f.tn_add(None, d_res.data_ptr(), ref.data_ptr(), n, ref.data_ptr()))
+    L.check(f.tn_q4_0_linear_decode(None, x.data_ptr(), k, L.TN_PRO_NONE, None, 0.0, qs, d, n, d_res.data_ptr(),
+                                    d_res.data_ptr()))
+    assert np.array_equal(d_res.numpy(), ref.numpy())
+    # and the plain row equals tn_q4_0_linear
+    lin(x.data_ptr(), ref)
+    L.check(f.tn_q4_0_linear_decode(None, x.data_ptr(), k, L.TN_PRO_NONE, None, 0.0, qs, d, n, None,
+                                    got.data_ptr()))
+    assert np.array_equal(got.numpy(), ref.numpy())
+
+
 SMALL = OD.LlamaConfig(n_layers=2, hidden=128, n_heads=2, n_kv_heads=1, head_dim=64, inter=256, vocab=512)
 
 
-def test_decode_step_matches_the_oracle_teacher_forced(tn):
+# cap 24: the fused split attention merged in the o projection; cap 600 (more
+# than 8 splits of 64 keys): RoPE + append, split-KV attention and its combine
+@pytest.mark.parametrize("cap", [24, 600])
+def test_decode_step_matches_the_oracle_teacher_forced(tn, cap):
     """A 2-layer model: the GPU's logits at every step within the bound of the
     oracle's float32 run on the same tokens, and its greedy token the
     oracle's wherever the oracle's top two logits are further apart than
@@ -174,7 +227,7 @@ def test_decode_step_matches_the_oracle_teacher_forced(tn):
     from torchnative_amd.decoder import Q4Llama
 
     prompt = [5, 77, 300, 12, 511, 0, 42, 9, 100, 250, 3, 64]
-    n_new, cap = 8, 24
+    n_new = 8
     model = Q4Llama(SMALL, seed=11, cap=cap)
     ref32 = OD.Decoder(SMALL, 11, cap, np.float32)
     ref64 = OD.Decoder(SMALL, 11, cap, np.float64)

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libtnhip.so")
 
 TN_OK, TN_EINVAL, TN_ENOTIMPL, TN_EHIP, TN_EVALUE = 0, 1, 2, 3, 4
 TN_F32, TN_BF16, TN_F16, TN_F64 = 0, 1, 2, 3
+TN_PRO_NONE, TN_PRO_RMSNORM, TN_PRO_SILU = 0, 1, 2
 
 # every symbol include/tnhip.h declares, with (restype, argtypes)
 _P, _I64, _I, _D, _SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double, ctypes.c_size_t
@@ -86,6 +87,7 @@ SIGNATURES = {
     "tn_q4_0_quantize": (_I, [_P, _P, _I64, _I64, _P, _P]),
     "tn_q4_0_dequantize": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "tn_q4_0_linear": (_I, [_P, _P, _I, _I64, _I64, _P, _P, _I64, _P, _P, _I]),
+    "tn_q4_0_linear_decode": (_I, [_P, _P, _I64, _I, _P, _D, _P, _P, _I64, _P, _P]),
     "tn_sdpa_fwd": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I, _I, _D, _P, _P]),
     "tn_sdpa_decode": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _D, _P, _P]),
     "tn_embedding": (_I, [_P, _P, _I64, _P, _I64, _I64, _P]),

@@ -27,29 +27,24 @@ __global__ __launch_bounds__(256) void k_embedding(const int32_t* __restrict__ i
     out[(int64_t)i * dim + c] = (id >= 0 && id < vocab) ? table[(int64_t)id * dim + c] : NAN;
 }
 
-// sum over the 256 threads of a workgroup, in a fixed order
-__device__ inline float block_sum256(float v, float* red) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
-
+// thread t adds the squares of elements 1024p + 4t .. 1024p + 4t + 3, p =
+// 0, 1, ..., in order, then block_sum256: the order the q4_0 GEMV's fused
+// RMSNorm prologue reproduces
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, int n, const float* __restrict__ w, float eps,
                                                  float* y) {
     __shared__ float red[4];
     const float* xr = x + (int64_t)blockIdx.x * n;
     float* yr = y + (int64_t)blockIdx.x * n;
     float ss = 0.0f;
-    for (int c = threadIdx.x; c < n; c += 256) {
-        const float v = xr[c];
-        ss = ss + v * v;
+    for (int64_t c0 = threadIdx.x * 4; c0 < n; c0 += 1024) {
+        const int64_t ce = c0 + 4 < n ? c0 + 4 : n;
+        for (int64_t c = c0; c < ce; c++) {
+            const float v = xr[c];
+            ss = ss + v * v;
+        }
     }
     // every read of the row precedes the barrier inside, so y may alias x
-    const float var = block_sum256(ss, red) / (float)n;
-    const float r = 1.0f / sqrtf(var + eps);
+    const float r = rms_scale(block_sum256(ss, red), n, eps);
     for (int c = threadIdx.x; c < n; c += 256) yr[c] = w[c] * (xr[c] * r);
 }
 
@@ -63,6 +58,202 @@ __global__ void k_rope(float* __restrict__ x, int heads, int d, const float* __r
     const float x1 = xr[i], x2 = xr[i + half];
     xr[i] = x1 * c + (-x2) * s;
     xr[i + half] = x2 * c + x1 * s;
+}
+
+// The decode step's RoPE and KV-cache append in one launch, d/2 threads per
+// row of the token's qkv vector [hq + 2 hkv][d]: q rows are rotated in place,
+// k rows are rotated into the k cache at the device position, v rows are
+// copied into the v cache. The rotation is k_rope's, bit for bit.
+__global__ void k_rope_append(float* __restrict__ qkv, int hq, int hkv, int d, const float* __restrict__ inv_freq,
+                              const int32_t* __restrict__ pos, float* __restrict__ kc, float* __restrict__ vc,
+                              int cap) {
+    const int row = blockIdx.x, i = threadIdx.x, half = d / 2;
+    const int p = pos[0];
+    float* xr = qkv + (int64_t)row * d;
+    if (row >= hq + hkv) {
+        if (p < 0 || p >= cap) return;
+        float* dst = vc + ((int64_t)(row - hq - hkv) * cap + p) * d;
+        dst[i] = xr[i];
+        dst[i + half] = xr[i + half];
+        return;
+    }
+    const float f = (float)p * inv_freq[i];
+    const float c = cosf(f), s = sinf(f);
+    const float x1 = xr[i], x2 = xr[i + half];
+    const float y1 = x1 * c + (-x2) * s, y2 = x2 * c + x1 * s;
+    if (row < hq) {
+        xr[i] = y1;
+        xr[i + half] = y2;
+        return;
+    }
+    if (p < 0 || p >= cap) return;
+    float* dst = kc + ((int64_t)(row - hq) * cap + p) * d;
+    dst[i] = y1;
+    dst[i + half] = y2;
+}
+
+// The decode step's attention for caches of at most STEP_MAX_SPLITS splits of
+// STEP_SPLIT keys, with the step's RoPE and KV append folded in. One
+// workgroup per (split, kv head) covers the NR query heads that share the kv
+// head: it rotates their queries (into LDS) and, in the split that holds the
+// new position, rotates the new key, writes it and the new value to the
+// caches and uses them for that row (other rows come from the caches). D/4
+// lanes share a row, a float4 each, all of the split's K and V rows in flight
+// at once; row dot products reduce with DPP. Each split writes an (O, m, l)
+// partial per query head (m in log2 units), merged by the o projection's
+// PRO_COMBINE prologue. The rotation is k_rope's, bit for bit.
+constexpr float STEP_LOG2E = 1.4426950408889634f;
+
+template <int D, int NR>
+__global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv, int hq, int hkv,
+                                                  const float* __restrict__ inv_freq,
+                                                  const int32_t* __restrict__ state, float* __restrict__ kc,
+                                                  float* __restrict__ vc, int cap, float sl2, int nsplit,
+                                                  float* __restrict__ part_o, float2* __restrict__ part_ml) {
+    constexpr int TPK = D / 4;             // lanes per row
+    constexpr int SLOTS = 256 / TPK;       // rows per load instruction of the workgroup
+    constexpr int U = STEP_SPLIT / SLOTS;  // rows per lane
+    static_assert(U * SLOTS == STEP_SPLIT && (TPK == 16 || TPK == 32), "shape");
+    __shared__ __align__(16) float sq[NR][D];
+    __shared__ __align__(16) float snew[2][D];  // the new key (rotated) and value
+    __shared__ float smax[NR][4], ssum[NR][4];
+    __shared__ float4 so[4][NR][TPK];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int c = tid % TPK, kl = tid / TPK;
+    const int sp = blockIdx.x, kvh = blockIdx.y;
+    const int pos = state[0];
+    const int len = pos < 0 ? 0 : (pos + 1 < cap ? pos + 1 : cap);
+    const int k0 = sp * STEP_SPLIT;
+    if (k0 >= len) return;  // uniform over the workgroup
+    const int ncached = pos < len ? pos : len;  // rows read from the caches
+    const bool fresh = pos >= k0 && pos < k0 + STEP_SPLIT && pos < len;
+    const int half = D / 2;
+
+    // the split's cached rows: every load in flight before the rotations
+    const float4* kp = reinterpret_cast<const float4*>(kc + (int64_t)kvh * cap * D);
+    const float4* vp = reinterpret_cast<const float4*>(vc + (int64_t)kvh * cap * D);
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 kr[U], vr[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int t = k0 + u * SLOTS + kl;
+        kr[u] = t < ncached ? kp[(int64_t)t * TPK + c] : zero;
+        vr[u] = t < ncached ? vp[(int64_t)t * TPK + c] : zero;
+    }
+    for (int i = tid; i < NR * half; i += 256) {
+        const int hh = i / half, j = i - hh * half;
+        const float* xr = qkv + (int64_t)(kvh * NR + hh) * D;
+        const float f = (float)pos * inv_freq[j];
+        const float cs = cosf(f), sn = sinf(f);
+        const float x1 = xr[j], x2 = xr[j + half];
+        sq[hh][j] = x1 * cs + (-x2) * sn;
+        sq[hh][j + half] = x2 * cs + x1 * sn;
+    }
+    if (fresh && tid < half) {
+        const float* xk = qkv + (int64_t)(hq + kvh) * D;
+        const float* xv = qkv + (int64_t)(hq + hkv + kvh) * D;
+        const float f = (float)pos * inv_freq[tid];
+        const float cs = cosf(f), sn = sinf(f);
+        const float x1 = xk[tid], x2 = xk[tid + half];
+        const float y1 = x1 * cs + (-x2) * sn, y2 = x2 * cs + x1 * sn;
+        const float v1 = xv[tid], v2 = xv[tid + half];
+        snew[0][tid] = y1;
+        snew[0][tid + half] = y2;
+        snew[1][tid] = v1;
+        snew[1][tid + half] = v2;
+        float* kd = kc + ((int64_t)kvh * cap + pos) * D;
+        float* vd = vc + ((int64_t)kvh * cap + pos) * D;
+        kd[tid] = y1;
+        kd[tid + half] = y2;
+        vd[tid] = v1;
+        vd[tid + half] = v2;
+    }
+    __syncthreads();
+    if (fresh) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (k0 + u * SLOTS + kl == pos) {
+                kr[u] = reinterpret_cast<const float4*>(snew[0])[c];
+                vr[u] = reinterpret_cast<const float4*>(snew[1])[c];
+            }
+        }
+    }
+    float4 qv[NR];
+#pragma unroll
+    for (int hh = 0; hh < NR; hh++) qv[hh] = reinterpret_cast<const float4*>(sq[hh])[c];
+
+    // scores (log2 units), then the split's max per head
+    float sc[NR][U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const bool valid = k0 + u * SLOTS + kl < len;
+#pragma unroll
+        for (int hh = 0; hh < NR; hh++) {
+            float d = qv[hh].x * kr[u].x;
+            d = d + qv[hh].y * kr[u].y;
+            d = d + qv[hh].z * kr[u].z;
+            d = d + qv[hh].w * kr[u].w;
+            d = row16_sum(d);
+            if constexpr (TPK == 32) d = d + __shfl_xor(d, 16);
+            sc[hh][u] = valid ? d * sl2 : -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < NR; hh++) {
+        float m = sc[hh][0];
+#pragma unroll
+        for (int u = 1; u < U; u++) m = fmaxf(m, sc[hh][u]);
+#pragma unroll
+        for (int off = TPK; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if (lane == 0) smax[hh][w] = m;
+    }
+    __syncthreads();
+    float4 acc[NR];
+#pragma unroll
+    for (int hh = 0; hh < NR; hh++) {
+        const float m = fmaxf(fmaxf(smax[hh][0], smax[hh][1]), fmaxf(smax[hh][2], smax[hh][3]));
+        const float mu = (m == -INFINITY) ? 0.0f : m;
+        float l = 0.0f;
+        acc[hh] = zero;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float p = exp2f(sc[hh][u] - mu);  // 0 past the end
+            l = l + p;
+            acc[hh].x = acc[hh].x + p * vr[u].x;
+            acc[hh].y = acc[hh].y + p * vr[u].y;
+            acc[hh].z = acc[hh].z + p * vr[u].z;
+            acc[hh].w = acc[hh].w + p * vr[u].w;
+        }
+        // over the wave's row slots (lanes c, c + TPK, ...)
+#pragma unroll
+        for (int off = TPK; off < 64; off <<= 1) {
+            l = l + __shfl_xor(l, off);
+            acc[hh].x = acc[hh].x + __shfl_xor(acc[hh].x, off);
+            acc[hh].y = acc[hh].y + __shfl_xor(acc[hh].y, off);
+            acc[hh].z = acc[hh].z + __shfl_xor(acc[hh].z, off);
+            acc[hh].w = acc[hh].w + __shfl_xor(acc[hh].w, off);
+        }
+        if (lane == 0) ssum[hh][w] = l;
+        if (lane < TPK) so[w][hh][lane] = acc[hh];
+    }
+    __syncthreads();
+    for (int i = tid; i < NR * TPK; i += 256) {
+        const int hh = i / TPK, cc = i - hh * TPK;
+        float4 o = so[0][hh][cc];
+#pragma unroll
+        for (int ww = 1; ww < 4; ww++) {
+            o.x = o.x + so[ww][hh][cc].x;
+            o.y = o.y + so[ww][hh][cc].y;
+            o.z = o.z + so[ww][hh][cc].z;
+            o.w = o.w + so[ww][hh][cc].w;
+        }
+        const int64_t prow = (int64_t)(kvh * NR + hh) * nsplit + sp;
+        reinterpret_cast<float4*>(part_o + prow * D)[cc] = o;
+        if (cc == 0) {
+            const float m = fmaxf(fmaxf(smax[hh][0], smax[hh][1]), fmaxf(smax[hh][2], smax[hh][3]));
+            part_ml[prow] = make_float2(m, (ssum[hh][0] + ssum[hh][1]) + (ssum[hh][2] + ssum[hh][3]));
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void k_silu_mul(const float* gate, const float* up, int64_t n, float* out) {
@@ -85,33 +276,116 @@ __device__ inline bool arg_before(float v, int i, float w, int j) {
     return v > w || (v == w && i < j);
 }
 
-__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, int32_t* __restrict__ out) {
-    __shared__ float sv[1024];
-    __shared__ int si[1024];
+constexpr int ARGMAX_THREADS = 1024;
+constexpr int ARGMAX_U = 12;  // loads in flight per thread (49152 f32 = one batch of float4s)
+
+// end of a decode step: advance the position, pick the next input token
+__device__ inline void llama_advance(int32_t* state, int32_t* tokens, const int32_t* prompt, int prompt_len,
+                                     int cap) {
+    const int pos = state[0] + 1;
+    const int next = pos < prompt_len ? prompt[pos] : state[3];
+    if (pos < cap) tokens[pos] = next;
+    state[0] = pos;
+    state[1] = pos + 1;
+    state[2] = next;
+}
+
+// One workgroup per row. arg_before is a strict total order on (value,
+// index) pairs, so the winner does not depend on how the pairs are reduced:
+// each thread scans its elements with ARGMAX_U loads in flight (16-byte
+// pieces when VEC4: rows 16-byte aligned, n % 4 == 0), then waves reduce by
+// shuffles and wave 0 merges the 16 waves.
+// ADVANCE (one row): the winner goes to state[3] and the decode step's
+// position advances.
+template <bool ADVANCE, bool VEC4>
+__global__ __launch_bounds__(ARGMAX_THREADS) void k_argmax(const float* __restrict__ x, int n,
+                                                          int32_t* __restrict__ out, int32_t* state,
+                                                          int32_t* tokens, const int32_t* prompt, int prompt_len,
+                                                          int cap) {
+    __shared__ float sv[ARGMAX_THREADS / 64];
+    __shared__ int si[ARGMAX_THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const float* xr = x + (int64_t)blockIdx.x * n;
     float bv = -INFINITY;
     int bi = n;  // loses every tie against a real element
-    for (int c = threadIdx.x; c < n; c += 1024) {
-        const float v = xr[c];
+    auto take = [&](float v, int c) {
         if (arg_before(v, c, bv, bi)) {
             bv = v;
             bi = c;
         }
-    }
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int half = 512; half >= 1; half >>= 1) {
-        if ((int)threadIdx.x < half) {
-            const int o = threadIdx.x + half;
-            if (arg_before(sv[o], si[o], sv[threadIdx.x], si[threadIdx.x])) {
-                sv[threadIdx.x] = sv[o];
-                si[threadIdx.x] = si[o];
+    };
+    if (VEC4) {
+        // the row in 16-byte pieces, ARGMAX_U pieces per thread in flight
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+        const int n4 = n / 4;
+        for (int c0 = tid; c0 < n4; c0 += ARGMAX_THREADS * ARGMAX_U) {
+            float4 v[ARGMAX_U];
+#pragma unroll
+            for (int u = 0; u < ARGMAX_U; u++) {
+                const int c = c0 + u * ARGMAX_THREADS;
+                v[u] = c < n4 ? x4[c] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            }
+#pragma unroll
+            for (int u = 0; u < ARGMAX_U; u++) {
+                const int c = c0 + u * ARGMAX_THREADS;
+                if (c < n4) {
+                    take(v[u].x, 4 * c);
+                    take(v[u].y, 4 * c + 1);
+                    take(v[u].z, 4 * c + 2);
+                    take(v[u].w, 4 * c + 3);
+                }
             }
         }
-        __syncthreads();
+    } else {
+        for (int c0 = tid; c0 < n; c0 += ARGMAX_THREADS * ARGMAX_U) {
+            float v[ARGMAX_U];
+#pragma unroll
+            for (int u = 0; u < ARGMAX_U; u++) {
+                const int c = c0 + u * ARGMAX_THREADS;
+                v[u] = c < n ? xr[c] : -INFINITY;
+            }
+#pragma unroll
+            for (int u = 0; u < ARGMAX_U; u++) {
+                const int c = c0 + u * ARGMAX_THREADS;
+                if (c < n) take(v[u], c);
+            }
+        }
     }
-    if (threadIdx.x == 0) out[blockIdx.x] = si[0] < n ? si[0] : 0;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (arg_before(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        sv[w] = bv;
+        si[w] = bi;
+    }
+    __syncthreads();
+    if (w != 0) return;
+    constexpr int NW = ARGMAX_THREADS / 64;
+    bv = lane < NW ? sv[lane] : -INFINITY;
+    bi = lane < NW ? si[lane] : n;
+#pragma unroll
+    for (int off = NW / 2; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (arg_before(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane != 0) return;
+    const int idx = bi < n ? bi : 0;
+    if (ADVANCE) {
+        state[3] = idx;
+        llama_advance(state, tokens, prompt, prompt_len, cap);
+    } else {
+        out[blockIdx.x] = idx;
+    }
 }
 
 // one workgroup of d threads per (row, kv head)
@@ -126,27 +400,17 @@ __global__ void k_kv_append(const float* __restrict__ k, const float* __restrict
     vc[dst] = v[src];
 }
 
-// end of a decode step: advance the position, pick the next input token
-__global__ void k_llama_advance(int32_t* state, int32_t* tokens, const int32_t* prompt, int prompt_len, int cap) {
-    if (threadIdx.x != 0) return;
-    const int pos = state[0] + 1;
-    const int next = pos < prompt_len ? prompt[pos] : state[3];
-    if (pos < cap) tokens[pos] = next;
-    state[0] = pos;
-    state[1] = pos + 1;
-    state[2] = next;
-}
-
 }  // namespace
 
 // scratch layout of a decode step, in floats
 struct LlamaWork {
-    int64_t h, x, qkv, attn, tmp, gu, part_o, part_ml, total;
+    int64_t h, qkv, attn, gu, part_o, part_ml, total;
 };
 
 static LlamaWork llama_work(const tn_llama* m) {
     LlamaWork w;
-    const int64_t nsplit = cdiv(m->cap, DECODE_SPLIT_KEYS);
+    // partials of either attention path: splits of DECODE_SPLIT_KEYS or of STEP_SPLIT keys
+    const int64_t nsplit = std::max(cdiv(m->cap, DECODE_SPLIT_KEYS), cdiv(m->cap, STEP_SPLIT));
     const int64_t qkv = (m->n_heads + 2 * m->n_kv_heads) * m->head_dim;
     int64_t o = 0;
     auto take = [&](int64_t n) {
@@ -155,10 +419,8 @@ static LlamaWork llama_work(const tn_llama* m) {
         return at;
     };
     w.h = take(m->hidden);
-    w.x = take(std::max(m->hidden, m->inter));
     w.qkv = take(qkv);
     w.attn = take(m->n_heads * m->head_dim);
-    w.tmp = take(m->hidden);
     w.gu = take(2 * m->inter);
     w.part_o = take(m->n_heads * nsplit * m->head_dim);
     w.part_ml = take(m->n_heads * nsplit * 2);
@@ -177,8 +439,10 @@ static tn_status check_model(const tn_llama* m) {
         return fail(TN_ENOTIMPL, "tn_llama: n_heads * head_dim must equal hidden");
     if (m->head_dim % 2 != 0 || m->head_dim > 1024)
         return fail(TN_ENOTIMPL, "tn_llama: head_dim must be even and at most 1024");
-    if (m->hidden > INT32_MAX || m->inter > INT32_MAX || m->vocab > INT32_MAX || m->cap > INT32_MAX)
+    if (m->vocab > INT32_MAX - ARGMAX_THREADS * ARGMAX_U || m->cap > INT32_MAX)
         return fail(TN_EVALUE, "tn_llama: shape too large");
+    if (m->hidden % 32 != 0 || m->inter % 32 != 0 || m->hidden > LINEAR_DECODE_MAX_K || m->inter > LINEAR_DECODE_MAX_K)
+        return fail(TN_ENOTIMPL, "tn_llama: hidden and inter must be multiples of 32 and at most 32768");
     for (int64_t l = 0; l < m->n_layers; l++) {
         const tn_llama_layer& L = m->layers[l];
         if (!L.qkv.qs || !L.qkv.d || !L.o.qs || !L.o.d || !L.gate_up.qs || !L.gate_up.d || !L.down.qs ||
@@ -253,8 +517,14 @@ tn_status tn_argmax(void* stream, const float* x, int64_t m, int64_t n, int32_t*
     if (m < 0 || n < 1) return fail(TN_EINVAL, "aten.argmax.default: bad sizes");
     if (m == 0) return TN_OK;
     if (!x || !out) return fail(TN_EVALUE, "aten.argmax.default: null pointer");
-    if (m > INT32_MAX || n > INT32_MAX - 1024) return fail(TN_EVALUE, "aten.argmax.default: shape too large");
-    hipLaunchKernelGGL(k_argmax, dim3((unsigned)m), dim3(1024), 0, (hipStream_t)stream, x, (int)n, out);
+    if (m > INT32_MAX || n > INT32_MAX - ARGMAX_THREADS * ARGMAX_U)
+        return fail(TN_EVALUE, "aten.argmax.default: shape too large");
+    if (n % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0)
+        hipLaunchKernelGGL((k_argmax<false, true>), dim3((unsigned)m), dim3(ARGMAX_THREADS), 0, (hipStream_t)stream,
+                           x, (int)n, out, nullptr, nullptr, nullptr, 0, 0);
+    else
+        hipLaunchKernelGGL((k_argmax<false, false>), dim3((unsigned)m), dim3(ARGMAX_THREADS), 0, (hipStream_t)stream,
+                           x, (int)n, out, nullptr, nullptr, nullptr, 0, 0);
     TN_LAUNCHED();
     return TN_OK;
 }
@@ -277,21 +547,32 @@ int64_t tn_llama_work_floats(const tn_llama* model) {
     return llama_work(model).total;
 }
 
+// One decode step. Per layer, for a cache of at most STEP_MAX_SPLITS *
+// STEP_SPLIT keys (four launches):
+//   qkv = Q4(rmsnorm(h, ln1))                    linear_decode, RMSNorm prologue
+//   rope q, k; append k, v; split attention      k_step_attn -> partials
+//   h = h + Q4(merge(partials))                  linear_decode, PRO_COMBINE, residual
+//   gu = Q4(rmsnorm(h, ln2))                     linear_decode, RMSNorm prologue
+//   h = h + Q4(silu(gate) * up)                  linear_decode, SiLU prologue
+// A longer cache replaces the middle two by k_rope_append, the split-KV decode
+// attention with its combine, and the o projection on its output.
+// Then logits = Q4(rmsnorm(h, norm)) and the argmax that advances the state.
+// The fused linears are bit-identical to the separate ops (tn_rmsnorm,
+// tn_q4_0_linear, tn_add, tn_silu_mul); RoPE is tn_rope's arithmetic.
 tn_status tn_llama_step(void* stream, const tn_llama* m) {
     tn_status s = check_model(m);
     if (s != TN_OK) return s;
     hipStream_t st = (hipStream_t)stream;
     const LlamaWork w = llama_work(m);
     float* h = m->work + w.h;
-    float* x = m->work + w.x;
     float* qkv = m->work + w.qkv;
     float* attn = m->work + w.attn;
-    float* tmp = m->work + w.tmp;
     float* gu = m->work + w.gu;
     float* part_o = m->work + w.part_o;
     float2* part_ml = reinterpret_cast<float2*>(m->work + w.part_ml);
     const int64_t H = m->hidden, D = m->head_dim, Hq = m->n_heads, Hkv = m->n_kv_heads, I = m->inter;
     const int64_t nqkv = (Hq + 2 * Hkv) * D;
+    const float eps = (float)m->eps;
     int32_t* pos = m->state;      // [0]: position of this token
     int32_t* len = m->state + 1;  // [1]: KV length after appending it
     int32_t* tok = m->state + 2;  // [2]: this token
@@ -301,28 +582,67 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
         tn_status e_ = (call);         \
         if (e_ != TN_OK) return e_;    \
     } while (0)
+    GemvPro none, ln1, ln2, fin, comb;
+    ln1.eps = ln2.eps = fin.eps = eps;
+    fin.w = m->norm;
+    // short caches: the fused split attention, merged in the o projection
+    const int nrep = (int)(Hq / Hkv);
+    const int64_t nsplit_step = cdiv(m->cap, STEP_SPLIT);
+    const bool fused = nsplit_step <= STEP_MAX_SPLITS && (D == 64 || D == 128) &&
+                       (nrep == 1 || nrep == 2 || nrep == 3 || nrep == 4 || nrep == 8);
+    comb.part_o = part_o;
+    comb.part_ml = part_ml;
+    comb.len = len;
+    comb.nsplit = (int)nsplit_step;
+    comb.head_dim = (int)D;
+    comb.cap = (int)m->cap;
+    const float sl2 = (float)(1.0 / std::sqrt((double)D)) * STEP_LOG2E;
     TN_TRY(tn_embedding(st, tok, 1, m->embed, m->vocab, H, h));
     for (int64_t l = 0; l < m->n_layers; l++) {
         const tn_llama_layer& L = m->layers[l];
-        TN_TRY(tn_rmsnorm(st, h, 1, H, L.ln1, m->eps, x));
-        TN_TRY(tn_q4_0_linear(st, x, TN_F32, 1, H, L.qkv.qs, L.qkv.d, nqkv, nullptr, qkv, TN_F32));
-        TN_TRY(tn_rope(st, qkv, 1, Hq + Hkv, D, m->inv_freq, pos));  // q heads, then k heads
-        TN_TRY(tn_kv_append(st, qkv + Hq * D, qkv + (Hq + Hkv) * D, 1, Hkv, D, L.k_cache, L.v_cache, m->cap, pos));
-        TN_TRY(decode_launch(st, TN_F32, qkv, L.k_cache, L.v_cache, 1, Hq, Hkv, m->cap, D, len, m->cap, nan, attn,
-                             nullptr, part_o, part_ml));
-        TN_TRY(tn_q4_0_linear(st, attn, TN_F32, 1, Hq * D, L.o.qs, L.o.d, H, nullptr, tmp, TN_F32));
-        TN_TRY(tn_add(st, h, tmp, H, h));
-        TN_TRY(tn_rmsnorm(st, h, 1, H, L.ln2, m->eps, x));
-        TN_TRY(tn_q4_0_linear(st, x, TN_F32, 1, H, L.gate_up.qs, L.gate_up.d, 2 * I, nullptr, gu, TN_F32));
-        TN_TRY(tn_silu_mul(st, gu, gu + I, I, x));
-        TN_TRY(tn_q4_0_linear(st, x, TN_F32, 1, I, L.down.qs, L.down.d, H, nullptr, tmp, TN_F32));
-        TN_TRY(tn_add(st, h, tmp, H, h));
+        ln1.w = L.ln1;
+        ln2.w = L.ln2;
+        TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, ln1, L.qkv.qs, L.qkv.d, nqkv, nullptr, qkv));
+        if (fused) {
+            const dim3 grid((unsigned)nsplit_step, (unsigned)Hkv);
+#define TN_STEP_ATTN(DD, NR)                                                                                  \
+    hipLaunchKernelGGL((k_step_attn<DD, NR>), grid, dim3(256), 0, st, qkv, (int)Hq, (int)Hkv, m->inv_freq, pos, \
+                       L.k_cache, L.v_cache, (int)m->cap, sl2, (int)nsplit_step, part_o, part_ml)
+#define TN_STEP_ATTN_D(DD)                    \
+    switch (nrep) {                           \
+        case 1: TN_STEP_ATTN(DD, 1); break;   \
+        case 2: TN_STEP_ATTN(DD, 2); break;   \
+        case 3: TN_STEP_ATTN(DD, 3); break;   \
+        case 4: TN_STEP_ATTN(DD, 4); break;   \
+        default: TN_STEP_ATTN(DD, 8); break;  \
     }
-    TN_TRY(tn_rmsnorm(st, h, 1, H, m->norm, m->eps, x));
-    TN_TRY(tn_q4_0_linear(st, x, TN_F32, 1, H, m->lm_head.qs, m->lm_head.d, m->vocab, nullptr, m->logits, TN_F32));
-    TN_TRY(tn_argmax(st, m->logits, 1, m->vocab, m->state + 3));
-    hipLaunchKernelGGL(k_llama_advance, dim3(1), dim3(64), 0, st, m->state, m->tokens, m->prompt,
-                       (int)m->prompt_len, (int)m->cap);
+            if (D == 64) {
+                TN_STEP_ATTN_D(64)
+            } else {
+                TN_STEP_ATTN_D(128)
+            }
+#undef TN_STEP_ATTN_D
+#undef TN_STEP_ATTN
+            TN_LAUNCHED();
+            TN_TRY(linear_decode(st, nullptr, Hq * D, PRO_COMBINE, comb, L.o.qs, L.o.d, H, h, h));
+        } else {
+            hipLaunchKernelGGL(k_rope_append, dim3((unsigned)(Hq + 2 * Hkv)), dim3((unsigned)(D / 2)), 0, st, qkv,
+                               (int)Hq, (int)Hkv, (int)D, m->inv_freq, pos, L.k_cache, L.v_cache, (int)m->cap);
+            TN_LAUNCHED();
+            TN_TRY(decode_launch(st, TN_F32, qkv, L.k_cache, L.v_cache, 1, Hq, Hkv, m->cap, D, len, m->cap, nan,
+                                 attn, nullptr, part_o, part_ml));
+            TN_TRY(linear_decode(st, attn, Hq * D, PRO_NONE, none, L.o.qs, L.o.d, H, h, h));
+        }
+        TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, ln2, L.gate_up.qs, L.gate_up.d, 2 * I, nullptr, gu));
+        TN_TRY(linear_decode(st, gu, I, PRO_SILU, none, L.down.qs, L.down.d, H, h, h));
+    }
+    TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, fin, m->lm_head.qs, m->lm_head.d, m->vocab, nullptr, m->logits));
+    if (m->vocab % 4 == 0 && reinterpret_cast<uintptr_t>(m->logits) % 16 == 0)
+        hipLaunchKernelGGL((k_argmax<true, true>), dim3(1), dim3(ARGMAX_THREADS), 0, st, m->logits, (int)m->vocab,
+                           nullptr, m->state, m->tokens, m->prompt, (int)m->prompt_len, (int)m->cap);
+    else
+        hipLaunchKernelGGL((k_argmax<true, false>), dim3(1), dim3(ARGMAX_THREADS), 0, st, m->logits, (int)m->vocab,
+                           nullptr, m->state, m->tokens, m->prompt, (int)m->prompt_len, (int)m->cap);
     TN_LAUNCHED();
 #undef TN_TRY
     return TN_OK;

@@ -173,43 +173,39 @@ __device__ inline int dot_block(uint4 w, const int* __restrict__ xw) {
     return s;
 }
 
-template <int MR, typename XT>
+// Phase 1 gives each 32-element block to 8 lanes, a float4 each: lane l of
+// the workgroup holds elements 4 (l % 8) .. 4 (l % 8) + 3 of block l / 8 + 32 p
+// in pass p, so for one row thread t holds elements 1024p + 4t .. 1024p + 4t + 3.
+// The block's amax and code sum are 8-lane DPP reductions (no LDS round
+// trip). The RMSNorm prologue's sum of squares uses that partition -- thread
+// t adds the squares of its elements in order, then block_sum256 -- which is
+// k_rmsnorm's order, so the fused norm reproduces it bit for bit.
+//
+// Prologues (MR == 1, f32 x only):
+//   PRO_RMSNORM  x -> w * (x * r), r = 1/sqrt(sum(x^2)/K + eps)
+//   PRO_SILU     x holds [gate | up] (2K floats) -> gate/(1 + exp(-gate)) * up
+//   PRO_COMBINE  the row is the attention output h * D + d, merged from the
+//                split partials: sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)
+// Epilogue: y = acc (+ bias) (+ resid); y may alias resid (each output reads
+// its own residual before writing), never x. x must be 16-byte aligned.
+constexpr int GEMV_HOLD = 4;  // passes of 32 blocks held in registers (K <= 4096 per row at once)
+
+template <int MR, typename XT, int PRO>
 __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x, int K, int nb,
                                                      const uint8_t* __restrict__ qs,
                                                      const uint16_t* __restrict__ dw, int N, int rows,
-                                                     const float* __restrict__ bias, void* __restrict__ y,
-                                                     int y_bf16) {
+                                                     const float* __restrict__ bias, const float* resid, void* y,
+                                                     int y_bf16, const GemvPro po) {
+    static_assert(PRO == PRO_NONE || (MR == 1 && sizeof(XT) == 4), "prologues take one f32 row");
+    constexpr int HOLD = PRO == PRO_COMBINE ? 1 : GEMV_HOLD;
     extern __shared__ __align__(16) char smem[];
+    __shared__ float red[4];
     int* xq = reinterpret_cast<int*>(smem);               // [MR][K/4] packed int8 codes
     float* dxs = reinterpret_cast<float*>(xq + MR * (K / 4));  // [MR][nb]
     int* sxs = reinterpret_cast<int*>(dxs + MR * nb);     // [MR][nb]
     float* terms = reinterpret_cast<float*>(sxs + MR * nb);  // [rows][MR][nb]
     const int tid = threadIdx.x;
 
-    // phase 1: Q8_0 of the MR activation rows, one 32-lane group per block
-    {
-        const int grp = tid >> 5, lane = tid & 31;
-        int8_t* xb = reinterpret_cast<int8_t*>(xq);
-        for (int blk = grp; blk < MR * nb; blk += GEMV_THREADS / 32) {
-            const int mr = blk / nb, b = blk - mr * nb;
-            float v = load_x<XT>(x + (int64_t)mr * K + b * QK + lane);
-            float dx;
-            int q = q8_0_lane(v, &dx);
-            xb[mr * K + b * QK + lane] = (int8_t)q;
-            int s = q;
-#pragma unroll
-            for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off, 32);
-            if (lane == 0) {
-                dxs[mr * nb + b] = dx;
-                sxs[mr * nb + b] = s;
-            }
-        }
-    }
-    __syncthreads();
-
-    // phase 2/3, persistent over row tiles: the next tile's weight loads are in
-    // flight while this tile's terms are computed and summed; the terms live
-    // in two LDS buffers, so one barrier per tile suffices
     const int ntiles = (N + rows - 1) / rows;
     const int tstride = (int)gridDim.x;
     uint4 wv[GEMV_ITEMS], wn[GEMV_ITEMS];
@@ -231,8 +227,135 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
             }
         }
     };
+    // the first tile's weight loads are in flight during the activation work
     int tile = (int)blockIdx.x;
     if (tile < ntiles) gload(tile, wv, dv);
+
+    // phase 1: Q8_0 of the MR activation rows (after the prologue)
+    {
+        const int g8 = tid & 7, slot = tid >> 3;
+        const int nblk = MR * nb, npass = (nblk + 31) / 32;
+        float4 xv[HOLD], av[HOLD];  // the row, and the prologue's second operand
+        int ns = 0;
+        if constexpr (PRO == PRO_COMBINE) {
+            int len = *po.len;
+            len = len < 0 ? 0 : (len > po.cap ? po.cap : len);
+            ns = (len + STEP_SPLIT - 1) / STEP_SPLIT;
+            ns = ns < po.nsplit ? ns : po.nsplit;
+        }
+        auto load_passes = [&](int p0) {
+#pragma unroll
+            for (int u = 0; u < HOLD; u++) {
+                const int blk = (p0 + u) * 32 + slot;
+                if (blk < nblk) {
+                    const int mr = blk / nb, b = blk - mr * nb;
+                    const int64_t off = (int64_t)mr * K + b * QK + 4 * g8;
+                    if constexpr (PRO == PRO_COMBINE) {
+                        // every split's (m, l) and O piece in flight at once
+                        const int h = (int)(off / po.head_dim), d = (int)(off - (int64_t)h * po.head_dim);
+                        float2 ml[STEP_MAX_SPLITS];
+                        float4 o4[STEP_MAX_SPLITS];
+#pragma unroll
+                        for (int sp = 0; sp < STEP_MAX_SPLITS; sp++) {
+                            if (sp < ns) {
+                                const int64_t prow = (int64_t)h * po.nsplit + sp;
+                                ml[sp] = po.part_ml[prow];
+                                o4[sp] = *reinterpret_cast<const float4*>(po.part_o + prow * po.head_dim + d);
+                            }
+                        }
+                        float mm = -INFINITY;
+#pragma unroll
+                        for (int sp = 0; sp < STEP_MAX_SPLITS; sp++)
+                            if (sp < ns) mm = fmaxf(mm, ml[sp].x);
+                        const float mu = (mm == -INFINITY) ? 0.0f : mm;
+                        float tl = 0.0f;
+                        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                        for (int sp = 0; sp < STEP_MAX_SPLITS; sp++) {
+                            if (sp < ns) {
+                                const float f = exp2f(ml[sp].x - mu);
+                                tl = tl + ml[sp].y * f;
+                                acc.x = acc.x + o4[sp].x * f;
+                                acc.y = acc.y + o4[sp].y * f;
+                                acc.z = acc.z + o4[sp].z * f;
+                                acc.w = acc.w + o4[sp].w * f;
+                            }
+                        }
+                        xv[u] = make_float4(acc.x / tl, acc.y / tl, acc.z / tl, acc.w / tl);
+                    } else if constexpr (sizeof(XT) == 4) {
+                        xv[u] = *reinterpret_cast<const float4*>(x + off);
+                    } else {
+                        const uint2 h = *reinterpret_cast<const uint2*>(x + off);
+                        xv[u] = make_float4(bf16_to_f32((uint16_t)(h.x & 0xffffu)), bf16_to_f32((uint16_t)(h.x >> 16)),
+                                            bf16_to_f32((uint16_t)(h.y & 0xffffu)), bf16_to_f32((uint16_t)(h.y >> 16)));
+                    }
+                    if constexpr (PRO == PRO_RMSNORM) av[u] = *reinterpret_cast<const float4*>(po.w + off);
+                    if constexpr (PRO == PRO_SILU)
+                        av[u] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + K + off);
+                }
+            }
+        };
+        float r = 0.0f;
+        if constexpr (PRO == PRO_RMSNORM) {
+            float ss = 0.0f;
+            for (int p0 = 0; p0 < npass; p0 += HOLD) {
+                load_passes(p0);
+#pragma unroll
+                for (int u = 0; u < HOLD; u++) {
+                    if ((p0 + u) * 32 + slot < nblk) {
+                        ss = ss + xv[u].x * xv[u].x;
+                        ss = ss + xv[u].y * xv[u].y;
+                        ss = ss + xv[u].z * xv[u].z;
+                        ss = ss + xv[u].w * xv[u].w;
+                    }
+                }
+            }
+            r = rms_scale(block_sum256(ss, red), K, po.eps);
+        }
+        int8_t* xb = reinterpret_cast<int8_t*>(xq);
+        for (int p0 = 0; p0 < npass; p0 += HOLD) {
+            // the RMSNorm pass already holds a row of up to HOLD passes
+            if (PRO != PRO_RMSNORM || npass > HOLD) load_passes(p0);
+#pragma unroll
+            for (int u = 0; u < HOLD; u++) {
+                const int blk = (p0 + u) * 32 + slot;
+                if (blk < nblk) {  // uniform over the block's 8 lanes
+                    float e[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+                    const float o[4] = {av[u].x, av[u].y, av[u].z, av[u].w};
+                    float amax = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        if constexpr (PRO == PRO_RMSNORM) e[i] = o[i] * (e[i] * r);
+                        if constexpr (PRO == PRO_SILU) e[i] = (e[i] / (1.0f + expf(-e[i]))) * o[i];
+                        amax = fmaxf(amax, fabsf(e[i]));
+                    }
+                    // BlockQ8_0::from_float (k_quants.rs:676-705)
+                    amax = group8_max(amax);
+                    const float d = amax / 127.0f;
+                    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+                    uint32_t wd = 0;
+                    int sq = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int q = sat_i8(roundf(e[i] * id));
+                        sq += q;
+                        wd |= ((uint32_t)q & 0xffu) << (8 * i);
+                    }
+                    sq = group8_sum(sq);
+                    reinterpret_cast<uint32_t*>(xb)[blk * 8 + g8] = wd;  // blocks of all rows are contiguous
+                    if (g8 == 0) {
+                        dxs[blk] = f16_to_f32(f16_from_f32(d));
+                        sxs[blk] = sq;
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // phase 2/3, persistent over row tiles: the next tile's weight loads are in
+    // flight while this tile's terms are computed and summed; the terms live
+    // in two LDS buffers, so one barrier per tile suffices
     for (int buf = 0; tile < ntiles; tile += tstride, buf ^= 1) {
         const int next = tile + tstride;
         if (next < ntiles) gload(next, wn, dn);
@@ -264,6 +387,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
             for (int b = 0; b < nb; b++) acc = acc + tr[b];
             const int64_t n = row0 + r;
             if (bias) acc = acc + bias[n];
+            if (resid) acc = acc + resid[(int64_t)mr * N + n];
             if (y_bf16)
                 reinterpret_cast<uint16_t*>(y)[(int64_t)mr * N + n] = bf16_from_f32(acc);
             else
@@ -504,9 +628,10 @@ tn_status check_weight(const char* op, int64_t n, int64_t k) {
     return TN_OK;
 }
 
-template <int MR, typename XT>
+template <int MR, typename XT, int PRO = PRO_NONE>
 tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, const uint16_t* dw, int N,
-                      const float* bias, void* y, int y_bf16) {
+                      const float* bias, void* y, int y_bf16, const float* resid = nullptr,
+                      const GemvPro& po = GemvPro()) {
     const int nb = K / QK;
     // rows per tile: as many as GEMV_ITEMS items per thread allow, but no more
     // than it takes to give every CU a tile of a small matrix
@@ -530,11 +655,12 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     // workgroup that had to wait for a slot would start its whole share of
     // tiles late)
     int resident = 0;
-    tn_status s = resident_workgroups(reinterpret_cast<const void*>(&k_gemv<MR, XT>), GEMV_THREADS, lds, &resident);
+    tn_status s =
+        resident_workgroups(reinterpret_cast<const void*>(&k_gemv<MR, XT, PRO>), GEMV_THREADS, lds, &resident);
     if (s != TN_OK) return s;
     const unsigned grid = (unsigned)(ntiles < resident ? ntiles : resident);
-    hipLaunchKernelGGL((k_gemv<MR, XT>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N, rows,
-                       bias, y, y_bf16);
+    hipLaunchKernelGGL((k_gemv<MR, XT, PRO>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N, rows,
+                       bias, resid, y, y_bf16, po);
     TN_LAUNCHED();
     return TN_OK;
 }
@@ -545,7 +671,8 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
     if (m == 0 || n == 0) return TN_OK;
     const int nb = (int)(k / QK);
     const size_t ysz = y_bf16 ? 2 : 4;
-    if (m <= GEMV_MAX_M && nb <= GEMV_THREADS * GEMV_ITEMS) {
+    // the GEMV reads x in 16-byte pieces; an unaligned x takes the GEMM path
+    if (m <= GEMV_MAX_M && nb <= GEMV_THREADS * GEMV_ITEMS && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
         // decode: GEMV in chunks of up to 4 rows of x (a row's result does not
         // depend on the chunking: every output is the same recurrence)
         int64_t r = 0;
@@ -592,6 +719,33 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
 }
 
 }  // namespace
+
+// One activation row through a q4_0 linear for the decode step, with the
+// step's neighbouring elementwise ops fused in (see k_gemv): bit-identical to
+// running tn_rmsnorm / tn_silu_mul, then tn_q4_0_linear, then tn_add.
+tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, const GemvPro& po, const uint8_t* qs,
+                        const uint16_t* d, int64_t n, const float* resid, float* y) {
+    tn_status s = check_weight("linear_decode", n, k);
+    if (s != TN_OK) return s;
+    if (k > LINEAR_DECODE_MAX_K || n > INT32_MAX) return fail(TN_ENOTIMPL, "linear_decode: shape too large");
+    if (n == 0) return TN_OK;
+    switch (pro) {
+        case PRO_RMSNORM:
+            s = launch_gemv<1, float, PRO_RMSNORM>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po);
+            break;
+        case PRO_SILU: s = launch_gemv<1, float, PRO_SILU>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po); break;
+        case PRO_COMBINE:
+            if (po.head_dim < 4 || po.head_dim % 4 != 0 || k % po.head_dim != 0 || po.nsplit < 1 ||
+                po.nsplit > STEP_MAX_SPLITS || !po.part_o || !po.part_ml || !po.len)
+                return fail(TN_EINVAL, "linear_decode: bad attention partials");
+            s = launch_gemv<1, float, PRO_COMBINE>(st, po.part_o, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po);
+            break;
+        default: s = launch_gemv<1, float, PRO_NONE>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po); break;
+    }
+    if (s == TN_ENOTIMPL) return fail(TN_ENOTIMPL, "linear_decode: the activation row does not fit the GEMV");
+    return s;
+}
+
 }  // namespace tn
 
 using namespace tn;
@@ -644,6 +798,30 @@ tn_status tn_q4_0_dequantize(void* stream, const uint8_t* qs, const uint16_t* d,
                        nblocks, out);
     TN_LAUNCHED();
     return TN_OK;
+}
+
+tn_status tn_q4_0_linear_decode(void* stream, const float* x, int64_t k, int prologue, const float* prologue_w,
+                                double eps, const uint8_t* qs, const uint16_t* d, int64_t n, const float* resid,
+                                float* y) {
+    const char* op = "q4_0_linear_decode";
+    if (prologue != TN_PRO_NONE && prologue != TN_PRO_RMSNORM && prologue != TN_PRO_SILU)
+        return fail(TN_EINVAL, std::string(op) + ": unknown prologue");
+    if (k <= 0 || n < 0) return fail(TN_EINVAL, std::string(op) + ": bad sizes");
+    if (n == 0) return TN_OK;
+    if (!x || !qs || !d || !y || (prologue == TN_PRO_RMSNORM && !prologue_w))
+        return fail(TN_EVALUE, std::string(op) + ": null pointer");
+    // y is written while other workgroups still read x
+    const char* xb = reinterpret_cast<const char*>(x);
+    const char* yb = reinterpret_cast<const char*>(y);
+    const int64_t xlen = (prologue == TN_PRO_SILU ? 2 * k : k) * 4;
+    if (yb < xb + xlen && xb < yb + n * 4) return fail(TN_EINVAL, std::string(op) + ": y overlaps x");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(prologue_w)) % 16 != 0)
+        return fail(TN_EINVAL, std::string(op) + ": x and prologue_w must be 16-byte aligned");
+    static_assert(TN_PRO_NONE == PRO_NONE && TN_PRO_RMSNORM == PRO_RMSNORM && TN_PRO_SILU == PRO_SILU, "prologues");
+    GemvPro po;
+    po.w = prologue_w;
+    po.eps = (float)eps;
+    return linear_decode((hipStream_t)stream, x, k, prologue, po, qs, d, n, resid, y);
 }
 
 tn_status tn_q4_0_linear(void* stream, const void* x, int x_dtype, int64_t m, int64_t k, const uint8_t* qs,

@@ -921,7 +921,18 @@ __global__ __launch_bounds__(256) void k_decode_f32(const float* __restrict__ Qg
 
     const int d = tid % D, g = tid / D;
     float acc = 0.0f;
-    for (int t = g; t < nk; t += G) acc = acc + sp[t] * vp[(int64_t)(k0 + t) * D + d];
+    constexpr int U = 8;  // V rows in flight per thread
+    for (int t0 = g; t0 < nk; t0 += G * U) {
+        float vr[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int t = t0 + u * G;
+            vr[u] = t < nk ? vp[(int64_t)(k0 + t) * D + d] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (t0 + u * G < nk) acc = acc + sp[t0 + u * G] * vr[u];
+    }
     so[g][d] = acc;
     __syncthreads();
     if (tid < D) {
@@ -931,6 +942,130 @@ __global__ __launch_bounds__(256) void k_decode_f32(const float* __restrict__ Qg
         const int64_t prow = ((int64_t)b * Hq + h) * nsplit + split;
         part_o[prow * D + tid] = o;
         if (tid == 0) part_ml[prow] = make_float2(m, l);
+    }
+}
+
+// Decode, f32, single pass: one workgroup per (query head, sequence) over the
+// whole sequence, for caches of at most DEC1_MAX_KEYS keys -- the decode
+// step's regime, where split partials and a combine launch cost more than
+// they save. D/4 lanes share a key row, a float4 each, so every load
+// instruction reads whole rows; each lane keeps DEC1_U rows in flight; the
+// scores stay in LDS. The first batch of V rows is loaded before the softmax.
+constexpr int DEC1_MAX_KEYS = 1024;
+constexpr int DEC1_U = 16;
+
+// s_waitcnt lgkmcnt(0) then s_barrier: orders LDS only, global loads stay in flight
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_decode1_f32(const float* __restrict__ Qg, const float* __restrict__ Kc,
+                                                   const float* __restrict__ Vc, int Hq, int Hkv, int nrep, int cap,
+                                                   const int32_t* __restrict__ lens, int max_len, float sl2,
+                                                   float* __restrict__ out, float* __restrict__ lse) {
+    constexpr int TPK = D / 4;     // lanes per key row
+    constexpr int RPI = 256 / TPK;  // rows per workgroup per load instruction
+    __shared__ float sp[DEC1_MAX_KEYS];
+    __shared__ float sred[2][4];
+    __shared__ float4 so[4][TPK];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int c = tid % TPK, kl = tid / TPK;  // float4 of the row, row slot
+    const int h = blockIdx.x, b = blockIdx.y, kvh = h / nrep;
+    int len = lens[b];
+    len = len < 0 ? 0 : (len > max_len ? max_len : len);  // max_len <= min(cap, DEC1_MAX_KEYS)
+    const float4* kp = reinterpret_cast<const float4*>(Kc + ((int64_t)b * Hkv + kvh) * cap * D);
+    const float4* vp = reinterpret_cast<const float4*>(Vc + ((int64_t)b * Hkv + kvh) * cap * D);
+    const float4 qv = reinterpret_cast<const float4*>(Qg + ((int64_t)b * Hq + h) * D)[c];
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    float4 rv[DEC1_U];
+    auto load_rows = [&](const float4* base, int t0) {
+#pragma unroll
+        for (int u = 0; u < DEC1_U; u++) {
+            const int t = t0 + u * RPI + kl;
+            rv[u] = t < len ? base[(int64_t)t * TPK + c] : zero;
+        }
+    };
+
+    // scores, scaled to log2 units, into LDS
+    float mx = -INFINITY;
+    for (int t0 = 0; t0 < len; t0 += RPI * DEC1_U) {
+        load_rows(kp, t0);
+#pragma unroll
+        for (int u = 0; u < DEC1_U; u++) {
+            float s = qv.x * rv[u].x;
+            s = s + qv.y * rv[u].y;
+            s = s + qv.z * rv[u].z;
+            s = s + qv.w * rv[u].w;
+            s = row16_sum(s);
+            if constexpr (TPK == 32) s = s + __shfl_xor(s, 16);
+            const int t = t0 + u * RPI + kl;
+            if (t < len) {
+                s = s * sl2;
+                mx = fmaxf(mx, s);
+                if (c == 0) sp[t] = s;
+            }
+        }
+    }
+    load_rows(vp, 0);  // the first V rows travel during the softmax
+    mx = wave_xor_max(row16_max(mx));
+    if (lane == 0) sred[0][w] = mx;
+    lds_barrier();
+    const float m = fmaxf(fmaxf(sred[0][0], sred[0][1]), fmaxf(sred[0][2], sred[0][3]));
+    const float mu = (m == -INFINITY) ? 0.0f : m;
+    float l = 0.0f;
+    for (int t = tid; t < len; t += 256) {
+        const float p = exp2f(sp[t] - mu);
+        sp[t] = p;
+        l = l + p;
+    }
+    l = wave_xor_sum(row16_sum(l));
+    if (lane == 0) sred[1][w] = l;
+    lds_barrier();
+    l = (sred[1][0] + sred[1][1]) + (sred[1][2] + sred[1][3]);
+
+    // P.V: the same row slots; each lane sums its float4 over its rows in order
+    float4 acc = zero;
+    for (int t0 = 0; t0 < len; t0 += RPI * DEC1_U) {
+        if (t0 > 0) load_rows(vp, t0);
+#pragma unroll
+        for (int u = 0; u < DEC1_U; u++) {
+            const int t = t0 + u * RPI + kl;
+            if (t < len) {
+                const float p = sp[t];
+                acc.x = acc.x + p * rv[u].x;
+                acc.y = acc.y + p * rv[u].y;
+                acc.z = acc.z + p * rv[u].z;
+                acc.w = acc.w + p * rv[u].w;
+            }
+        }
+    }
+    // the wave's row slots (lanes c, c + TPK, ...), then the four waves
+#pragma unroll
+    for (int off = TPK; off < 64; off <<= 1) {
+        acc.x = acc.x + __shfl_xor(acc.x, off);
+        acc.y = acc.y + __shfl_xor(acc.y, off);
+        acc.z = acc.z + __shfl_xor(acc.z, off);
+        acc.w = acc.w + __shfl_xor(acc.w, off);
+    }
+    if (lane < TPK) so[w][lane] = acc;
+    lds_barrier();
+    if (tid < TPK) {
+        float4 o = so[0][tid];
+#pragma unroll
+        for (int ww = 1; ww < 4; ww++) {
+            o.x = o.x + so[ww][tid].x;
+            o.y = o.y + so[ww][tid].y;
+            o.z = o.z + so[ww][tid].z;
+            o.w = o.w + so[ww][tid].w;
+        }
+        reinterpret_cast<float4*>(out + ((int64_t)b * Hq + h) * D)[tid] =
+            make_float4(o.x / l, o.y / l, o.z / l, o.w / l);
+        if (lse && tid == 0) lse[(int64_t)b * Hq + h] = mu * LN2 + logf(l);
     }
 }
 
@@ -1007,6 +1142,17 @@ tn_status decode_launch(hipStream_t st, int dtype, const void* q, const void* k_
         auto kk = static_cast<const float*>(k_cache);
         auto vv = static_cast<const float*>(v_cache);
         auto oo = static_cast<float*>(out);
+        if (max_len <= DEC1_MAX_KEYS) {
+            const dim3 g1((unsigned)Hq, (unsigned)B);
+            if (D == 128)
+                hipLaunchKernelGGL(k_decode1_f32<128>, g1, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, nrep,
+                                   (int)cap, lens, (int)max_len, sl2, oo, lse);
+            else
+                hipLaunchKernelGGL(k_decode1_f32<64>, g1, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, nrep,
+                                   (int)cap, lens, (int)max_len, sl2, oo, lse);
+            TN_LAUNCHED();
+            return TN_OK;
+        }
         const dim3 grid((unsigned)nsplit, (unsigned)Hq, (unsigned)B);
         if (D == 128)
             hipLaunchKernelGGL(k_decode_f32<128>, grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, nrep,
@@ -1285,6 +1431,9 @@ tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_c
     tn_status s = decode_check(dtype, B, Hq, Hkv, cap, D, max_len);
     if (s != TN_OK || B == 0 || Hq == 0) return s;
     if (!q || !k_cache || !v_cache || !out || !lens) return fail(TN_EVALUE, "sdpa_decode: null pointer");
+    // the f32 kernels move rows in 16-byte pieces
+    if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) % 16 != 0)
+        return fail(TN_EINVAL, "sdpa_decode: q, the caches and out must be 16-byte aligned");
     const int64_t nsplit = cdiv(max_len, DEC_SPLIT);
     const size_t po = (size_t)B * Hq * nsplit * D * sizeof(float);
     const size_t pm = (size_t)B * Hq * nsplit * sizeof(float2);

@@ -115,4 +115,98 @@ __host__ __device__ inline float bf16_to_f32(uint16_t h) {
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Sum of one float per thread over a 256-thread workgroup, in one fixed order
+// (each 16-lane row, then rows r + (r ^ 1), then halves, then the four waves
+// as (w0 + w1) + (w2 + w3)). Every kernel that normalises a row uses this, so
+// a fused RMSNorm gives the bits of the separate one. `red` is 4 floats of
+// LDS; all threads must call.
+__device__ inline float block_sum256(float v, float* red);
+
+// One DPP-routed copy of v (a VALU op, no LDS round trip). The patterns used
+// here read within each 16-lane row, so every lane has a source:
+//   0xB1 lane ^ 1, 0x4E lane ^ 2 (quad_perm), 0x141 the mirror lane within
+//   each 8 (row_half_mirror), 0x140 the mirror lane within each 16 (row_mirror).
+template <int CTRL>
+__device__ inline int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
+// Reductions over aligned groups of 8 or 16 lanes; every lane of a group gets
+// the same bits (each step combines a value with its partner's, and the
+// partner computes b + a for a + b). All lanes of a group must be active.
+__device__ inline float group8_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    return fmaxf(v, dpp_f<0x141>(v));
+}
+__device__ inline int group8_sum(int v) {
+    v = v + dpp_i<0xB1>(v);
+    v = v + dpp_i<0x4E>(v);
+    return v + dpp_i<0x141>(v);
+}
+__device__ inline float row16_sum(float v) {
+    v = v + dpp_f<0xB1>(v);
+    v = v + dpp_f<0x4E>(v);
+    v = v + dpp_f<0x141>(v);
+    return v + dpp_f<0x140>(v);
+}
+__device__ inline float row16_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    return fmaxf(v, dpp_f<0x140>(v));
+}
+
+__device__ inline float block_sum256(float v, float* red) {
+    v = row16_sum(v);
+    v = v + __shfl_xor(v, 16);
+    v = v + __shfl_xor(v, 32);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float s = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();  // red may be reused at once
+    return s;
+}
+
+// The RMSNorm scale of a row from its sum of squares: 1 / sqrt(ss/n + eps),
+// sqrt then reciprocal as the reference's rsqrt (aten.rs:11112-11133).
+__device__ inline float rms_scale(float ss, int n, float eps) { return 1.0f / sqrtf(ss / (float)n + eps); }
+
+// Input transforms a decode linear can apply while it quantises its input.
+// PRO_COMBINE builds the row from split attention partials (the decode
+// step's o projection).
+enum LinearPrologue { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU = 2, PRO_COMBINE = 3 };
+
+// Keys per workgroup of the decode step's fused attention, and the most
+// splits whose merge the o projection's prologue takes on; a longer cache
+// runs the split-KV attention with its own combine.
+constexpr int STEP_SPLIT = 64;
+constexpr int STEP_MAX_SPLITS = 8;
+
+// Prologue operands of the decode GEMV.
+struct GemvPro {
+    const float* w = nullptr;  // PRO_RMSNORM weight [K]
+    float eps = 0.0f;
+    // PRO_COMBINE: partials [heads][nsplit][head_dim] and (m, l) [heads][nsplit]
+    // in log2 units over splits of STEP_SPLIT keys; the KV length is
+    // min(*len, cap)
+    const float* part_o = nullptr;
+    const float2* part_ml = nullptr;
+    const int32_t* len = nullptr;
+    int nsplit = 0, head_dim = 0, cap = 0;
+};
+
+// One f32 row through a q4_0 linear (q4_0.hip), y[n] = Q8_0(pro(x)) . W^T
+// (+ resid[n]): pro is a LinearPrologue (PRO_RMSNORM scales by po.w with
+// po.eps; PRO_SILU reads x as [gate | up], 2k floats; PRO_COMBINE ignores x
+// and merges po's attention partials). Bit-identical to the separate ops in
+// sequence. y may alias resid, not x. k <= LINEAR_DECODE_MAX_K.
+constexpr int64_t LINEAR_DECODE_MAX_K = 32768;
+tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, const GemvPro& po, const uint8_t* qs,
+                        const uint16_t* d, int64_t n, const float* resid, float* y);
+
 }  // namespace tn
