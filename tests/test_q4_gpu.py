@@ -89,6 +89,43 @@ def test_gemv_is_bit_identical_to_the_oracle(tn, m, n, k, seed):
     assert got.tobytes() == want.tobytes(), np.argwhere(got != want)[:5]
 
 
+def test_gemv_scales_across_every_f16_regime(tn):
+    """Weight scales over every finite f16 bit pattern (subnormals, both
+    zeros, the largest normal) and activation blocks whose Q8_0 scale
+    amax/127 lands below the smallest subnormal, among the subnormals, on
+    the normal boundary and around the f16 maximum: dequantisation and the
+    GEMV bit for bit against the oracle. In a row whose block scale overflows
+    to inf the outputs are infinities and NaNs (inf - inf, 0 * inf) in the
+    oracle's places."""
+    k, nb = 1024, 32
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = bits[(bits & 0x7C00) != 0x7C00]
+    n = len(finite) // nb
+    rng = np.random.default_rng(41)
+    blob = np.zeros((n * nb, 18), np.uint8)
+    blob[:, :2] = finite[: n * nb].view(np.uint8).reshape(-1, 2)
+    blob[:, 2:] = rng.integers(0, 256, size=(n * nb, 16), dtype=np.uint8)
+    blob = blob.tobytes()
+    q = _qweight(tn, blob, n, k)
+    assert tn._dequantize(q).numpy().tobytes() == O.q4_0_dequantize(blob, n * k).tobytes()
+
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    targets = [0.0, 1e-9, 2.9e-8, 5.9604645e-08, 8.9e-8, 6.097e-05, 6.1035156e-05, 6.104e-05, 1.0, 65504.0,
+               65519.0, 65519.996]
+    for i, t in enumerate(targets):
+        blk = x[0, 32 * i:32 * (i + 1)]
+        x[0, 32 * i:32 * (i + 1)] = (blk / np.max(np.abs(blk)) * np.float32(t * 127.0)).astype(np.float32)
+    x[1, :32] *= np.float32(1e7)  # amax / 127 > 65520: the scale rounds to inf
+    want = O.q4_0_linear(x, blob, n, threads=8)
+    got = tn._quantized_linear(tn.tensor(x, device="hip"), q).numpy()
+    assert got[0].tobytes() == want[0].tobytes(), np.argwhere(got[0] != want[0])[:5]
+    assert not np.isfinite(want[1]).any()
+    assert np.array_equal(got[1], want[1], equal_nan=True)
+    # one row at a time takes the single-row kernel
+    got0 = tn._quantized_linear(tn.tensor(x[:1], device="hip"), q).numpy()
+    assert got0.tobytes() == want[:1].tobytes()
+
+
 @pytest.mark.parametrize("m,n,k,seed", [
     (5, 11, 512, 21), (17, 10, 512, 22), (130, 9, 512, 23),  # test_qgemm.py row / tail counts
     (128, 256, 1024, 24), (200, 333, 576, 25), (512, 384, 4096, 26),

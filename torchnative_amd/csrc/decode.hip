@@ -121,15 +121,10 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int c = tid % TPK, kl = tid / TPK;
     const int sp = blockIdx.x, kvh = blockIdx.y;
-    const int pos = state[0];
-    const int len = pos < 0 ? 0 : (pos + 1 < cap ? pos + 1 : cap);
     const int k0 = sp * STEP_SPLIT;
-    if (k0 >= len) return;  // uniform over the workgroup
-    const int ncached = pos < len ? pos : len;  // rows read from the caches
-    const bool fresh = pos >= k0 && pos < k0 + STEP_SPLIT && pos < len;
-    const int half = D / 2;
-
-    // the split's cached rows: every load in flight before the rotations
+    // the split's rows below cap go out before the position is known (rows at
+    // or past the position are replaced or masked below), so the cache reads
+    // and the read of the position overlap
     const float4* kp = reinterpret_cast<const float4*>(kc + (int64_t)kvh * cap * D);
     const float4* vp = reinterpret_cast<const float4*>(vc + (int64_t)kvh * cap * D);
     const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -137,26 +132,67 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const int t = k0 + u * SLOTS + kl;
-        kr[u] = t < ncached ? kp[(int64_t)t * TPK + c] : zero;
-        vr[u] = t < ncached ? vp[(int64_t)t * TPK + c] : zero;
+        kr[u] = t < cap ? kp[(int64_t)t * TPK + c] : zero;
+        vr[u] = t < cap ? vp[(int64_t)t * TPK + c] : zero;
     }
-    for (int i = tid; i < NR * half; i += 256) {
-        const int hh = i / half, j = i - hh * half;
-        const float* xr = qkv + (int64_t)(kvh * NR + hh) * D;
-        const float f = (float)pos * inv_freq[j];
-        const float cs = cosf(f), sn = sinf(f);
-        const float x1 = xr[j], x2 = xr[j + half];
-        sq[hh][j] = x1 * cs + (-x2) * sn;
-        sq[hh][j + half] = x2 * cs + x1 * sn;
+    // the rotation's operands too: thread i < NR * D/2 rotates pair i of the
+    // query heads, thread i < D/2 also pair i of the new key
+    constexpr int half = D / 2;
+    constexpr int QP = (NR * half + 255) / 256;  // query pairs per thread
+    float qx1[QP], qx2[QP], qf[QP], kx1 = 0.f, kx2 = 0.f, kvv1 = 0.f, kvv2 = 0.f, kf = 0.f;
+#pragma unroll
+    for (int i = 0; i < QP; i++) {
+        const int pi = tid + 256 * i;
+        qx1[i] = qx2[i] = qf[i] = 0.0f;
+        if (pi < NR * half) {
+            const int hh = pi / half, j = pi - hh * half;
+            const float* xr = qkv + (int64_t)(kvh * NR + hh) * D;
+            qx1[i] = xr[j];
+            qx2[i] = xr[j + half];
+            qf[i] = inv_freq[j];
+        }
     }
-    if (fresh && tid < half) {
+    if (tid < half) {
         const float* xk = qkv + (int64_t)(hq + kvh) * D;
         const float* xv = qkv + (int64_t)(hq + hkv + kvh) * D;
-        const float f = (float)pos * inv_freq[tid];
+        kx1 = xk[tid];
+        kx2 = xk[tid + half];
+        kvv1 = xv[tid];
+        kvv2 = xv[tid + half];
+        kf = inv_freq[tid];
+    }
+    const int pos = state[0];
+    const int len = pos < 0 ? 0 : (pos + 1 < cap ? pos + 1 : cap);
+    if (k0 >= len) return;  // uniform over the workgroup
+    const int ncached = pos < len ? pos : len;  // rows taken from the caches
+    const bool fresh = pos >= k0 && pos < k0 + STEP_SPLIT && pos < len;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        // rows past the cached ones hold stale or unwritten values: zero them
+        // (a NaN there would survive a zero probability)
+        if (k0 + u * SLOTS + kl >= ncached) {
+            kr[u] = zero;
+            vr[u] = zero;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < QP; i++) {
+        const int pi = tid + 256 * i;
+        if (pi < NR * half) {
+            const int hh = pi / half, j = pi - hh * half;
+            const float f = (float)pos * qf[i];
+            const float cs = cosf(f), sn = sinf(f);
+            const float x1 = qx1[i], x2 = qx2[i];
+            sq[hh][j] = x1 * cs + (-x2) * sn;
+            sq[hh][j + half] = x2 * cs + x1 * sn;
+        }
+    }
+    if (fresh && tid < half) {
+        const float f = (float)pos * kf;
         const float cs = cosf(f), sn = sinf(f);
-        const float x1 = xk[tid], x2 = xk[tid + half];
+        const float x1 = kx1, x2 = kx2;
         const float y1 = x1 * cs + (-x2) * sn, y2 = x2 * cs + x1 * sn;
-        const float v1 = xv[tid], v2 = xv[tid + half];
+        const float v1 = kvv1, v2 = kvv2;
         snew[0][tid] = y1;
         snew[0][tid + half] = y2;
         snew[1][tid] = v1;
@@ -194,7 +230,7 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
             d = d + qv[hh].z * kr[u].z;
             d = d + qv[hh].w * kr[u].w;
             d = row16_sum(d);
-            if constexpr (TPK == 32) d = d + __shfl_xor(d, 16);
+            if constexpr (TPK == 32) d = xor16_sum(d);
             sc[hh][u] = valid ? d * sl2 : -INFINITY;
         }
     }
@@ -203,8 +239,8 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
         float m = sc[hh][0];
 #pragma unroll
         for (int u = 1; u < U; u++) m = fmaxf(m, sc[hh][u]);
-#pragma unroll
-        for (int off = TPK; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if constexpr (TPK == 16) m = xor16_max(m);
+        m = xor32_max(m);
         if (lane == 0) smax[hh][w] = m;
     }
     __syncthreads();
@@ -225,14 +261,18 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
             acc[hh].w = acc[hh].w + p * vr[u].w;
         }
         // over the wave's row slots (lanes c, c + TPK, ...)
-#pragma unroll
-        for (int off = TPK; off < 64; off <<= 1) {
-            l = l + __shfl_xor(l, off);
-            acc[hh].x = acc[hh].x + __shfl_xor(acc[hh].x, off);
-            acc[hh].y = acc[hh].y + __shfl_xor(acc[hh].y, off);
-            acc[hh].z = acc[hh].z + __shfl_xor(acc[hh].z, off);
-            acc[hh].w = acc[hh].w + __shfl_xor(acc[hh].w, off);
+        if constexpr (TPK == 16) {
+            l = xor16_sum(l);
+            acc[hh].x = xor16_sum(acc[hh].x);
+            acc[hh].y = xor16_sum(acc[hh].y);
+            acc[hh].z = xor16_sum(acc[hh].z);
+            acc[hh].w = xor16_sum(acc[hh].w);
         }
+        l = xor32_sum(l);
+        acc[hh].x = xor32_sum(acc[hh].x);
+        acc[hh].y = xor32_sum(acc[hh].y);
+        acc[hh].z = xor32_sum(acc[hh].z);
+        acc[hh].w = xor32_sum(acc[hh].w);
         if (lane == 0) ssum[hh][w] = l;
         if (lane < TPK) so[w][hh][lane] = acc[hh];
     }

@@ -186,8 +186,8 @@ __device__ inline int dot_block(uint4 w, const int* __restrict__ xw) {
 //   PRO_SILU     x holds [gate | up] (2K floats) -> gate/(1 + exp(-gate)) * up
 //   PRO_COMBINE  the row is the attention output h * D + d, merged from the
 //                split partials: sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)
-// Epilogue: y = acc (+ bias) (+ resid); y may alias resid (each output reads
-// its own residual before writing), never x. x must be 16-byte aligned.
+// Epilogue: y = acc (+ bias, or + resid: never both); y may alias resid (each
+// output's thread reads its residual before writing it), never x. x must be 16-byte aligned.
 constexpr int GEMV_HOLD = 4;  // passes of 32 blocks held in registers (K <= 4096 per row at once)
 
 template <int MR, typename XT, int PRO>
@@ -203,7 +203,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
     int* xq = reinterpret_cast<int*>(smem);               // [MR][K/4] packed int8 codes
     float* dxs = reinterpret_cast<float*>(xq + MR * (K / 4));  // [MR][nb]
     int* sxs = reinterpret_cast<int*>(dxs + MR * nb);     // [MR][nb]
-    float* terms = reinterpret_cast<float*>(sxs + MR * nb);  // [rows][MR][nb]
+    // [2][rows][MR][nbp]: term rows padded to 16 bytes for the float4 reads of phase 3
+    const int nbp = (nb + 3) & ~3;
+    float* terms = reinterpret_cast<float*>(smem + ((MR * K + 8 * MR * nb + 15) & ~15));
     const int tid = threadIdx.x;
 
     const int ntiles = (N + rows - 1) / rows;
@@ -227,9 +229,20 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
             }
         }
     };
-    // the first tile's weight loads are in flight during the activation work
+    // the first tile's weight loads (and this thread's residual and bias for
+    // it) are in flight during the activation work
     int tile = (int)blockIdx.x;
-    if (tile < ntiles) gload(tile, wv, dv);
+    float pre_add = 0.0f;
+    if (tile < ntiles) {
+        gload(tile, wv, dv);
+        const int64_t row0 = (int64_t)tile * rows;
+        const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
+        if (tid < nrows * MR) {
+            const int r = tid / MR, mr = tid - r * MR;
+            if (bias) pre_add = bias[row0 + r];
+            if (resid) pre_add = resid[(int64_t)mr * N + row0 + r];  // resid and bias are not combined
+        }
+    }
 
     // phase 1: Q8_0 of the MR activation rows (after the prologue)
     {
@@ -251,13 +264,14 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                     const int mr = blk / nb, b = blk - mr * nb;
                     const int64_t off = (int64_t)mr * K + b * QK + 4 * g8;
                     if constexpr (PRO == PRO_COMBINE) {
-                        // every split's (m, l) and O piece in flight at once
+                        // every split's (m, l) and O piece in flight at once, read
+                        // before the length is known; splits past it are not used
                         const int h = (int)(off / po.head_dim), d = (int)(off - (int64_t)h * po.head_dim);
                         float2 ml[STEP_MAX_SPLITS];
                         float4 o4[STEP_MAX_SPLITS];
 #pragma unroll
                         for (int sp = 0; sp < STEP_MAX_SPLITS; sp++) {
-                            if (sp < ns) {
+                            if (sp < po.nsplit) {
                                 const int64_t prow = (int64_t)h * po.nsplit + sp;
                                 ml[sp] = po.part_ml[prow];
                                 o4[sp] = *reinterpret_cast<const float4*>(po.part_o + prow * po.head_dim + d);
@@ -344,7 +358,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                     sq = group8_sum(sq);
                     reinterpret_cast<uint32_t*>(xb)[blk * 8 + g8] = wd;  // blocks of all rows are contiguous
                     if (g8 == 0) {
-                        dxs[blk] = f16_to_f32(f16_from_f32(d));
+                        dxs[blk] = f16_round_hw(d);  // d is never NaN: amax ignores NaN
                         sxs[blk] = sq;
                     }
                 }
@@ -362,32 +376,53 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
         const int64_t row0 = (int64_t)tile * rows;
         const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
         const int total = nrows * nb;
-        float* tb = terms + buf * rows * MR * nb;
+        float* tb = terms + buf * rows * MR * nbp;
 #pragma unroll
         for (int it = 0; it < GEMV_ITEMS; it++) {
             const int g = tid + it * GEMV_THREADS;
             if (g < total) {
                 const int r = g / nb, b = g - r * nb;
-                const float dwf = f16_to_f32(dv[it]);
+                const float dwf = f16_bits_hw(dv[it]);
 #pragma unroll
                 for (int mr = 0; mr < MR; mr++) {
                     int s = dot_block(wv[it], xq + mr * (K / 4) + b * 8) - 8 * sxs[mr * nb + b];
                     float t = (float)s * dwf;
                     t = t * dxs[mr * nb + b];
-                    tb[(r * MR + mr) * nb + b] = t;
+                    tb[(r * MR + mr) * nbp + b] = t;
                 }
             }
         }
         __syncthreads();
-        // each output's terms in block order
+        // each output's terms in block order, read 16 at a time
         for (int o = tid; o < nrows * MR; o += GEMV_THREADS) {
             const int r = o / MR, mr = o - r * MR;
-            const float* tr = tb + (r * MR + mr) * nb;
-            float acc = 0.0f;
-            for (int b = 0; b < nb; b++) acc = acc + tr[b];
             const int64_t n = row0 + r;
-            if (bias) acc = acc + bias[n];
-            if (resid) acc = acc + resid[(int64_t)mr * N + n];
+            float add = pre_add;
+            if (tile != (int)blockIdx.x || o != tid) add = bias ? bias[n] : resid ? resid[(int64_t)mr * N + n] : 0.0f;
+            const float* tr = tb + (r * MR + mr) * nbp;
+            float acc = 0.0f;
+            int b = 0;
+            for (; b + 16 <= nb; b += 16) {
+                float4 t4[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) t4[j] = reinterpret_cast<const float4*>(tr + b)[j];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    acc = acc + t4[j].x;
+                    acc = acc + t4[j].y;
+                    acc = acc + t4[j].z;
+                    acc = acc + t4[j].w;
+                }
+            }
+            for (; b + 4 <= nb; b += 4) {
+                const float4 t4 = *reinterpret_cast<const float4*>(tr + b);
+                acc = acc + t4.x;
+                acc = acc + t4.y;
+                acc = acc + t4.z;
+                acc = acc + t4.w;
+            }
+            for (; b < nb; b++) acc = acc + tr[b];
+            if (bias || resid) acc = acc + add;
             if (y_bf16)
                 reinterpret_cast<uint16_t*>(y)[(int64_t)mr * N + n] = bf16_from_f32(acc);
             else
@@ -641,7 +676,11 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     if (rows < 1) rows = 1;
     if (rows > N) rows = N;
     // two term buffers (double-buffered across tiles)
-    auto lds_of = [&](int r) { return (size_t)MR * K + (size_t)MR * nb * 8 + 2 * (size_t)r * MR * nb * 4; };
+    if (bias && resid) return fail(TN_EINVAL, "q4_0 GEMV: bias and residual together are not supported");
+    const int nbp = (nb + 3) & ~3;
+    auto lds_of = [&](int r) {
+        return (((size_t)MR * K + (size_t)MR * nb * 8 + 15) & ~(size_t)15) + 2 * (size_t)r * MR * nbp * 4;
+    };
     size_t lds = lds_of(rows);
     while (rows > 1 && lds > 64 * 1024) {
         rows >>= 1;

@@ -41,17 +41,9 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.69314718055994531f;
 constexpr float RESCALE_SLACK = 8.0f;  // log2 of the largest unnormalised probability
 
-__device__ inline float wave_xor_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
-}
-
-__device__ inline float wave_xor_sum(float v) {
-    v = v + __shfl_xor(v, 16);
-    v = v + __shfl_xor(v, 32);
-    return v;
-}
+// over lanes l, l ^ 16, l ^ 32, l ^ 48
+__device__ inline float wave_xor_max(float v) { return xor32_max(xor16_max(v)); }
+__device__ inline float wave_xor_sum(float v) { return xor32_sum(xor16_sum(v)); }
 
 // two f32 -> packed bf16 pair, RNE (v_cvt_pk_bf16_f32); used for the
 // probabilities, which are finite and non-negative
@@ -87,17 +79,6 @@ __device__ inline void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-// max / sum of a value over lanes l and l ^ 32 (v_permlane32_swap: one VALU
-// op, no LDS round trip); both lanes get the same result
-__device__ inline float xor32_max(float v) {
-    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
-}
-
-__device__ inline float xor32_sum(float v) {
-    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
-}
 
 // Raw buffer descriptor over `bytes` bytes at `base`: offsets at or past the
 // end read as zero. Word 3 selects a 32-bit data format (any non-zero format
@@ -1002,7 +983,7 @@ __global__ __launch_bounds__(256) void k_decode1_f32(const float* __restrict__ Q
             s = s + qv.z * rv[u].z;
             s = s + qv.w * rv[u].w;
             s = row16_sum(s);
-            if constexpr (TPK == 32) s = s + __shfl_xor(s, 16);
+            if constexpr (TPK == 32) s = xor16_sum(s);
             const int t = t0 + u * RPI + kl;
             if (t < len) {
                 s = s * sl2;
@@ -1045,13 +1026,16 @@ __global__ __launch_bounds__(256) void k_decode1_f32(const float* __restrict__ Q
         }
     }
     // the wave's row slots (lanes c, c + TPK, ...), then the four waves
-#pragma unroll
-    for (int off = TPK; off < 64; off <<= 1) {
-        acc.x = acc.x + __shfl_xor(acc.x, off);
-        acc.y = acc.y + __shfl_xor(acc.y, off);
-        acc.z = acc.z + __shfl_xor(acc.z, off);
-        acc.w = acc.w + __shfl_xor(acc.w, off);
+    if constexpr (TPK == 16) {
+        acc.x = xor16_sum(acc.x);
+        acc.y = xor16_sum(acc.y);
+        acc.z = xor16_sum(acc.z);
+        acc.w = xor16_sum(acc.w);
     }
+    acc.x = xor32_sum(acc.x);
+    acc.y = xor32_sum(acc.y);
+    acc.z = xor32_sum(acc.z);
+    acc.w = xor32_sum(acc.w);
     if (lane < TPK) so[w][lane] = acc;
     lds_barrier();
     if (tid < TPK) {

@@ -102,6 +102,14 @@ __host__ __device__ inline float f16_to_f32(uint16_t h) {
     return __builtin_bit_cast(float, sign | ((exp + 112u) << 23) | (man << 13));
 }
 
+// The same two conversions through the hardware (v_cvt_f16_f32 under the
+// default round-to-nearest-even mode with f16 denormals, v_cvt_f32_f16): one
+// instruction each, equal to f16_from_f32 / f16_to_f32 for every input but
+// the payload bits of a NaN (compared over all 2^32 floats and all 65536
+// halves on gfx950).
+__device__ inline float f16_round_hw(float f) { return (float)(_Float16)f; }
+__device__ inline float f16_bits_hw(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
 // f32 -> bf16 round-to-nearest-even, NaN quieted (reduced.rs:161-218).
 __host__ __device__ inline uint16_t bf16_from_f32(float f) {
     uint32_t x = __builtin_bit_cast(uint32_t, f);
@@ -119,7 +127,8 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // (each 16-lane row, then rows r + (r ^ 1), then halves, then the four waves
 // as (w0 + w1) + (w2 + w3)). Every kernel that normalises a row uses this, so
 // a fused RMSNorm gives the bits of the separate one. `red` is 4 floats of
-// LDS; all threads must call.
+// LDS, used once per kernel (there is no barrier after the final reads, so a
+// second call on the same `red` could overwrite it early); all threads call.
 __device__ inline float block_sum256(float v, float* red);
 
 // One DPP-routed copy of v (a VALU op, no LDS round trip). The patterns used
@@ -161,15 +170,31 @@ __device__ inline float row16_max(float v) {
     return fmaxf(v, dpp_f<0x140>(v));
 }
 
+// v(l) combined with v(l ^ 16) or v(l ^ 32) through one VALU swap
+// (v_permlane16_swap / v_permlane32_swap: rows 2i and 2i+1, or the two
+// halves of the wave, trade places); both lanes of a pair get the same bits.
+__device__ inline float xor16_sum(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ inline float xor16_max(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ inline float xor32_sum(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ inline float xor32_max(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
 __device__ inline float block_sum256(float v, float* red) {
-    v = row16_sum(v);
-    v = v + __shfl_xor(v, 16);
-    v = v + __shfl_xor(v, 32);
+    v = xor32_sum(xor16_sum(row16_sum(v)));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    const float s = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();  // red may be reused at once
-    return s;
+    return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // The RMSNorm scale of a row from its sum of squares: 1 / sqrt(ss/n + eps),
