@@ -39,6 +39,8 @@ namespace {
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
+    uint32_t* tickets = nullptr;  // zeroed counters, returned to zero by their users
+    size_t ntickets = 0;
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
@@ -65,6 +67,35 @@ tn_status workspace(hipStream_t stream, size_t bytes, void** out) {
         counters().workspace_bytes.fetch_add(want);
     }
     *out = w.ptr;
+    return TN_OK;
+}
+
+tn_status tickets(hipStream_t stream, size_t n, uint32_t** out) {
+    int dev = 0;
+    TN_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace& w = g_ws[{dev, stream}];
+    if (w.ntickets < n) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        TN_HIP(hipStreamIsCapturing(stream, &cs));
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(TN_EINVAL, "tnhip: the first call that needs the stream's ticket counters cannot be captured "
+                                   "(they are cleared when allocated); make one call before capturing");
+        size_t want = n < 4096 ? 4096 : (n + 4095) & ~(size_t)4095;
+        if (w.tickets) {
+            TN_HIP(hipStreamSynchronize(stream));
+            TN_HIP(hipFree(w.tickets));
+            counters().workspace_bytes.fetch_sub(w.ntickets * 4);
+            w.tickets = nullptr;
+            w.ntickets = 0;
+        }
+        TN_HIP(hipMalloc(reinterpret_cast<void**>(&w.tickets), want * 4));
+        // zeroed once, ahead of the first kernel on this stream that takes a ticket
+        TN_HIP(hipMemsetAsync(w.tickets, 0, want * 4, stream));
+        w.ntickets = want;
+        counters().workspace_bytes.fetch_add(want * 4);
+    }
+    *out = w.tickets;
     return TN_OK;
 }
 
@@ -250,6 +281,10 @@ tn_status tn_stream_destroy(void* stream) {
                 if (it->second.ptr) {
                     TN_HIP(hipFree(it->second.ptr));
                     counters().workspace_bytes.fetch_sub(it->second.bytes);
+                }
+                if (it->second.tickets) {
+                    TN_HIP(hipFree(it->second.tickets));
+                    counters().workspace_bytes.fetch_sub(it->second.ntickets * 4);
                 }
                 g_ws.erase(it);
             }

@@ -23,6 +23,9 @@
 // the accumulators are touched only when a wave actually needs it. The result
 // is the same softmax; only the common factor differs until the end.
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <type_traits>
 #include <utility>
 #include <vector>
@@ -139,10 +142,12 @@ __device__ inline void lds_direct16(buf_rsrc rsrc, uint32_t voffset, void* lds_w
 // 32x32 result layout (lane l holds rows 8(r/4) + 4(l>>5) + r%4) put them.
 //
 // Long rows are also split across workgroups (the work list, FlashWork,
-// balances the items); a split writes unnormalised (m, l, O) partials that
-// k_prefill_combine merges. (A merge inside this kernel would take a
-// device-scope release per workgroup, which writes back the XCD's whole L2
-// and serialises there.)
+// balances the items). The splits of a row merge inside this kernel
+// (merge_split_rows): each publishes unnormalised (m, l, O) partials with
+// device-coherent stores and takes a ticket, and the last one merges them.
+// The partials bypass the non-coherent L2, so no device-scope release (which
+// writes back the XCD's whole L2) is needed. The softmax runs per 32-key half
+// so that one half's products can overlap the other's softmax.
 // ---------------------------------------------------------------------------
 
 constexpr int F3_BQ = 64, F3_BK = 64;  // queries per workgroup; key tile of the host-side split unit
@@ -153,6 +158,106 @@ __device__ inline float max3f(float a, float b, float c) {
     float r;
     asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
     return r;
+}
+
+// The rows of a split query block, merged inside the prefill kernel. Every
+// split item publishes its unnormalised (O, m, l) for the block's rows with
+// device-coherent stores (sc1: written through to memory, past this XCD's
+// L2), waits until they are acknowledged, and takes a ticket from the block's
+// counter. The item that draws the last ticket reads every split's partials
+// back with device-coherent loads and merges them in split order -- the
+// arithmetic of k_prefill_combine, so the result does not depend on which
+// item finishes last -- then returns the counter to zero for the next launch.
+// No fence is needed: only the partials cross workgroups, and they never sit
+// in a non-coherent cache. The partial stride is nsplit (the launch's
+// maximum); rows of the block are contiguous from `row0`.
+template <int D>
+__device__ __attribute__((always_inline)) inline void merge_split_rows(float* part_o, float2* part_ml, uint32_t* tickets, int nsplit,
+                                              int split, int ns, int64_t row0, int nrows, int64_t ticket,
+                                              bool holder, int r, int hh, const f32x16 (&o)[D / 32], float m,
+                                              float l, uint16_t* __restrict__ Og, float* __restrict__ lse,
+                                              uint32_t& s_ticket) {
+    constexpr uint32_t SC1 = 16;  // cache policy: device scope
+    const uint32_t po_bytes = (uint32_t)(nrows * nsplit * D * 4);
+    const buf_rsrc ro = make_rsrc(part_o + row0 * nsplit * D, po_bytes);
+    const buf_rsrc rm = make_rsrc(part_ml + row0 * nsplit, (uint32_t)(nrows * nsplit * 8));
+#if __HIP_DEVICE_COMPILE__
+    if (holder) {
+        const uint32_t base = (uint32_t)((r * nsplit + split) * D) * 4u;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+                const u32x4_t v = {__float_as_uint(o[dt][4 * g4]), __float_as_uint(o[dt][4 * g4 + 1]),
+                                   __float_as_uint(o[dt][4 * g4 + 2]), __float_as_uint(o[dt][4 * g4 + 3])};
+                __builtin_amdgcn_raw_buffer_store_b128(v, ro, base + (uint32_t)(32 * dt + 8 * g4 + 4 * hh) * 4u, 0,
+                                                       SC1);
+            }
+        if (hh == 0) {
+            typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+            const u32x2_t v = {__float_as_uint(m), __float_as_uint(l)};
+            __builtin_amdgcn_raw_buffer_store_b64(v, rm, (uint32_t)(r * nsplit + split) * 8u, 0, SC1);
+        }
+    }
+#endif
+    wait_vmcnt<0>();  // this thread's partials are acknowledged by memory
+    __syncthreads();
+    if (threadIdx.x == 0) s_ticket = __hip_atomic_fetch_add(tickets + ticket, 1u, __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_ticket != (uint32_t)(ns - 1)) return;  // uniform: another split merges the block
+#if __HIP_DEVICE_COMPILE__
+    // thread -> (row, 4 columns), every split's loads in flight before any is used
+    const buf_rsrc rout = make_rsrc(Og + row0 * D, (uint32_t)(nrows * D * 2));
+    constexpr int TPR = D / 4;
+    constexpr int CMAX = 4;
+    const int c4 = ((int)threadIdx.x % TPR) * 4;
+    for (int rr = (int)threadIdx.x / TPR; rr < nrows; rr += (int)blockDim.x / TPR) {
+        typedef float f32x2_t __attribute__((ext_vector_type(2)));
+        typedef float f32x4_t __attribute__((ext_vector_type(4)));
+        auto ld_ml = [&](int sp) {
+            return __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                                  rm, (uint32_t)(rr * nsplit + sp) * 8u, 0, SC1));
+        };
+        auto ld_o = [&](int sp) {
+            return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  ro, ((uint32_t)((rr * nsplit + sp) * D + c4)) * 4u, 0, SC1));
+        };
+        f32x2_t mlv[CMAX];
+        f32x4_t pv[CMAX];
+#pragma unroll
+        for (int sp = 0; sp < CMAX; sp++) {
+            mlv[sp] = sp < ns ? ld_ml(sp) : (f32x2_t){-INFINITY, 0.0f};
+            pv[sp] = sp < ns ? ld_o(sp) : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        }
+        float mm = -INFINITY;
+#pragma unroll
+        for (int sp = 0; sp < CMAX; sp++) mm = fmaxf(mm, mlv[sp][0]);
+        for (int sp = CMAX; sp < ns; sp++) mm = fmaxf(mm, ld_ml(sp)[0]);
+        const float mu = (mm == -INFINITY) ? 0.0f : mm;
+        float tl = 0.0f, a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        auto add = [&](f32x2_t m_l, f32x4_t v) {
+            const float f = exp2f(m_l[0] - mu);
+            tl = tl + m_l[1] * f;
+            a0 = a0 + v[0] * f;
+            a1 = a1 + v[1] * f;
+            a2 = a2 + v[2] * f;
+            a3 = a3 + v[3] * f;
+        };
+#pragma unroll
+        for (int sp = 0; sp < CMAX; sp++)
+            if (sp < ns) add(mlv[sp], pv[sp]);
+        for (int sp = CMAX; sp < ns; sp++) add(ld_ml(sp), ld_o(sp));
+        const float inv = 1.0f / tl;
+        const int64_t row = row0 + rr;
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x2_t ov = {pack2_bf16(a0 * inv, a1 * inv), pack2_bf16(a2 * inv, a3 * inv)};
+        __builtin_amdgcn_raw_buffer_store_b64(ov, rout, (uint32_t)(rr * D + c4) * 2u, 0, SC1);
+        if (lse && c4 == 0) lse[row] = mu * LN2 + logf(tl);
+    }
+#endif
+    if (threadIdx.x == 0) __hip_atomic_store(tickets + ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // key groups and keys per wave tile by head dim: both stage 32 KB of K and V
@@ -179,17 +284,17 @@ __host__ __device__ inline int row_splits(int n, int target) { return n <= targe
 // split and class c is query block nqb-1-c.
 constexpr int FLASH_MAX_CLS = 768;
 struct FlashWork {
-    int target;   // tiles per item
-    int bh;       // B * Hq
+    int target;            // tiles per item
+    int bh;                // B * Hq
     int ncls;
-    uint32_t cls[FLASH_MAX_CLS];  // qt | split << 16
+    const uint32_t* cls;   // device table [ncls]: qt | split << 16
 };
 
 template <int D>
 __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
     const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kg, const uint16_t* __restrict__ Vg, int Hq,
     int Hkv, int L, int S, float sl2, int causal, const FlashWork work, int nsplit, uint16_t* __restrict__ Og,
-    float* __restrict__ lse, float* __restrict__ part_o, float2* __restrict__ part_ml) {
+    float* __restrict__ lse, float* __restrict__ part_o, float2* __restrict__ part_ml, uint32_t* __restrict__ tickets) {
     constexpr int KG = FlashCfg<D>::KG;        // key groups
     constexpr int BKW = FlashCfg<D>::BKW;      // keys per wave tile
     constexpr int NH = BKW / 32;               // 32-key halves per wave tile
@@ -206,6 +311,7 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
     __shared__ __align__(16) uint16_t sK0[STAGE], sK1[STAGE];
     __shared__ __align__(16) uint16_t sV0[STAGE], sV1[STAGE];
     __shared__ float2 s_ml[KG / 2][2][64];
+    __shared__ uint32_t s_ticket;
     auto stK = [&](auto sc) -> uint16_t* {
         if constexpr (decltype(sc)::value == 0) return sK0; else return sK1;
     };
@@ -323,62 +429,58 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
 #pragma unroll
             for (int r = 0; r < 16; r++) sv[s2][r] = acc[r];
         }
-        if (k0 + BKW > S || (causal && k0 + BKW - 1 > qw0)) {
-#pragma unroll
-            for (int s2 = 0; s2 < NH; s2++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int key = k0 + 32 * s2 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                    if (key >= S || (causal && key > qi)) sv[s2][r] = -INFINITY;
-                }
-        }
-        // row maximum: independent max3 chains over 8 scores each
-        float mq[2 * NH];
-#pragma unroll
-        for (int g = 0; g < 2 * NH; g++) {
-            const float* v = &sv[g >> 1][8 * (g & 1)];
-            float a = max3f(v[0], v[1], v[2]);
-            a = max3f(a, v[3], v[4]);
-            a = max3f(a, v[5], v[6]);
-            mq[g] = max3f(a, v[7], v[7]);
-        }
-        float mx = NH == 2 ? max3f(max3f(mq[0], mq[1], mq[2]), mq[2 * NH - 1], mq[2 * NH - 1])
-                           : max3f(mq[0], mq[2 * NH - 1], mq[2 * NH - 1]);
-        mx = xor32_max(mx) * sl2;
-        const bool need = mx > m + RESCALE_SLACK;
-        if (__any(need)) {
-            const float mn = need ? mx : m;
-            const float alpha = __builtin_amdgcn_exp2f(m - mn);
-            l = l * alpha;
-#pragma unroll
-            for (int i = 0; i < D / 32; i++) o[i] = o[i] * alpha;
-            m = mn;
-        }
-        const float mu = (m == -INFINITY) ? 0.0f : m;
-        bf16x8 pf[NH][2];
-#pragma unroll
-        for (int s2 = 0; s2 < NH; s2++) {
-            float p[16];
-#pragma unroll
-            for (int r = 0; r < 16; r++) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[s2][r], sl2, -mu));
-            float ps = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; r += 4) ps = ps + ((p[r] + p[r + 1]) + (p[r + 2] + p[r + 3]));
-            l = l + ps;
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                pf[s2][j] = __builtin_bit_cast(
-                    bf16x8, make_uint4(pack2_bf16_hw(p[8 * j], p[8 * j + 1]), pack2_bf16_hw(p[8 * j + 2], p[8 * j + 3]),
-                                       pack2_bf16_hw(p[8 * j + 4], p[8 * j + 5]),
-                                       pack2_bf16_hw(p[8 * j + 6], p[8 * j + 7])));
-        }
+        // Online softmax per 32-key half: the half-1 S products (issued above)
+        // run on the matrix core while half 0's softmax runs on the VALU, and
+        // half 0's P.V products while half 1's softmax runs.
+        const bool edge = k0 + BKW > S || (causal && k0 + BKW - 1 > qw0);
         // V^T operand rows for this lane's 16-lane group: d = 32dt + 16*((lane>>4)&1) + (lane&15)
         const int gi = lane & 15;
         const int dcol = 16 * ((lane >> 4) & 1) + 4 * (gi & 3);  // source lane's 4 columns
 #pragma unroll
-        for (int dt = 0; dt < D / 32; dt++) {
+        for (int s2 = 0; s2 < NH; s2++) {
+            float* v = sv[s2];
+            if (edge) {
 #pragma unroll
-            for (int s2 = 0; s2 < NH; s2++) {
+                for (int r = 0; r < 16; r++) {
+                    const int key = k0 + 32 * s2 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    if (key >= S || (causal && key > qi)) v[r] = -INFINITY;
+                }
+            }
+            // half maximum: two independent max3 chains over 8 scores each
+            float a = max3f(v[0], v[1], v[2]);
+            a = max3f(a, v[3], v[4]);
+            a = max3f(a, v[5], v[6]);
+            float bm = max3f(v[8], v[9], v[10]);
+            bm = max3f(bm, v[11], v[12]);
+            bm = max3f(bm, v[13], v[14]);
+            float mx = max3f(max3f(a, v[7], v[15]), bm, bm);
+            mx = xor32_max(mx) * sl2;
+            const bool need = mx > m + RESCALE_SLACK;
+            if (__any(need)) {
+                const float mn = need ? mx : m;
+                const float alpha = __builtin_amdgcn_exp2f(m - mn);
+                l = l * alpha;
+#pragma unroll
+                for (int i = 0; i < D / 32; i++) o[i] = o[i] * alpha;
+                m = mn;
+            }
+            const float mu = (m == -INFINITY) ? 0.0f : m;
+            float p[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[r], sl2, -mu));
+            float ps = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r += 4) ps = ps + ((p[r] + p[r + 1]) + (p[r + 2] + p[r + 3]));
+            l = l + ps;
+            bf16x8 pf[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                pf[j] = __builtin_bit_cast(
+                    bf16x8, make_uint4(pack2_bf16_hw(p[8 * j], p[8 * j + 1]), pack2_bf16_hw(p[8 * j + 2], p[8 * j + 3]),
+                                       pack2_bf16_hw(p[8 * j + 4], p[8 * j + 5]),
+                                       pack2_bf16_hw(p[8 * j + 6], p[8 * j + 7])));
+#pragma unroll
+            for (int dt = 0; dt < D / 32; dt++) {
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
                     const int r0 = kr + 32 * s2 + 16 * j + 4 * hh + (gi >> 2);
@@ -387,7 +489,7 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
                     const uint2 lo = lds_read_tr16(tV + r0 * D + swz(r0, col >> 3) * 8 + (col & 7));
                     const uint2 hi = lds_read_tr16(tV + r1 * D + swz(r1, col >> 3) * 8 + (col & 7));
                     const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[s2][j], o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[j], o[dt], 0, 0, 0);
                 }
             }
         }
@@ -440,30 +542,35 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
             m = mm;
         }
     }
-    if (kg != 0 || qi >= L) return;
     const int64_t row = ((int64_t)b * Hq + h) * L + qi;
-    if (nsplit_row == 1) {
+    if (nsplit_row > 1) {
+        merge_split_rows<D>(part_o, part_ml, tickets, nsplit, split, nsplit_row, (int64_t)bh * L + q0,
+                            min(F3_BQ, L - q0), bh * nqb + qt, kg == 0 && qi < L, qi - q0, hh, o, m, l, Og, lse,
+                            s_ticket);
+        return;
+    }
+    if (kg != 0 || qi >= L) return;
+#if __HIP_DEVICE_COMPILE__
+    {
+        // written through to memory (sc1) as they are produced, so the
+        // output does not sit dirty in the L2s for the end-of-kernel writeback
+        const buf_rsrc ro = make_rsrc(Og + ((int64_t)bh * L + q0) * D, (uint32_t)(min(F3_BQ, L - q0) * D * 2));
+        const uint32_t rbase = (uint32_t)((qi - q0) * D) * 2u;
         const float inv = 1.0f / l;
-        uint16_t* op = Og + row * D;
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
-            for (int g4 = 0; g4 < 4; g4++)
+            for (int g4 = 0; g4 < 4; g4++) {
                 // O^T[d = 32dt + 8g4 + 4hh + e][q = lq]
-                *reinterpret_cast<uint2*>(op + 32 * dt + 8 * g4 + 4 * hh) =
-                    make_uint2(pack2_bf16(o[dt][4 * g4] * inv, o[dt][4 * g4 + 1] * inv),
-                               pack2_bf16(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv));
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                const u32x2_t v = {pack2_bf16(o[dt][4 * g4] * inv, o[dt][4 * g4 + 1] * inv),
+                                   pack2_bf16(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv)};
+                __builtin_amdgcn_raw_buffer_store_b64(v, ro, rbase + (uint32_t)(32 * dt + 8 * g4 + 4 * hh) * 2u, 0,
+                                                      16);
+            }
         if (lse && hh == 0) lse[row] = m * LN2 + logf(l);
-        return;
     }
-    float* po = part_o + (row * nsplit + split) * D;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; g4++)
-            *reinterpret_cast<float4*>(po + 32 * dt + 8 * g4 + 4 * hh) =
-                make_float4(o[dt][4 * g4], o[dt][4 * g4 + 1], o[dt][4 * g4 + 2], o[dt][4 * g4 + 3]);
-    if (hh == 0) part_ml[row * nsplit + split] = make_float2(m, l);
+#endif
 }
 
 constexpr int PF_BQ = 64, PF_BK = 64;
@@ -1222,12 +1329,15 @@ int64_t first_split_row(int64_t L, int64_t S, int causal, int bq, int bk, int ta
 }
 
 // Work list of the bf16 prefill (see FlashWork). Items aim at the tiles of
-// the whole call spread over 512 workgroups (two per CU), at least 16 tiles
-// each: a split costs a workgroup's start-up, about 2 us, and the partials it
-// writes and merges (measured on config 2: 16-tile items beat 8 to 12 and
-// whole rows), so rows that fit stay whole. Returns the number of workgroups
-// and the largest split count (the partial layout's stride).
-int64_t flash_work(int64_t B, int64_t Hq, int64_t L, int64_t S, int causal, FlashWork& w, int& nsplit) {
+// the whole call spread over the device's resident workgroups (two per CU),
+// at least 16 tiles (1024 keys) each: a split row costs its items a
+// published partial, a ticket and a merge at the end (about 4 us on gfx950),
+// so rows that fit stay whole. Timestamp sweeps of config 2 over items of
+// 8..32 tiles found 16-24 within a few percent of each other and 8 or 32
+// clearly slower. Returns the number of workgroups; `nsplit` gets the largest
+// split count (the partial layout's stride) and `table` the classes.
+int64_t flash_work(int64_t B, int64_t Hq, int64_t L, int64_t S, int causal, int slots, FlashWork& w, int& nsplit,
+                   std::vector<uint32_t>& table) {
     const int64_t nqb = cdiv(L, F3_BQ);
     auto ntiles = [&](int64_t qt) {
         return (int)cdiv(causal ? std::min<int64_t>(S, (qt + 1) * F3_BQ) : S, F3_BK);
@@ -1239,14 +1349,14 @@ int64_t flash_work(int64_t B, int64_t Hq, int64_t L, int64_t S, int causal, Flas
         total += ntiles(qt);
     }
     w.bh = (int)(B * Hq);
-    int target = (int)std::min<int64_t>(row_max, std::max<int64_t>(16, cdiv(total * B * Hq, 512)));
+    int target = (int)std::min<int64_t>(row_max, std::max<int64_t>(16, cdiv(total * B * Hq, slots)));
     std::vector<std::pair<int, uint32_t>> cls;  // (tiles, qt | split << 16)
     for (;;) {
         cls.clear();
         for (int64_t qt = nqb - 1; qt >= 0 && (int64_t)cls.size() <= FLASH_MAX_CLS; qt--) {
             const int n = ntiles(qt), ns = row_splits(n, target);
-            for (int s = 0; s < ns; s++)
-                cls.emplace_back((s + 1) * n / ns - s * n / ns, (uint32_t)qt | ((uint32_t)s << 16));
+            for (int sp = 0; sp < ns; sp++)
+                cls.emplace_back((sp + 1) * n / ns - sp * n / ns, (uint32_t)qt | ((uint32_t)sp << 16));
         }
         if (target >= row_max || (int64_t)cls.size() <= FLASH_MAX_CLS) break;
         target = std::min(row_max, target * 2);  // too many classes for the table: coarser items
@@ -1257,14 +1367,72 @@ int64_t flash_work(int64_t B, int64_t Hq, int64_t L, int64_t S, int causal, Flas
         nsplit = 1;
         return nqb * B * Hq;
     }
+    // longest first: the dispatcher hands out workgroups in order, and
+    // consecutive workgroups go to different XCDs
     std::stable_sort(cls.begin(), cls.end(), [](const auto& a, const auto& b) { return a.first > b.first; });
     w.ncls = (int)cls.size();
     nsplit = 1;
+    table.resize(cls.size());
     for (size_t i = 0; i < cls.size(); i++) {
-        w.cls[i] = cls[i].second;
+        table[i] = cls[i].second;
         nsplit = std::max(nsplit, (int)(cls[i].second >> 16) + 1);
     }
     return (int64_t)w.ncls * B * Hq;
+}
+
+// The work list of a shape, built once and kept in device memory for the
+// life of the process (a few KB per distinct (device, B*Hq, L, S, causal)):
+// the kernel reads its class with one scalar load, and a launch passes a
+// pointer instead of the table.
+struct PlanKey {
+    int dev;
+    int64_t bh, L, S;
+    int causal, D;
+    bool operator<(const PlanKey& o) const {
+        return std::tie(dev, bh, L, S, causal, D) < std::tie(o.dev, o.bh, o.L, o.S, o.causal, o.D);
+    }
+};
+struct Plan {
+    FlashWork w;
+    int nsplit;
+    int64_t nitems;
+};
+std::mutex g_plan_mu;
+std::map<PlanKey, Plan> g_plans;
+
+tn_status flash_plan(hipStream_t st, int64_t B, int64_t Hq, int64_t L, int64_t S, int causal, int D, int slots,
+                     Plan& out) {
+    int dev = 0;
+    TN_HIP(hipGetDevice(&dev));
+    const PlanKey key{dev, B * Hq, L, S, causal, D};
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    auto it = g_plans.find(key);
+    if (it != g_plans.end()) {
+        out = it->second;
+        return TN_OK;
+    }
+    Plan p{};
+    std::vector<uint32_t> table;
+    p.nitems = flash_work(B, Hq, L, S, causal, slots, p.w, p.nsplit, table);
+    p.w.cls = nullptr;
+    if (!table.empty()) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        TN_HIP(hipStreamIsCapturing(st, &cs));
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(TN_EINVAL, std::string(OP) + ": the first call of a shape cannot be captured (its work list "
+                                                     "is uploaded then); make one call before capturing");
+        uint32_t* d = nullptr;
+        TN_HIP(hipMalloc(reinterpret_cast<void**>(&d), table.size() * sizeof(uint32_t)));
+        const hipError_t e = hipMemcpy(d, table.data(), table.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(d);
+            return hip_fail(e, "hipMemcpy (prefill work list)");
+        }
+        p.w.cls = d;
+    }
+    g_plans[key] = p;
+    out = p;
+    return TN_OK;
 }
 
 }  // namespace
@@ -1320,46 +1488,50 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     if (dtype == TN_BF16) {
         // the key/value buffer descriptors cover one head's S*D elements
         if (S * D * 2 > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": key length too large");
-        FlashWork work;
-        int nsplit = 1;
-        const int64_t nitems = flash_work(B, Hq, L, S, c, work, nsplit);
+        // resident workgroups of the prefill kernel: the slots the schedule is planned over
+        int slots = 0;
+        tn_status sp = resident_workgroups(D == 64 ? reinterpret_cast<const void*>(&k_flash_bf16<64>)
+                                                    : reinterpret_cast<const void*>(&k_flash_bf16<128>),
+                                           128 * FlashCfg<64>::KG, 0, &slots);
+        if (sp != TN_OK) return sp;
+        Plan plan;
+        sp = flash_plan(st, B, Hq, L, S, c, (int)D, std::max(slots, 1), plan);
+        if (sp != TN_OK) return sp;
+        const FlashWork work = plan.w;
+        const int nsplit = plan.nsplit;
+        const int64_t nitems = plan.nitems;
         if (nitems > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": shape too large");
         float* part_o = nullptr;
         float2* part_ml = nullptr;
+        uint32_t* tick = nullptr;
         if (nsplit > 1) {
             const size_t po = (size_t)rows * nsplit * D * sizeof(float);
             const size_t pm = (size_t)rows * nsplit * sizeof(float2);
+            if ((size_t)F3_BQ * nsplit * D * sizeof(float) > UINT32_MAX)
+                return fail(TN_EVALUE, std::string(OP) + ": too many splits");
             void* ws = nullptr;
             tn_status s = workspace(st, po + pm, &ws);
             if (s != TN_OK) return s;
             part_o = static_cast<float*>(ws);
             part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + po);
+            // one counter per (batch, head, query block)
+            s = tickets(st, (size_t)(B * Hq) * (size_t)cdiv(L, F3_BQ), &tick);
+            if (s != TN_OK) return s;
         }
         auto qq = static_cast<const uint16_t*>(q);
         auto kk = static_cast<const uint16_t*>(k);
         auto vv = static_cast<const uint16_t*>(v);
         auto oo = static_cast<uint16_t*>(out);
+        // split rows are merged inside the kernel (merge_split_rows)
         if (D == 64)
             hipLaunchKernelGGL(k_flash_bf16<64>, dim3((unsigned)nitems), dim3(128 * FlashCfg<64>::KG), 0, st, qq, kk,
-                               vv, (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, work, nsplit, oo, lse, part_o, part_ml);
+                               vv, (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, work, nsplit, oo, lse, part_o, part_ml,
+                               tick);
         else
             hipLaunchKernelGGL(k_flash_bf16<128>, dim3((unsigned)nitems), dim3(128 * FlashCfg<128>::KG), 0, st, qq,
                                kk, vv, (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, work, nsplit, oo, lse, part_o,
-                               part_ml);
+                               part_ml, tick);
         TN_LAUNCHED();
-        if (nsplit > 1) {
-            const int64_t row_lo = first_split_row(L, S, c, F3_BQ, F3_BK, work.target);
-            const int64_t nrb = cdiv(L - row_lo, 256 / (D / 4));
-            if (nrb * B * Hq > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": shape too large");
-            const dim3 g2((unsigned)(nrb * B * Hq));
-            if (D == 64)
-                hipLaunchKernelGGL((k_prefill_combine<64, uint16_t>), g2, dim3(256), 0, st, part_o, part_ml, (int)L,
-                                   (int)S, c, F3_BQ, F3_BK, work.target, nsplit, (int)row_lo, (int)nrb, oo, lse);
-            else
-                hipLaunchKernelGGL((k_prefill_combine<128, uint16_t>), g2, dim3(256), 0, st, part_o, part_ml, (int)L,
-                                   (int)S, c, F3_BQ, F3_BK, work.target, nsplit, (int)row_lo, (int)nrb, oo, lse);
-            TN_LAUNCHED();
-        }
         return TN_OK;
     }
     const int bk = (D == 128) ? 32 : PF_BK;

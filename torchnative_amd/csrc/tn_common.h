@@ -33,6 +33,10 @@ Counters& counters();
 // Grow-only device workspace, one per (device, stream). Calls on one stream
 // are ordered, so reuse across them is safe.
 tn_status workspace(hipStream_t stream, size_t bytes, void** out);
+// Per-(device, stream) array of n uint32 counters, zero when first handed out
+// (cleared on the stream at allocation). A kernel that takes tickets from it
+// must leave every counter at zero again when it ends.
+tn_status tickets(hipStream_t stream, size_t n, uint32_t** out);
 // Workgroups of `kernel` (block threads, lds dynamic bytes) that the current
 // device holds at once: the size of a persistent grid, all of whose
 // workgroups must be resident from the start. Cached per (device, kernel,
