@@ -236,7 +236,7 @@ tn_status tn_kv_append(void* stream, const float* k, const float* v, int64_t m, 
  * MLP and the residual adds of modeling_llama.py around
  * `_quantized_linear`, quant.rs:286-369); the fusion saves the launches and
  * the round trips of the intermediate rows. y may alias resid (the decoder's
- * in-place residual), never x. k must be a multiple of 32, at most 32768. */
+ * in-place residual), never x. k must be a multiple of 32, at most 24576. */
 #define TN_PRO_NONE 0
 #define TN_PRO_RMSNORM 1
 #define TN_PRO_SILU 2

@@ -482,7 +482,7 @@ static tn_status check_model(const tn_llama* m) {
     if (m->vocab > INT32_MAX - ARGMAX_THREADS * ARGMAX_U || m->cap > INT32_MAX)
         return fail(TN_EVALUE, "tn_llama: shape too large");
     if (m->hidden % 32 != 0 || m->inter % 32 != 0 || m->hidden > LINEAR_DECODE_MAX_K || m->inter > LINEAR_DECODE_MAX_K)
-        return fail(TN_ENOTIMPL, "tn_llama: hidden and inter must be multiples of 32 and at most 32768");
+        return fail(TN_ENOTIMPL, "tn_llama: hidden and inter must be multiples of 32 and at most 24576");
     for (int64_t l = 0; l < m->n_layers; l++) {
         const tn_llama_layer& L = m->layers[l];
         if (!L.qkv.qs || !L.qkv.d || !L.o.qs || !L.o.d || !L.gate_up.qs || !L.gate_up.d || !L.down.qs ||

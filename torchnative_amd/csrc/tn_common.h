@@ -234,7 +234,7 @@ struct GemvPro {
 // po.eps; PRO_SILU reads x as [gate | up], 2k floats; PRO_COMBINE ignores x
 // and merges po's attention partials). Bit-identical to the separate ops in
 // sequence. y may alias resid, not x. k <= LINEAR_DECODE_MAX_K.
-constexpr int64_t LINEAR_DECODE_MAX_K = 32768;
+constexpr int64_t LINEAR_DECODE_MAX_K = 24576;  // 768 blocks: one per (row, block) item of the workgroup
 tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, const GemvPro& po, const uint8_t* qs,
                         const uint16_t* d, int64_t n, const float* resid, float* y);
 
