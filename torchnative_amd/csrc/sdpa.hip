@@ -209,7 +209,6 @@ __device__ __attribute__((always_inline)) inline void merge_split_rows(float* pa
     if (s_ticket != (uint32_t)(ns - 1)) return;  // uniform: another split merges the block
 #if __HIP_DEVICE_COMPILE__
     // thread -> (row, 4 columns), every split's loads in flight before any is used
-    const buf_rsrc rout = make_rsrc(Og + row0 * D, (uint32_t)(nrows * D * 2));
     constexpr int TPR = D / 4;
     constexpr int CMAX = 4;
     const int c4 = ((int)threadIdx.x % TPR) * 4;
@@ -251,9 +250,8 @@ __device__ __attribute__((always_inline)) inline void merge_split_rows(float* pa
         for (int sp = CMAX; sp < ns; sp++) add(ld_ml(sp), ld_o(sp));
         const float inv = 1.0f / tl;
         const int64_t row = row0 + rr;
-        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-        const u32x2_t ov = {pack2_bf16(a0 * inv, a1 * inv), pack2_bf16(a2 * inv, a3 * inv)};
-        __builtin_amdgcn_raw_buffer_store_b64(ov, rout, (uint32_t)(rr * D + c4) * 2u, 0, SC1);
+        *reinterpret_cast<uint2*>(Og + row * D + c4) =
+            make_uint2(pack2_bf16(a0 * inv, a1 * inv), pack2_bf16(a2 * inv, a3 * inv));
         if (lse && c4 == 0) lse[row] = mu * LN2 + logf(tl);
     }
 #endif
@@ -550,27 +548,17 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
         return;
     }
     if (kg != 0 || qi >= L) return;
-#if __HIP_DEVICE_COMPILE__
-    {
-        // written through to memory (sc1) as they are produced, so the
-        // output does not sit dirty in the L2s for the end-of-kernel writeback
-        const buf_rsrc ro = make_rsrc(Og + ((int64_t)bh * L + q0) * D, (uint32_t)(min(F3_BQ, L - q0) * D * 2));
-        const uint32_t rbase = (uint32_t)((qi - q0) * D) * 2u;
-        const float inv = 1.0f / l;
+    const float inv = 1.0f / l;
+    uint16_t* op = Og + row * D;
 #pragma unroll
-        for (int dt = 0; dt < D / 32; dt++)
+    for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
-            for (int g4 = 0; g4 < 4; g4++) {
-                // O^T[d = 32dt + 8g4 + 4hh + e][q = lq]
-                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-                const u32x2_t v = {pack2_bf16(o[dt][4 * g4] * inv, o[dt][4 * g4 + 1] * inv),
-                                   pack2_bf16(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv)};
-                __builtin_amdgcn_raw_buffer_store_b64(v, ro, rbase + (uint32_t)(32 * dt + 8 * g4 + 4 * hh) * 2u, 0,
-                                                      16);
-            }
-        if (lse && hh == 0) lse[row] = m * LN2 + logf(l);
-    }
-#endif
+        for (int g4 = 0; g4 < 4; g4++)
+            // O^T[d = 32dt + 8g4 + 4hh + e][q = lq]
+            *reinterpret_cast<uint2*>(op + 32 * dt + 8 * g4 + 4 * hh) =
+                make_uint2(pack2_bf16(o[dt][4 * g4] * inv, o[dt][4 * g4 + 1] * inv),
+                           pack2_bf16(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv));
+    if (lse && hh == 0) lse[row] = m * LN2 + logf(l);
 }
 
 constexpr int PF_BQ = 64, PF_BK = 64;
