@@ -509,6 +509,7 @@ __device__ inline uint32_t codes_pair01(uint32_t x) { return __builtin_amdgcn_pe
 __device__ inline uint32_t codes_pair23(uint32_t x) { return __builtin_amdgcn_perm(0x43434343u, x, 0x04030402u); }
 
 constexpr int GM_AS = QK + 8;  // LDS row stride (bf16) of the code tiles: 80 B, conflict-free b128 reads
+constexpr int GM_RS = 4;       // K blocks whose operands are in flight ahead of the one computed
 
 __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict__ xc,
                                                     const float* __restrict__ dxT,
@@ -542,58 +543,52 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    // per-thread staging registers
-    uint4 ra[2];
-    uint2 rb;
-    float rs0 = 0.0f, rs1 = 0.0f;
-    uint16_t rdw = 0;
+    // Per-thread staging registers, GM_RS register sets: block b's operands are
+    // requested GM_RS blocks before they are computed (about 1.7 us of
+    // memory latency against about 0.4 us of work per block), then stored to
+    // the LDS double buffer one block ahead. The set index is a compile-time
+    // constant (the K loop is unrolled by GM_RS), so the sets stay in VGPRs.
+    // one register set: two 16-byte chunks of activation codes, 8 bytes of
+    // weight nibbles, and (threads < GM_BM) the row's Q8_0 scale and
+    // accumulator start or (threads >= GM_BM) the column's f16 weight scale
     const int bcol = tid >> 1, bhalf = tid & 1;
-    auto gload = [&](int b) {
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int chunk = tid + c * GM_THREADS;
-            const int r = chunk >> 2, part = chunk & 3;
-            ra[c] = *reinterpret_cast<const uint4*>(xc + ((int64_t)(m0 + r) * nb + b) * QK + part * 8);
-        }
-        rb = make_uint2(0x88888888u, 0x88888888u);
-        if (n0 + bcol < N) rb = *reinterpret_cast<const uint2*>(qs + ((int64_t)(n0 + bcol) * nb + b) * 16 + bhalf * 8);
+    const int ar0 = tid >> 2, ar1 = (tid + GM_THREADS) >> 2, apart = tid & 3;  // the two A chunks
+    auto gload = [&](int b, uint4& a0, uint4& a1, uint2& w, float& dx, float& corr, uint32_t& dws) {
+        a0 = *reinterpret_cast<const uint4*>(xc + ((int64_t)(m0 + ar0) * nb + b) * QK + apart * 8);
+        a1 = *reinterpret_cast<const uint4*>(xc + ((int64_t)(m0 + ar1) * nb + b) * QK + apart * 8);
+        w = make_uint2(0x88888888u, 0x88888888u);
+        if (n0 + bcol < N) w = *reinterpret_cast<const uint2*>(qs + ((int64_t)(n0 + bcol) * nb + b) * 16 + bhalf * 8);
+        dx = corr = 0.0f;
+        dws = 0;
         if (tid < GM_BM) {
-            rs0 = dxT[(int64_t)b * M_pad + m0 + tid];
-            rs1 = corrT[(int64_t)b * M_pad + m0 + tid];
+            dx = dxT[(int64_t)b * M_pad + m0 + tid];
+            corr = corrT[(int64_t)b * M_pad + m0 + tid];
         } else {
             const int n = n0 + tid - GM_BM;
-            rdw = (n < N) ? dw[(int64_t)n * nb + b] : (uint16_t)0;
+            dws = (n < N) ? dw[(int64_t)n * nb + b] : 0u;
         }
     };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int chunk = tid + c * GM_THREADS;
-            const int r = chunk >> 2, part = chunk & 3;
-            *reinterpret_cast<uint4*>(&sA[buf][r * GM_AS + part * 8]) = ra[c];
-        }
+    auto lstore = [&](int buf, const uint4& a0, const uint4& a1, const uint2& w, float dx, float corr,
+                      uint32_t dws) {
+        *reinterpret_cast<uint4*>(&sA[buf][ar0 * GM_AS + apart * 8]) = a0;
+        *reinterpret_cast<uint4*>(&sA[buf][ar1 * GM_AS + apart * 8]) = a1;
         // weight dwords g = 2*bhalf, 2*bhalf+1 -> K slots 8g..8g+7 each
-        const uint32_t w0 = rb.x, w1 = rb.y;
+        const uint32_t w0 = w.x, w1 = w.y;
         const uint32_t lo0 = w0 & 0x0f0f0f0fu, hi0 = (w0 >> 4) & 0x0f0f0f0fu;
         const uint32_t lo1 = w1 & 0x0f0f0f0fu, hi1 = (w1 >> 4) & 0x0f0f0f0fu;
         uint4* dst = reinterpret_cast<uint4*>(&sB[buf][bcol * GM_AS + bhalf * 16]);
         dst[0] = make_uint4(codes_pair01(lo0), codes_pair23(lo0), codes_pair01(hi0), codes_pair23(hi0));
         dst[1] = make_uint4(codes_pair01(lo1), codes_pair23(lo1), codes_pair01(hi1), codes_pair23(hi1));
         if (tid < GM_BM) {
-            sdx[buf][tid] = rs0;
-            scr[buf][tid] = rs1;
+            sdx[buf][tid] = dx;
+            scr[buf][tid] = corr;
         } else {
-            sdw[buf][tid - GM_BM] = f16_to_f32(rdw);
+            sdw[buf][tid - GM_BM] = f16_bits_hw((uint16_t)dws);
         }
     };
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int b = 0; b < nb; b++) {
-        const int buf = b & 1;
-        if (b + 1 < nb) gload(b + 1);
-
+    // one K block from LDS buffer `buf`: the exact block dot on MFMA, then
+    // the reference's two roundings and the ordered addition
+    auto compute = [&](int buf) {
         bf16x8 afr[4], bfr[4];
 #pragma unroll
         for (int i = 0; i < 4; i++)
@@ -610,25 +605,52 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
             dxv[i] = *reinterpret_cast<const f32x4*>(&sdx[buf][wm * 64 + i * 16 + lgrp * 4]);
             crv[i] = *reinterpret_cast<const f32x4*>(&scr[buf][wm * 64 + i * 16 + lgrp * 4]);
         }
-
 #pragma unroll
         for (int i = 0; i < 4; i++) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 // C[row][col]: col = lane & 15 (weight column), row = 4*(lane>>4) + r;
                 // A = activation rows, B = weight columns; C starts at -136*sum(x codes)
-                const f32x4 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[i], bfr[j], crv[i], 0, 0, 0);
+                const f32x4 sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[i], bfr[j], crv[i], 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    float t = s[r] * dwv[j];
+                    float t = sv[r] * dwv[j];
                     t = t * dxv[i][r];
                     acc[i][j][r] = acc[i][j][r] + t;
                 }
             }
         }
-        if (b + 1 < nb) lstore(buf ^ 1);
-        __syncthreads();
+    };
+    // Four register sets, named: step b refills set b % 4 with block b + 4
+    // (set b's data went to LDS at the end of step b - 1), computes block b,
+    // and stores block b + 1 to the other LDS buffer.
+    uint4 a0_0, a1_0, a0_1, a1_1, a0_2, a1_2, a0_3, a1_3;
+    uint2 w_0, w_1, w_2, w_3;
+    float dx_0, dx_1, dx_2, dx_3, cr_0, cr_1, cr_2, cr_3;
+    uint32_t dw_0, dw_1, dw_2, dw_3;
+    static_assert(GM_RS == 4, "the unrolled K loop below names four register sets");
+#define TN_GM_SET(S) a0_##S, a1_##S, w_##S, dx_##S, cr_##S, dw_##S
+#define TN_GM_STEP(S, NEXT, B)                                    \
+    {                                                             \
+        if ((B) + GM_RS < nb) gload((B) + GM_RS, TN_GM_SET(S));   \
+        compute((B)&1);                                           \
+        if ((B) + 1 < nb) lstore(((B) + 1) & 1, TN_GM_SET(NEXT)); \
+        __syncthreads();                                          \
     }
+    gload(0, TN_GM_SET(0));
+    if (1 < nb) gload(1, TN_GM_SET(1));
+    if (2 < nb) gload(2, TN_GM_SET(2));
+    if (3 < nb) gload(3, TN_GM_SET(3));
+    lstore(0, TN_GM_SET(0));
+    __syncthreads();
+    for (int b = 0; b < nb; b += GM_RS) {
+        TN_GM_STEP(0, 1, b)
+        if (b + 1 < nb) TN_GM_STEP(1, 2, b + 1)
+        if (b + 2 < nb) TN_GM_STEP(2, 3, b + 2)
+        if (b + 3 < nb) TN_GM_STEP(3, 0, b + 3)
+    }
+#undef TN_GM_STEP
+#undef TN_GM_SET
 
 #pragma unroll
     for (int i = 0; i < 4; i++) {
