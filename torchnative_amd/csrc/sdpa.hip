@@ -1154,16 +1154,39 @@ __global__ __launch_bounds__(D) void k_decode_combine(const float* __restrict__ 
                                                     const int32_t* __restrict__ lens, int Hq, int cap, int nsplit,
                                                     OT* __restrict__ out, float* __restrict__ lse) {
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const int64_t base = ((int64_t)b * Hq + h) * nsplit;
+    // the first CMAX splits' partials are requested before the length is
+    // known (one round trip for both); splits past it are not used
+    constexpr int CMAX = 16;
+    float2 mlv[CMAX];
+    float pv[CMAX];
+#pragma unroll
+    for (int s = 0; s < CMAX; s++) {
+        if (s < nsplit) {
+            mlv[s] = part_ml[base + s];
+            pv[s] = part_o[(base + s) * D + d];
+        }
+    }
     int len = lens[b];
     len = len < 0 ? 0 : (len > cap ? cap : len);
     int ns = (len + DEC_SPLIT - 1) / DEC_SPLIT;
     ns = ns < nsplit ? ns : nsplit;  // a length above max_len is truncated, never read past
-    const int64_t base = ((int64_t)b * Hq + h) * nsplit;
     float mm = -INFINITY;
-    for (int s = 0; s < ns; s++) mm = fmaxf(mm, part_ml[base + s].x);
+#pragma unroll
+    for (int s = 0; s < CMAX; s++)
+        if (s < ns) mm = fmaxf(mm, mlv[s].x);
+    for (int s = CMAX; s < ns; s++) mm = fmaxf(mm, part_ml[base + s].x);
     const float mu = (mm == -INFINITY) ? 0.0f : mm;
     float tl = 0.0f, acc = 0.0f;
-    for (int s = 0; s < ns; s++) {
+#pragma unroll
+    for (int s = 0; s < CMAX; s++) {
+        if (s < ns) {
+            const float f = exp2f(mlv[s].x - mu);
+            tl = tl + mlv[s].y * f;
+            acc = acc + pv[s] * f;
+        }
+    }
+    for (int s = CMAX; s < ns; s++) {
         const float2 ml = part_ml[base + s];
         const float f = exp2f(ml.x - mu);
         tl = tl + ml.y * f;
