@@ -146,7 +146,10 @@ tn_status tn_q4_0_linear(void* stream, const void* x, int x_dtype, int64_t m, in
  *   materialised (aten.rs:17106-17126); Hq % Hkv != 0 is refused by name.
  *   is_causal: upper-left aligned, row t attends keys 0..=t (aten.rs:10038-10041).
  *   attn_mask: nullable, [B,Hq,L,S] dense additive, in `mask_dtype` (the query
- *   dtype or TN_F32, aten.rs:10142-10148), added after scaling.
+ *   dtype or TN_F32, aten.rs:10142-10148; others are refused with the
+ *   reference's wording), added after scaling (aten.rs:10383-10389). A row
+ *   whose every key is masked gives NaN in out and lse, as the reference's
+ *   row-max shift does (aten.rs:10392-10420).
  *   scale: NaN selects 1/sqrt(D) (aten.rs:10216).
  *   out: [B,Hq,L,D] in `dtype` (row-major, aten.rs:10436-10437);
  *   lse: nullable f32 [B,Hq,L], logsumexp over the masked, scaled scores.

@@ -68,16 +68,19 @@ def test_sdpa_refusals_name_the_reason(L):
 
     args = dict(B=1, Hq=9, Hkv=3, L=8, S=8, D=64)
 
-    def call(dtype=_lib.TN_BF16, mask=None, **kw):
+    def call(dtype=_lib.TN_BF16, mask=None, mask_dtype=0, **kw):
         a = {**args, **kw}
         return L.tn_sdpa_fwd(None, dtype, None, None, None, a["B"], a["Hq"], a["Hkv"], a["L"], a["S"], a["D"],
-                             mask, 0, 1, float("nan"), None, None)
+                             mask, mask_dtype, 1, float("nan"), None, None)
 
     assert call(D=16) == _lib.TN_ENOTIMPL and "head_dim 16" in _lib.last_error()
     assert call(Hkv=4) == _lib.TN_ENOTIMPL and "do not divide" in _lib.last_error()
     assert call(S=0) == _lib.TN_ENOTIMPL and "zero key length" in _lib.last_error()
     assert call(dtype=_lib.TN_F64) == _lib.TN_ENOTIMPL and "Double" in _lib.last_error()
-    assert call(mask=1) == _lib.TN_ENOTIMPL and "attn_mask" in _lib.last_error()
+    # the mask is the query's dtype or float32 (aten.rs:10142-10150)
+    assert call(mask=1, mask_dtype=_lib.TN_F16) == _lib.TN_EINVAL
+    assert "Attention mask is the same data type as query" in _lib.last_error()
+    assert call(dtype=_lib.TN_F32, mask=1, mask_dtype=_lib.TN_BF16) == _lib.TN_EINVAL
     # empty batch: nothing to write, success without touching a pointer
     assert call(B=0) == _lib.TN_OK
     st = L.tn_sdpa_decode(None, _lib.TN_BF16, None, None, None, 2, 32, 8, 64, 128, None, 65, float("nan"),

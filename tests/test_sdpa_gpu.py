@@ -174,3 +174,83 @@ def test_config4_decode_attention_at_full_size(tn):
     lens = [int(x) for x in rng.integers(512, 4097, size=16)]
     worst = _decode_case(tn, 16, 32, 8, 128, lens, 4096, 44)
     print(f"config 4: worst error {worst:.3f} of the bound", flush=True)
+
+
+def _check_masked(tn, dtype, q, k, v, mask, mask_dtype, causal=False, nan_rows=()):
+    """An additive mask (aten.rs:10383-10389) against the oracle, same bound
+    as the unmasked runs. `mask` may be any shape broadcastable to
+    [B, Hq, L, S]; rows listed in nan_rows are fully masked and must be NaN
+    in out and lse, as the reference's are (aten.rs:10392-10420)."""
+    B, Hq, L, D = q.shape
+    S = k.shape[2]
+    if dtype == "bfloat16":
+        qt, kt, vt = (tn.tensor(a.astype(np.float32), dtype="bfloat16", device="hip") for a in (q, k, v))
+    else:
+        qt, kt, vt = (tn.tensor(a.astype(np.float32), device="hip") for a in (q, k, v))
+    mt = tn.tensor(mask.astype(np.float32), dtype=mask_dtype, device="hip")
+    o, lse = tn._aten_dispatch(OP, qt, kt, vt, 0.0, causal, attn_mask=mt)
+    qw, kw, vw = (t.numpy().astype(np.float64) for t in (qt, kt, vt))
+    mw = np.ascontiguousarray(np.broadcast_to(mt.numpy().astype(np.float64), (B, Hq, L, S)))
+    with np.errstate(invalid="ignore"):
+        r32, l32 = O.sdpa(qw, kw, vw, mask=mw, is_causal=causal, threads=16)
+        r64, l64 = O.sdpa(qw, kw, vw, mask=mw, is_causal=causal, threads=16, dtype=np.float64)
+        pav = O.sdpa(qw, kw, np.abs(vw), mask=mw, is_causal=causal, threads=16, dtype=np.float64)[0] \
+            if dtype == "bfloat16" else None
+    got, gl = o.numpy().astype(np.float64), lse.numpy().astype(np.float64)
+    nan = np.zeros((B, Hq, L), bool)
+    for (b, h, i) in nan_rows:
+        nan[b, h, i] = True
+    assert np.array_equal(np.isnan(got).any(axis=-1), nan) and np.all(np.isnan(got[nan]))
+    assert np.array_equal(np.isnan(gl), nan)
+    keep = ~nan
+    if dtype == "bfloat16":
+        ref = O.bf16_to_f32(O.bf16_from_f32(r32)).astype(np.float64)
+        tol = _bound(r32[keep], r64[keep], pav[keep], bf16=True, got=got[keep])
+    else:
+        ref = r32.astype(np.float64)
+        tol = _bound(r32[keep], r64[keep])
+    worst = float(np.max(np.abs(got[keep] - ref[keep]) / tol))
+    assert worst <= 1.0, f"{dtype} mask {mask_dtype} causal={causal}: {worst:.3g}x the bound"
+    lt = _bound(l32[keep], l64[keep])
+    assert float(np.max(np.abs(gl[keep] - l32[keep]) / lt)) <= 1.0
+
+
+@pytest.mark.parametrize("dtype,mask_dtype,D,causal", [
+    ("bfloat16", "float32", 64, False), ("bfloat16", "bfloat16", 64, True), ("bfloat16", "float32", 128, True),
+    ("float32", "float32", 64, True), ("float32", "float32", 128, False)])
+def test_additive_mask_within_the_derived_bound(tn, dtype, mask_dtype, D, causal):
+    rng = np.random.default_rng(D + int(causal))
+    B, Hq, Hkv, L, S = 2, 4, 2, 70, 90
+    q, k, v = (rng.standard_normal(s) for s in ((B, Hq, L, D), (B, Hkv, S, D), (B, Hkv, S, D)))
+    mask = rng.standard_normal((B, Hq, L, S)) * 2
+    mask[rng.random(mask.shape) < 0.1] = -np.inf  # a sprinkle of masked keys (never a whole row here)
+    mask[:, :, :, 0] = 0.0
+    _check_masked(tn, dtype, q, k, v, mask, mask_dtype, causal)
+
+
+def test_broadcast_mask_and_fully_masked_rows(tn):
+    rng = np.random.default_rng(7)
+    B, Hq, Hkv, L, S, D = 1, 3, 1, 40, 65, 64
+    q, k, v = (rng.standard_normal(s) for s in ((B, Hq, L, D), (B, Hkv, S, D), (B, Hkv, S, D)))
+    mask = np.where(rng.random((L, S)) < 0.3, -np.inf, 0.0)  # [L, S], broadcast over batch and heads
+    mask[:, 5] = 0.0
+    mask[17, :] = -np.inf  # row 17 of every head sees no key
+    _check_masked(tn, "bfloat16", q, k, v, mask, "float32", nan_rows=[(0, h, 17) for h in range(Hq)])
+
+
+def test_mask_on_split_rows_merged_in_kernel(tn):
+    """Rows of 2048 keys are split across workgroups and merged inside the
+    kernel; the mask is applied in every split."""
+    rng = np.random.default_rng(9)
+    B, Hq, Hkv, L, S, D = 1, 2, 1, 128, 2048, 64
+    q, k, v = (rng.standard_normal(s) for s in ((B, Hq, L, D), (B, Hkv, S, D), (B, Hkv, S, D)))
+    mask = rng.standard_normal((B, Hq, L, S))
+    mask[:, :, :, 1024:1500] = -np.inf
+    _check_masked(tn, "bfloat16", q, k, v, mask, "bfloat16")
+
+
+def test_mask_dtype_rule(tn):
+    qt = tn.tensor(np.zeros((1, 1, 4, 64), np.float32), device="hip")
+    mt = tn.tensor(np.zeros((1, 1, 4, 4), np.float32), dtype="bfloat16", device="hip")
+    with pytest.raises(RuntimeError, match="Attention mask is the same data type as query"):
+        tn._aten_dispatch(OP, qt, qt, qt, 0.0, False, attn_mask=mt)

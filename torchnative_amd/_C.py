@@ -260,6 +260,15 @@ def _scaled_dot_product_flash_attention(query: Tensor, key: Tensor, value: Tenso
         if t.shape[0] != B or t.shape[2] != S or t.shape[3] != D or t.shape[1] != Hkv:
             raise RuntimeError(f"{op}: query {list(query.shape)} and {name} {list(t.shape)} do not describe one "
                                "attention -- batch, key length and head dimension all have to agree")
+    if attn_mask is not None and tuple(attn_mask.shape) != (B, Hq, L, S):
+        # the kernels read a dense [B, Hq, L, S] mask: a broadcastable one is
+        # materialised first, as the reference's own path does (aten.rs:10293-10303)
+        try:
+            full = np.broadcast_to(attn_mask.bits(), (B, Hq, L, S))
+        except ValueError:
+            raise RuntimeError(f"{op}: attn_mask of shape {list(attn_mask.shape)} cannot be broadcast to "
+                               f"[{B}, {Hq}, {L}, {S}]") from None
+        attn_mask = Tensor.from_numpy(np.ascontiguousarray(full), dtype=attn_mask.dtype, device="hip")
     out = Tensor((B, Hq, L, D), query.dtype, "hip")
     lse = Tensor((B, Hq, L), "float32", "hip")
     sc = float("nan") if scale is None else float(scale)

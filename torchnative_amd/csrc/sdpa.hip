@@ -252,7 +252,7 @@ __device__ __attribute__((always_inline)) inline void merge_split_rows(float* pa
         const int64_t row = row0 + rr;
         *reinterpret_cast<uint2*>(Og + row * D + c4) =
             make_uint2(pack2_bf16(a0 * inv, a1 * inv), pack2_bf16(a2 * inv, a3 * inv));
-        if (lse && c4 == 0) lse[row] = mu * LN2 + logf(tl);
+        if (lse && c4 == 0) lse[row] = mm == -INFINITY ? NAN : mu * LN2 + logf(tl);  // a fully masked row is NaN (aten.rs:10392-10420)
     }
 #endif
     if (threadIdx.x == 0) __hip_atomic_store(tickets + ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -288,11 +288,14 @@ struct FlashWork {
     const uint32_t* cls;   // device table [ncls]: qt | split << 16
 };
 
-template <int D>
+// MASK: 0 none; 1 an f32 additive mask; 2 a bf16 one, dense [B, Hq, L, S]
+// (aten.rs:10383-10389: added to the scaled scores before the row maximum)
+template <int D, int MASK = 0>
 __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
     const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kg, const uint16_t* __restrict__ Vg, int Hq,
     int Hkv, int L, int S, float sl2, int causal, const FlashWork work, int nsplit, uint16_t* __restrict__ Og,
-    float* __restrict__ lse, float* __restrict__ part_o, float2* __restrict__ part_ml, uint32_t* __restrict__ tickets) {
+    float* __restrict__ lse, float* __restrict__ part_o, float2* __restrict__ part_ml, uint32_t* __restrict__ tickets,
+    const void* __restrict__ mask) {
     constexpr int KG = FlashCfg<D>::KG;        // key groups
     constexpr int BKW = FlashCfg<D>::BKW;      // keys per wave tile
     constexpr int NH = BKW / 32;               // 32-key halves per wave tile
@@ -431,12 +434,32 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
         // run on the matrix core while half 0's softmax runs on the VALU, and
         // half 0's P.V products while half 1's softmax runs.
         const bool edge = k0 + BKW > S || (causal && k0 + BKW - 1 > qw0);
+        const float scl = MASK ? 1.0f : sl2;  // scores' factor to log2 units
         // V^T operand rows for this lane's 16-lane group: d = 32dt + 16*((lane>>4)&1) + (lane&15)
         const int gi = lane & 15;
         const int dcol = 16 * ((lane >> 4) & 1) + 4 * (gi & 3);  // source lane's 4 columns
 #pragma unroll
         for (int s2 = 0; s2 < NH; s2++) {
             float* v = sv[s2];
+            if constexpr (MASK != 0) {
+                // scores to log2 units with the mask added: raw*scale*log2e + mask*log2e;
+                // from here on the scale is 1
+                if (qi < L) {
+                    const int64_t mrow = ((int64_t)bh * L + qi) * S;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int key = k0 + 32 * s2 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                        float mv = 0.0f;
+                        if (key < S) {
+                            if constexpr (MASK == 1)
+                                mv = reinterpret_cast<const float*>(mask)[mrow + key];
+                            else
+                                mv = bf16_to_f32(reinterpret_cast<const uint16_t*>(mask)[mrow + key]);
+                        }
+                        v[r] = v[r] * sl2 + mv * LOG2E;
+                    }
+                }
+            }
             if (edge) {
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
@@ -452,11 +475,12 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
             bm = max3f(bm, v[11], v[12]);
             bm = max3f(bm, v[13], v[14]);
             float mx = max3f(max3f(a, v[7], v[15]), bm, bm);
-            mx = xor32_max(mx) * sl2;
+            mx = xor32_max(mx) * scl;
             const bool need = mx > m + RESCALE_SLACK;
             if (__any(need)) {
                 const float mn = need ? mx : m;
-                const float alpha = __builtin_amdgcn_exp2f(m - mn);
+                // a row with no key seen yet keeps m = mn = -inf: alpha 1, not 2^NaN
+                const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
                 l = l * alpha;
 #pragma unroll
                 for (int i = 0; i < D / 32; i++) o[i] = o[i] * alpha;
@@ -465,7 +489,7 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
             const float mu = (m == -INFINITY) ? 0.0f : m;
             float p[16];
 #pragma unroll
-            for (int r = 0; r < 16; r++) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[r], sl2, -mu));
+            for (int r = 0; r < 16; r++) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[r], scl, -mu));
             float ps = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; r += 4) ps = ps + ((p[r] + p[r + 1]) + (p[r + 2] + p[r + 3]));
@@ -558,7 +582,7 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
             *reinterpret_cast<uint2*>(op + 32 * dt + 8 * g4 + 4 * hh) =
                 make_uint2(pack2_bf16(o[dt][4 * g4] * inv, o[dt][4 * g4 + 1] * inv),
                            pack2_bf16(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv));
-    if (lse && hh == 0) lse[row] = m * LN2 + logf(l);
+    if (lse && hh == 0) lse[row] = m == -INFINITY ? NAN : m * LN2 + logf(l);
 }
 
 constexpr int PF_BQ = 64, PF_BK = 64;
@@ -573,12 +597,14 @@ constexpr int PF_BQ = 64, PF_BK = 64;
 // hit 64 distinct banks.
 // ---------------------------------------------------------------------------
 
-template <int D, int BK>
+// MASK: 1 adds a dense f32 [B, Hq, L, S] mask to the scaled scores (aten.rs:10383-10389)
+template <int D, int BK, int MASK = 0>
 __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, const float* __restrict__ Kg,
                                               const float* __restrict__ Vg, int Hq, int Hkv, int L, int S,
                                               float sl2, int causal, int tiles_per, int nsplit,
                                               float* __restrict__ Og, float* __restrict__ lse,
-                                              float* __restrict__ part_o, float2* __restrict__ part_ml) {
+                                              float* __restrict__ part_o, float2* __restrict__ part_ml,
+                                              const float* __restrict__ mask) {
     constexpr int BQ = PF_BQ;
     constexpr int RS = D + 4;
     constexpr int CH = (BK * D / 4) / 256;  // float4 chunks of K (and of V) per thread
@@ -653,6 +679,21 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
 #pragma unroll
             for (int c = 0; c < D / 4; c++) s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(krow[4 * c], qf[c], s[kt], 0, 0, 0);
         }
+        if constexpr (MASK != 0) {
+            // scores to log2 units with the mask added; from here on the scale is 1
+            if (qi < L) {
+                const int64_t mrow = (((int64_t)b * Hq + h) * L + qi) * S;
+#pragma unroll
+                for (int kt = 0; kt < BK / 16; kt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int key = k0 + 16 * kt + 4 * g + r;
+                        const float mv = key < S ? mask[mrow + key] : 0.0f;
+                        s[kt][r] = s[kt][r] * sl2 + mv * LOG2E;
+                    }
+            }
+        }
+        const float scl = MASK ? 1.0f : sl2;  // scores' factor to log2 units
         if (k0 + BK > S || (causal && k0 + BK - 1 > q0 + w * 16)) {
 #pragma unroll
             for (int kt = 0; kt < BK / 16; kt++)
@@ -666,11 +707,11 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
 #pragma unroll
         for (int kt = 0; kt < BK / 16; kt++)
             mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
-        mx = wave_xor_max(mx) * sl2;
+        mx = wave_xor_max(mx) * scl;
         const bool need = mx > m + RESCALE_SLACK;
         if (__any(need)) {
             const float mn = need ? mx : m;
-            const float alpha = exp2f(m - mn);
+            const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);  // no key seen yet: 1, not 2^NaN
             l = l * alpha;
 #pragma unroll
             for (int i = 0; i < D / 16; i++) o[i] = o[i] * alpha;
@@ -681,7 +722,7 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
         for (int kt = 0; kt < BK / 16; kt++) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float p = exp2f(__builtin_fmaf(s[kt][r], sl2, -mu));
+                const float p = exp2f(__builtin_fmaf(s[kt][r], scl, -mu));
                 l = l + p;
                 const float* vrow = &sV[buf][(16 * kt + 4 * g + r) * RS + lq];
 #pragma unroll
@@ -703,7 +744,7 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
         for (int dt = 0; dt < D / 16; dt++)
             *reinterpret_cast<float4*>(op + 16 * dt + 4 * g) =
                 make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
-        if (lse && g == 0) lse[row] = m * LN2 + logf(l);
+        if (lse && g == 0) lse[row] = m == -INFINITY ? NAN : m * LN2 + logf(l);
     } else {
         float* po = part_o + (row * nsplit + split) * D;
 #pragma unroll
@@ -772,7 +813,7 @@ __global__ __launch_bounds__(256) void k_prefill_combine(const float* __restrict
                                                                    pack2_bf16(a2 * inv, a3 * inv));
     else
         *reinterpret_cast<float4*>(out + row * D + c4) = make_float4(a0 * inv, a1 * inv, a2 * inv, a3 * inv);
-    if (lse && c4 == 0) lse[row] = mu * LN2 + logf(tl);
+    if (lse && c4 == 0) lse[row] = mm == -INFINITY ? NAN : mu * LN2 + logf(tl);
 }
 
 // ---------------------------------------------------------------------------
@@ -1481,11 +1522,12 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
                       OP, (long long)Hq, (long long)Hkv);
         return fail(TN_ENOTIMPL, buf);
     }
-    if (attn_mask) {
-        (void)mask_dtype;
-        return fail(TN_ENOTIMPL, std::string(OP) + ": an attn_mask is not implemented on the hip device yet "
-                                                   "(is_causal is); pass the mask to the CPU device");
-    }
+    // the mask is the query's dtype or float32 (aten.rs:10142-10150)
+    if (attn_mask && mask_dtype != dtype && mask_dtype != TN_F32)
+        return fail(TN_EINVAL, "scaled_dot_product_attention_flash_attention: Attention mask is the same data type "
+                               "as query");
+    // 0 none, 1 f32, 2 bf16: the kernels' MASK parameter
+    const int mk = !attn_mask ? 0 : mask_dtype == TN_F32 ? 1 : 2;
     if (D != 64 && D != 128) return refuse_head_dim(D);
     if (B * Hq * L == 0) return TN_OK;  // nothing to write (aten.rs:10242-10259 returns empty zeros)
     if (!q || !k || !v || !out) return fail(TN_EVALUE, std::string(OP) + ": null pointer");
@@ -1534,14 +1576,20 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         auto vv = static_cast<const uint16_t*>(v);
         auto oo = static_cast<uint16_t*>(out);
         // split rows are merged inside the kernel (merge_split_rows)
-        if (D == 64)
-            hipLaunchKernelGGL(k_flash_bf16<64>, dim3((unsigned)nitems), dim3(128 * FlashCfg<64>::KG), 0, st, qq, kk,
-                               vv, (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, work, nsplit, oo, lse, part_o, part_ml,
-                               tick);
-        else
-            hipLaunchKernelGGL(k_flash_bf16<128>, dim3((unsigned)nitems), dim3(128 * FlashCfg<128>::KG), 0, st, qq,
-                               kk, vv, (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, work, nsplit, oo, lse, part_o,
-                               part_ml, tick);
+#define TN_FLASH(DD, MK)                                                                                            \
+    hipLaunchKernelGGL((k_flash_bf16<DD, MK>), dim3((unsigned)nitems), dim3(128 * FlashCfg<DD>::KG), 0, st, qq, kk, \
+                       vv, (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, work, nsplit, oo, lse, part_o, part_ml, tick,   \
+                       attn_mask)
+        if (D == 64) {
+            if (mk == 0) TN_FLASH(64, 0);
+            else if (mk == 1) TN_FLASH(64, 1);
+            else TN_FLASH(64, 2);
+        } else {
+            if (mk == 0) TN_FLASH(128, 0);
+            else if (mk == 1) TN_FLASH(128, 1);
+            else TN_FLASH(128, 2);
+        }
+#undef TN_FLASH
         TN_LAUNCHED();
         return TN_OK;
     }
@@ -1568,12 +1616,22 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         auto kk = static_cast<const float*>(k);
         auto vv = static_cast<const float*>(v);
         auto oo = static_cast<float*>(out);
-        if (D == 64)
-            hipLaunchKernelGGL((k_fa_f32<64, 64>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
-                               (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml);
-        else
-            hipLaunchKernelGGL((k_fa_f32<128, 32>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
-                               (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml);
+        auto mm = static_cast<const float*>(attn_mask);  // an f32 query takes an f32 mask only
+        if (D == 64) {
+            if (mk)
+                hipLaunchKernelGGL((k_fa_f32<64, 64, 1>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv,
+                                   (int)L, (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml, mm);
+            else
+                hipLaunchKernelGGL((k_fa_f32<64, 64>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
+                                   (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml, nullptr);
+        } else {
+            if (mk)
+                hipLaunchKernelGGL((k_fa_f32<128, 32, 1>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv,
+                                   (int)L, (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml, mm);
+            else
+                hipLaunchKernelGGL((k_fa_f32<128, 32>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
+                                   (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml, nullptr);
+        }
         TN_LAUNCHED();
         if (nsplit > 1) {
             const int64_t row_lo = first_split_row(L, S, c, PF_BQ, bk, tiles_per);
