@@ -137,6 +137,34 @@ tn_status tn_q4_0_linear(void* stream, const void* x, int x_dtype, int64_t m, in
                          const uint8_t* qs, const uint16_t* d, int64_t n, const float* bias,
                          void* y, int y_dtype);
 
+/* ---- GGML q8_0 weights ----
+ * The other block format `_quantize` takes whose VecDotType is Q8_0
+ * (k_quants.rs:652-757). Same two-plane layout as q4_0 with 32 code bytes
+ * per block:
+ *   qs: N * nb * 32 int8 codes, block (n, b) at byte (n*nb + b)*32, element j
+ *       at byte j (the 34-byte GGML block minus its scale);
+ *   d : N * nb f16 scales, d[n*nb + b].
+ * Each function is its q4_0 namesake's counterpart, with the same refusals:
+ *   from_blob / to_blob: the device half of `_quantized_to` / `_quantized_blob`
+ *     (quant.rs:384-405, :213-221), byte for byte;
+ *   quantize: BlockQ8_0::from_float (k_quants.rs:676-705) on w f32 [n, k];
+ *   dequantize: BlockQ8_0::to_float (k_quants.rs:659-674);
+ *   linear: `_quantized_linear` with BlockQ8_0::vec_dot_unopt
+ *     (k_quants.rs:738-757): y[m, n] = sum over blocks, in block order, of
+ *     ((float)(int dot of the two int8 code rows) * d_w) * d_x (+ bias[n]),
+ *     bit-identical for every m. */
+tn_status tn_q8_0_from_blob(void* stream, const uint8_t* blob, int64_t n, int64_t k, int8_t* qs,
+                            uint16_t* d);
+tn_status tn_q8_0_to_blob(void* stream, const int8_t* qs, const uint16_t* d, int64_t n,
+                          int64_t k, uint8_t* blob);
+tn_status tn_q8_0_quantize(void* stream, const float* w, int64_t n, int64_t k, int8_t* qs,
+                           uint16_t* d);
+tn_status tn_q8_0_dequantize(void* stream, const int8_t* qs, const uint16_t* d, int64_t n,
+                             int64_t k, float* out);
+tn_status tn_q8_0_linear(void* stream, const void* x, int x_dtype, int64_t m, int64_t k,
+                         const int8_t* qs, const uint16_t* d, int64_t n, const float* bias,
+                         void* y, int y_dtype);
+
 /* ---- scaled dot-product attention ----
  * `aten._scaled_dot_product_flash_attention_for_cpu(q, k, v, dropout_p=0.,
  * is_causal=False, *, attn_mask=None, scale=None) -> (out, logsumexp)`

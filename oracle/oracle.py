@@ -18,8 +18,8 @@ __all__ = [
     "lib", "build", "QK", "Q4_0_BYTES", "Q8_0_BYTES",
     "f16_from_f32", "f16_to_f32", "bf16_from_f32", "bf16_to_f32",
     "q4_0_quantize", "q4_0_dequantize", "q8_0_quantize", "q8_0_dequantize",
-    "vec_dot_q4_0_q8_0", "q4_0_linear", "sdpa", "sdpa_bf16",
-    "q4_0_parts", "q8_0_parts", "exact_linear_q4_0", "gamma", "accumulation_k",
+    "vec_dot_q4_0_q8_0", "q4_0_linear", "vec_dot_q8_0_q8_0", "q8_0_linear", "sdpa", "sdpa_bf16",
+    "q4_0_parts", "q8_0_parts", "exact_linear_q4_0", "exact_linear_q8_0", "synth_q8_0_weight", "gamma", "accumulation_k",
     "linear_bound", "sdpa_closed_form", "sdpa_det", "q8_0_ties", "signed_max_ties",
     "synth_q4_0_weight", "sdpa_tolerance",
 ]
@@ -63,6 +63,9 @@ def lib():
     L.tnref_vec_dot_q4_0_q8_0.argtypes = [I64, P, P]
     L.tnref_q4_0_linear.restype = I
     L.tnref_q4_0_linear.argtypes = [I64, I64, I64, P, P, P, P, I]
+    L.tnref_vec_dot_q8_0_q8_0.restype = ctypes.c_float
+    L.tnref_vec_dot_q8_0_q8_0.argtypes = [I64, P, P]
+    L.tnref_q8_0_linear.argtypes = [I64, I64, I64, P, P, P, P, I]
     for name in ("tnref_sdpa_f32", "tnref_sdpa_f64"):
         fn = getattr(L, name)
         fn.restype = I
@@ -145,20 +148,35 @@ def vec_dot_q4_0_q8_0(k, w_row: bytes, xq_row: bytes) -> float:
     return float(np.float32(lib().tnref_vec_dot_q4_0_q8_0(k, _p(w), _p(x))))
 
 
-def q4_0_linear(x, w_blob, n, bias=None, threads=1) -> np.ndarray:
-    """``torch._C._quantized_linear`` restated: y = Q8_0(x) . W^T (+ bias).
+def vec_dot_q8_0_q8_0(k, w_row: bytes, xq_row: bytes) -> float:
+    w = np.frombuffer(bytes(w_row), dtype=np.uint8)
+    x = np.frombuffer(bytes(xq_row), dtype=np.uint8)
+    return float(np.float32(lib().tnref_vec_dot_q8_0_q8_0(k, _p(w), _p(x))))
 
-    x is float32 [..., K]; the result is float32 [..., N]."""
+
+def _linear(fn, block_bytes, x, w_blob, n, bias, threads):
     x = np.ascontiguousarray(x, dtype=np.float32)
     k = x.shape[-1]
     m = x.size // k if k else 0
     w = np.frombuffer(bytes(w_blob), dtype=np.uint8)
-    assert w.size == n * (k // QK) * Q4_0_BYTES, "blob size does not match [N, K]"
+    assert w.size == n * (k // QK) * block_bytes, "blob size does not match [N, K]"
     y = np.empty(x.shape[:-1] + (n,), dtype=np.float32)
     b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
-    rc = lib().tnref_q4_0_linear(m, k, n, _p(x), _p(w), _p(b), _p(y), int(threads))
+    rc = fn(m, k, n, _p(x), _p(w), _p(b), _p(y), int(threads))
     assert rc == 0
     return y
+
+
+def q4_0_linear(x, w_blob, n, bias=None, threads=1) -> np.ndarray:
+    """``torch._C._quantized_linear`` restated: y = Q8_0(x) . W^T (+ bias).
+
+    x is float32 [..., K]; the result is float32 [..., N]."""
+    return _linear(lib().tnref_q4_0_linear, Q4_0_BYTES, x, w_blob, n, bias, threads)
+
+
+def q8_0_linear(x, w_blob, n, bias=None, threads=1) -> np.ndarray:
+    """The same with a Q8_0 weight blob (34-byte blocks, K:738-757)."""
+    return _linear(lib().tnref_q8_0_linear, Q8_0_BYTES, x, w_blob, n, bias, threads)
 
 
 # --- SDPA -------------------------------------------------------------------
@@ -227,6 +245,17 @@ def exact_linear_q4_0(xq_blob, w_blob, m, n, k):
     float64 (15 + 11 + 11 bits); only the summation rounds, by at most
     ``ref_err``."""
     dw, qw = q4_0_parts(w_blob, n, k)
+    return _exact_linear(dw, qw, xq_blob, m, n, k)
+
+
+def exact_linear_q8_0(xq_blob, w_blob, m, n, k):
+    """The same for a Q8_0 weight: block integers up to 32 * 127 * 128 (20
+    bits) times two 11-bit scales, still exact in float64."""
+    dw, qw = q8_0_parts(w_blob, n, k)
+    return _exact_linear(dw, qw, xq_blob, m, n, k)
+
+
+def _exact_linear(dw, qw, xq_blob, m, n, k):
     dx, qx = q8_0_parts(xq_blob, m, k)
     ints = np.einsum("rbk,obk->rob", qx, qw)
     absints = np.einsum("rbk,obk->rob", np.abs(qx), np.abs(qw))
@@ -331,6 +360,21 @@ def synth_q4_0_weight(n, k, sigma, seed):
     blob[:, :, 0] = (dh & 0xFF).astype(np.uint8)
     blob[:, :, 1] = (dh >> 8).astype(np.uint8)
     blob[:, :, 2:] = packed
+    return blob.tobytes()
+
+
+def synth_q8_0_weight(n, k, sigma, seed):
+    """A Q8_0 weight blob built directly in the format: codes uniform in
+    [-127, 127], per-block d = f16_rne(|N(0, sigma)| / 127)."""
+    rng = np.random.default_rng(seed)
+    nb = k // QK
+    codes = rng.integers(-127, 128, size=(n, nb, QK), dtype=np.int64)
+    d = (np.abs(rng.standard_normal((n, nb))) * sigma / 127.0).astype(np.float32)
+    dh = f16_from_f32(d)
+    blob = np.empty((n, nb, Q8_0_BYTES), dtype=np.uint8)
+    blob[:, :, 0] = (dh & 0xFF).astype(np.uint8)
+    blob[:, :, 1] = (dh >> 8).astype(np.uint8)
+    blob[:, :, 2:] = codes.astype(np.int8).view(np.uint8)
     return blob.tobytes()
 
 

@@ -203,11 +203,32 @@ float tnref_vec_dot_q4_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq) {
     return sumf;
 }
 
+/* BlockQ8_0::vec_dot_unopt, K:738-757: exact i32 block sum of the two int8
+ * code rows, then sumf += (sum_i as f32 * d_w) * d_x in block order. */
+float tnref_vec_dot_q8_0_q8_0(int64_t k, const uint8_t* w, const uint8_t* xq) {
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < k / QK; b++) {
+        const uint8_t* wb = w + b * 34;
+        const uint8_t* xb = xq + b * 34;
+        int32_t sum_i = 0;
+        for (int j = 0; j < QK; j++) sum_i += (int32_t)(int8_t)wb[2 + j] * (int32_t)(int8_t)xb[2 + j];
+        float dw = tnref_f16_to_f32((uint16_t)(wb[0] | (wb[1] << 8)));
+        float dx = tnref_f16_to_f32((uint16_t)(xb[0] | (xb[1] << 8)));
+        float t = (float)sum_i * dw;
+        t = t * dx;
+        sumf = sumf + t;
+    }
+    return sumf;
+}
+
+typedef float (*dot_fn)(int64_t, const uint8_t*, const uint8_t*);
+
 typedef struct {
-    int64_t m, k, n, c0, c1;
+    int64_t m, k, n, c0, c1, wrow;
     const uint8_t* xq;
     const uint8_t* w;
     float* y;
+    dot_fn dot;
 } lin_job;
 
 /* One worker's contiguous column range, ROW_TILE rows at a time: the loop
@@ -219,16 +240,19 @@ static void* lin_worker(void* arg) {
     for (int64_t r0 = 0; r0 < j->m; r0 += 16) {
         int64_t r1 = r0 + 16 < j->m ? r0 + 16 : j->m;
         for (int64_t c = j->c0; c < j->c1; c++) {
-            const uint8_t* wr = j->w + c * nb * 18;
+            const uint8_t* wr = j->w + c * j->wrow;
             for (int64_t r = r0; r < r1; r++)
-                j->y[r * j->n + c] = tnref_vec_dot_q4_0_q8_0(j->k, wr, j->xq + r * nb * 34);
+                j->y[r * j->n + c] = j->dot(j->k, wr, j->xq + r * nb * 34);
         }
     }
     return NULL;
 }
 
-int tnref_q4_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w,
-                      const float* bias, float* y, int threads) {
+/* Both weight formats quantise the activation rows to Q8_0 (their VecDotType,
+ * K:281 and K:654) and differ only in the block dot and the weight's bytes
+ * per block. */
+static int q_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w, int64_t wblock,
+                    dot_fn dot, const float* bias, float* y, int threads) {
     if (m < 0 || n < 0 || k <= 0 || k % QK) return -1;
     const int64_t nb = k / QK;
     uint8_t* xq = (uint8_t*)malloc((size_t)(m * nb * 34 + 1));
@@ -248,7 +272,7 @@ int tnref_q4_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uin
         if (c0 > quads * 4) c0 = quads * 4;
         if (c1 > quads * 4) c1 = quads * 4;
         if (t == threads - 1) c1 = n;
-        jobs[t] = (lin_job){m, k, n, c0, c1, xq, w, y};
+        jobs[t] = (lin_job){m, k, n, c0, c1, nb * wblock, xq, w, y, dot};
         live[t] = threads > 1 && pthread_create(&tid[t], NULL, lin_worker, &jobs[t]) == 0;
         if (!live[t]) lin_worker(&jobs[t]);
     }
@@ -258,6 +282,16 @@ int tnref_q4_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uin
         for (int64_t r = 0; r < m; r++)
             for (int64_t c = 0; c < n; c++) y[r * n + c] = y[r * n + c] + bias[c];
     return 0;
+}
+
+int tnref_q4_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w,
+                      const float* bias, float* y, int threads) {
+    return q_linear(m, k, n, x, w, 18, tnref_vec_dot_q4_0_q8_0, bias, y, threads);
+}
+
+int tnref_q8_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w,
+                      const float* bias, float* y, int threads) {
+    return q_linear(m, k, n, x, w, 34, tnref_vec_dot_q8_0_q8_0, bias, y, threads);
 }
 
 /* ------------------------------------------------------------------------ */

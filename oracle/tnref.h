@@ -45,6 +45,10 @@ float tnref_vec_dot_q4_0_q8_0(int64_t k, const uint8_t* w_row, const uint8_t* xq
  * threads <= 0 means one thread. Returns 0, or -1 on a bad shape. */
 int tnref_q4_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w_blob,
                       const float* bias, float* y, int threads);
+/* Q8_0 weights: K:738-757 (vec_dot_unopt) per output, the same driver. */
+float tnref_vec_dot_q8_0_q8_0(int64_t k, const uint8_t* w_row, const uint8_t* xq_row);
+int tnref_q8_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w_blob,
+                      const float* bias, float* y, int threads);
 
 /* ---- SDPA, the default (flat) path: A:10330-10423 ----
  * q [B,Hq,L,D], k/v [B,Hkv,S,D] row-major; mask nullable, [B,Hq,L,S] row-major

@@ -41,6 +41,7 @@ def test_abi_version_and_op_list(L):
     assert L.tn_abi_version() == 1
     ops = L.tn_ops().decode()
     assert "torch._C._quantized_linear(q4_0)" in ops
+    assert "torch._C._quantized_linear(q8_0)" in ops
     assert "aten._scaled_dot_product_flash_attention_for_cpu.default" in ops
 
 
@@ -59,6 +60,16 @@ def test_linear_refusals_use_the_reference_wording(L):
     st = L.tn_q4_0_quantize(None, None, 4, 48, None, None)
     assert st == _lib.TN_ENOTIMPL
     assert "must have their last dim divisible by block size -- got 48" in _lib.last_error()
+    # q8_0 entry points: the same refusals, naming their format
+    st = L.tn_q8_0_linear(None, None, _lib.TN_F16, 1, 64, None, None, 8, None, None, _lib.TN_F32)
+    assert st == _lib.TN_ENOTIMPL and "activation must be float32" in _lib.last_error()
+    st = L.tn_q8_0_linear(None, None, _lib.TN_F32, 2, 40, None, None, 8, None, None, _lib.TN_F32)
+    assert st == _lib.TN_EINVAL and "cannot be multiplied ([2, 40]" in _lib.last_error()
+    for fn in (L.tn_q8_0_quantize, L.tn_q8_0_from_blob):
+        assert fn(None, None, 4, 48, None, None) == _lib.TN_ENOTIMPL
+        assert "q8_0 stores 32 elements per block" in _lib.last_error()
+    assert L.tn_q8_0_dequantize(None, None, None, 4, 96, None) == _lib.TN_EVALUE  # null planes
+    assert "null pointer" in _lib.last_error()
     with pytest.raises(NotImplementedError):
         _lib.check(_lib.TN_ENOTIMPL)
 
@@ -111,6 +122,11 @@ def test_python_mirror_refuses_host_operands_instead_of_falling_back():
         tn._quantize(x, "q8_1")
     with pytest.raises(ValueError, match="needs 18 bytes; got 17"):
         tn._quantized_from_blob(b"\0" * 17, (1, 32), "q4_0")
+    with pytest.raises(ValueError, match="q8_0 stores 32 elements in 34 bytes.*needs 68 bytes; got 36"):
+        tn._quantized_from_blob(b"\0" * 36, (1, 64), "q8_0")
+    with pytest.raises(NotImplementedError, match="'q4_k' is not implemented on the hip device"):
+        tn._quantize(x, "q4_k")
+    assert tn._quantized_formats() == ["q4_0", "q8_0"]
     q = tn._quantized_from_blob(b"\0" * 36, (1, 64), "q4_0")  # stays on the host: no compute
     assert tn._quantized_blob(q) == b"\0" * 36 and tn._quantized_nbytes(q) == 36
     with pytest.raises(NotImplementedError, match="hip device"):

@@ -216,6 +216,74 @@ def test_bias_is_added_after_the_matmul_in_float32():
     assert O.q4_0_linear(x, blob, 6, bias=b).tobytes() == (O.q4_0_linear(x, blob, 6) + b).astype(np.float32).tobytes()
 
 
+# --- q8_0 weights (K:652-757): the same recurrence with an int8 block dot ----
+
+
+@pytest.mark.parametrize("rows,out_f,in_f,seed", [(1, 8, 64, 31), (3, 12, 512, 32), (2, 5, 1024, 33)])
+def test_q8_0_linear_is_within_the_counted_bound_of_its_exact_value(rows, out_f, in_f, seed):
+    w = (np.random.default_rng(seed + 1).standard_normal((out_f, in_f)) * 0.05).astype(np.float32)
+    x = _tie_free(rows, in_f, seed)
+    blob = O.q8_0_quantize(w)
+    got = O.q8_0_linear(x, blob, out_f).astype(np.float64)
+    exact, abs_sum, ref_err = O.exact_linear_q8_0(O.q8_0_quantize(x), blob, rows, out_f, in_f)
+    bound = O.linear_bound(in_f, abs_sum, ref_err)
+    assert np.max(np.abs(got - exact) / bound) <= 1.0
+    # the bound refuses the matmul that skips activation quantisation
+    wdq = O.q8_0_dequantize(blob, out_f * in_f).astype(np.float64).reshape(out_f, in_f)
+    assert np.max(np.abs(x.astype(np.float64) @ wdq.T - exact) / bound) > 1.0
+
+
+def test_q8_0_linear_matches_a_numpy_float32_restatement_bit_for_bit():
+    """K:738-757 spelled in numpy float32: the int8 block dot, then the two
+    roundings and the ordered sum; the q4_0 dot on the same bytes differs."""
+    rng = np.random.default_rng(23)
+    m, k, n = 3, 256, 40
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    blob = O.synth_q8_0_weight(n, k, 0.02, 24)
+    dw, qw = O.q8_0_parts(blob, n, k)
+    dx, qx = O.q8_0_parts(O.q8_0_quantize(x), m, k)
+    ints = np.einsum("rbk,obk->rob", qx, qw)
+    acc = np.zeros((m, n), np.float32)
+    for b in range(k // 32):
+        t = ints[:, :, b].astype(np.float32) * dw[None, :, b].astype(np.float32)
+        t = (t * dx[:, None, b].astype(np.float32)).astype(np.float32)
+        acc = (acc + t).astype(np.float32)
+    assert O.q8_0_linear(x, blob, n).tobytes() == acc.tobytes()
+    xq = O.q8_0_quantize(x[0])
+    assert O.vec_dot_q8_0_q8_0(k, blob[: (k // 32) * 34], xq) == float(acc[0, 0])
+
+
+@pytest.mark.parametrize("m", [2, 5, 17, 130])
+def test_q8_0_batched_rows_equal_one_row_calls_bit_for_bit(m):
+    rng = np.random.default_rng(277 + m)
+    k, n = 512, 11
+    blob = O.q8_0_quantize((rng.standard_normal((n, k)) * 0.05).astype(np.float32))
+    x = (rng.standard_normal((m, k)) * 1.3).astype(np.float32)
+    batched = O.q8_0_linear(x, blob, n, threads=3)
+    rows = np.concatenate([O.q8_0_linear(x[i:i + 1], blob, n) for i in range(m)])
+    assert batched.tobytes() == rows.tobytes()
+
+
+def test_q8_0_lossless_operands_give_the_exact_integer_matmul():
+    """test_qgemm.py:103-137's q8_0 half: scale-1 blocks of integer codes and
+    activation blocks with absmax 127 quantise exactly, so the result is the
+    integer matmul."""
+    rng = np.random.default_rng(1771)
+    k = 64
+    for n in (8, 9, 10, 11):
+        codes = rng.integers(-127, 128, size=(n, k // 32, 32))
+        blob = bytearray()
+        for r in range(n):
+            for b in range(k // 32):
+                blob += struct.pack("<e", 1.0) + struct.pack("<32b", *codes[r, b])
+        dense = codes.reshape(n, k)
+        for m in (2, 5, 17, 130):
+            xs = rng.integers(-126, 127, size=(m, k))
+            xs[:, 0], xs[:, 32] = 127, -127
+            got = O.q8_0_linear(xs.astype(np.float32), bytes(blob), n, threads=2)
+            assert np.array_equal(got.astype(np.int64), xs @ dense.T)
+
+
 # --- 4. planted faults fail the fixtures -------------------------------------
 
 

@@ -22,7 +22,12 @@ from .tensor import Tensor, current_stream
 
 QK4_0 = 32
 Q4_0_TYPE_SIZE = 18
-_FORMATS = ("q4_0",)
+# format -> (elements per block, GGML bytes per block, device code bytes per block, C-ABI prefix)
+_LAYOUT = {
+    "q4_0": (32, 18, 16, "tn_q4_0"),
+    "q8_0": (32, 34, 32, "tn_q8_0"),
+}
+_FORMATS = tuple(_LAYOUT)
 _REFERENCE_FORMATS = ("f32", "f16", "bf16", "q4_0", "q4_1", "q5_0", "q5_1", "q8_0", "q8_1",
                       "q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "q8_k")
 SDPA_OP = "aten._scaled_dot_product_flash_attention_for_cpu.default"
@@ -30,8 +35,8 @@ SDPA_OP = "aten._scaled_dot_product_flash_attention_for_cpu.default"
 
 class QTensor:
     """A block-quantised weight [N, K] (the reference's `Repr::Quantized`,
-    tensor.rs:970). On "hip" it is two device planes (the 16-byte nibble
-    groups and the f16 scales, include/tnhip.h); on "cpu" it is the GGML blob
+    tensor.rs:970). On "hip" it is two device planes (the code bytes of every
+    block and the f16 scales, include/tnhip.h); on "cpu" it is the GGML blob
     itself. The dtype tag is float32, as the reference's is (quant.rs:167)."""
 
     dtype = "float32"
@@ -54,7 +59,10 @@ class QTensor:
 
     @property
     def nblocks(self) -> int:
-        return math.prod(self.shape) // QK4_0
+        return math.prod(self.shape) // _LAYOUT[self.format][0]
+
+    def _fn(self, op):
+        return getattr(lib(), f"{_LAYOUT[self.format][3]}_{op}")
 
     def __repr__(self):
         return f"QTensor(shape={self.shape}, format={self.format}, device={self.device})"
@@ -69,10 +77,17 @@ def _require_hip(op, *tensors):
             )
 
 
-def _shape2(shape):
+def _shape2(shape, fmt="q4_0"):
     if len(shape) != 2:
-        raise NotImplementedError(f"q4_0 weights are 2-d [out_features, in_features] here, got shape {list(shape)}")
+        raise NotImplementedError(f"{fmt} weights are 2-d [out_features, in_features] here, got shape {list(shape)}")
     return shape
+
+
+def _planes(n, k, fmt):
+    """Empty device planes for an [n, k] weight: (codes, f16 scales as bytes)."""
+    blk, _, code_bytes, _ = _LAYOUT[fmt]
+    nb = n * k // blk
+    return Tensor((nb * code_bytes,), "uint8", "hip"), Tensor((nb * 2,), "uint8", "hip")
 
 
 def _quantized_formats():
@@ -88,12 +103,14 @@ def _format_check(op, fmt):
             "vec_dot and no weight format names it as a VecDotType, so a weight stored this way has no matmul. "
             "Use q8_0."
         )
-    if fmt != "q4_0":
-        raise NotImplementedError(f"{op}: format {fmt!r} is not implemented on the hip device (q4_0 is)")
+    if fmt not in _LAYOUT:
+        raise NotImplementedError(
+            f"{op}: format {fmt!r} is not implemented on the hip device ({', '.join(_FORMATS)} are)")
 
 
 def _quantize(t: Tensor, fmt: str) -> QTensor:
-    """`_C._quantize(t, format)` (quant.rs:124-172), BlockQ4_0::from_float on the device."""
+    """`_C._quantize(t, format)` (quant.rs:124-172): BlockQ4_0::from_float or
+    BlockQ8_0::from_float on the device."""
     op = "torch._C._quantize"
     _format_check(op, fmt)
     _require_hip(op, t)
@@ -101,30 +118,32 @@ def _quantize(t: Tensor, fmt: str) -> QTensor:
         raise NotImplementedError(f"{op}: a 0-d tensor cannot be quantised")
     if t.dtype != "float32":
         raise NotImplementedError(f"{op}: the hip quantiser takes float32, got {t.dtype}")
-    if t.shape[-1] % QK4_0:
+    blk = _LAYOUT[fmt][0]
+    if t.shape[-1] % blk:
         raise NotImplementedError(
-            f"{op}: {fmt} stores {QK4_0} elements per block, so it must have their last dim divisible by block "
-            f"size -- got {t.shape[-1]}, which is not a multiple of {QK4_0} (shape {list(t.shape)})"
+            f"{op}: {fmt} stores {blk} elements per block, so it must have their last dim divisible by block "
+            f"size -- got {t.shape[-1]}, which is not a multiple of {blk} (shape {list(t.shape)})"
         )
-    n, k = _shape2(t.shape)
-    qs = Tensor((n * k // 2,), "uint8", "hip")
-    d = Tensor((n * k // QK4_0 * 2,), "uint8", "hip")
-    check(lib().tn_q4_0_quantize(current_stream(), t.data_ptr(), n, k, qs.data_ptr(), d.data_ptr()))
-    return QTensor((n, k), fmt, "hip", qs=qs, d=d)
+    n, k = _shape2(t.shape, fmt)
+    qs, d = _planes(n, k, fmt)
+    q = QTensor((n, k), fmt, "hip", qs=qs, d=d)
+    check(q._fn("quantize")(current_stream(), t.data_ptr(), n, k, qs.data_ptr(), d.data_ptr()))
+    return q
 
 
 def _quantized_from_blob(data: bytes, shape, fmt: str, device="cpu") -> QTensor:
     """`_C._quantized_from_blob(bytes, shape, format)` (quant.rs:230-262)."""
     op = "torch._C._quantized_from_blob"
     _format_check(op, fmt)
+    blk, size = _LAYOUT[fmt][:2]
     numel = math.prod(shape)
-    want = numel // QK4_0 * Q4_0_TYPE_SIZE
-    if numel % QK4_0 or len(data) != want:
+    want = numel // blk * size
+    if numel % blk or len(data) != want:
         raise ValueError(
-            f"{op}: {fmt} stores {QK4_0} elements in {Q4_0_TYPE_SIZE} bytes, so a {list(shape)} tensor needs "
+            f"{op}: {fmt} stores {blk} elements in {size} bytes, so a {list(shape)} tensor needs "
             f"{want} bytes; got {len(data)}"
         )
-    q = QTensor(_shape2(tuple(shape)), fmt, "cpu", blob=bytes(data))
+    q = QTensor(_shape2(tuple(shape), fmt), fmt, "cpu", blob=bytes(data))
     return _quantized_to(q, device)
 
 
@@ -140,10 +159,10 @@ def _quantized_to(t: QTensor, device) -> QTensor:
     n, k = t.shape
     if dev == "hip":
         blob = Tensor.from_numpy(np.frombuffer(t._blob, dtype=np.uint8), device="hip")
-        qs = Tensor((n * k // 2,), "uint8", "hip")
-        d = Tensor((n * k // QK4_0 * 2,), "uint8", "hip")
-        check(lib().tn_q4_0_from_blob(current_stream(), blob.data_ptr(), n, k, qs.data_ptr(), d.data_ptr()))
-        return QTensor(t.shape, t.format, "hip", qs=qs, d=d)
+        qs, d = _planes(n, k, t.format)
+        q = QTensor(t.shape, t.format, "hip", qs=qs, d=d)
+        check(q._fn("from_blob")(current_stream(), blob.data_ptr(), n, k, qs.data_ptr(), d.data_ptr()))
+        return q
     return QTensor(t.shape, t.format, "cpu", blob=_quantized_blob(t))
 
 
@@ -152,8 +171,8 @@ def _quantized_blob(t: QTensor) -> bytes:
     if t.device == "cpu":
         return t._blob
     n, k = t.shape
-    blob = Tensor((n * k // QK4_0 * Q4_0_TYPE_SIZE,), "uint8", "hip")
-    check(lib().tn_q4_0_to_blob(current_stream(), t._qs.data_ptr(), t._d.data_ptr(), n, k, blob.data_ptr()))
+    blob = Tensor((t.nblocks * _LAYOUT[t.format][1],), "uint8", "hip")
+    check(t._fn("to_blob")(current_stream(), t._qs.data_ptr(), t._d.data_ptr(), n, k, blob.data_ptr()))
     return blob.bits().tobytes()
 
 
@@ -163,7 +182,7 @@ def _quantized_format(t: QTensor) -> str:
 
 def _quantized_nbytes(t: QTensor) -> int:
     """What the weight costs (quant.rs:197-211): the GGML storage size."""
-    return t.nblocks * Q4_0_TYPE_SIZE
+    return t.nblocks * _LAYOUT[t.format][1]
 
 
 def _dequantize(t: QTensor) -> Tensor:
@@ -172,7 +191,7 @@ def _dequantize(t: QTensor) -> Tensor:
     _require_hip(op, t)
     n, k = t.shape
     out = Tensor((n, k), "float32", "hip")
-    check(lib().tn_q4_0_dequantize(current_stream(), t._qs.data_ptr(), t._d.data_ptr(), n, k, out.data_ptr()))
+    check(t._fn("dequantize")(current_stream(), t._qs.data_ptr(), t._d.data_ptr(), n, k, out.data_ptr()))
     return out
 
 
@@ -211,7 +230,7 @@ def _quantized_linear(input: Tensor, weight: QTensor, bias: Tensor | None = None
     m = input.numel // in_features
     odt = out_dtype or "float32"
     out = Tensor(input.shape[:-1] + (out_features,), odt, "hip")
-    check(lib().tn_q4_0_linear(current_stream(), input.data_ptr(), _dt(input.dtype), m, in_features,
+    check(weight._fn("linear")(current_stream(), input.data_ptr(), _dt(input.dtype), m, in_features,
                                weight._qs.data_ptr(), weight._d.data_ptr(), out_features,
                                bias.data_ptr() if bias is not None else None, out.data_ptr(), _dt(odt)))
     return out

@@ -1,22 +1,43 @@
-// GGML q4_0 on gfx950: upload/repack, quantise, dequantise, and the
-// quantised linear (decode GEMV and prefill MFMA GEMM).
+// GGML block-quantised weights on gfx950 (q4_0 and q8_0): upload/repack,
+// quantise, dequantise, and the quantised linear (decode GEMV and prefill
+// MFMA GEMM).
 //
 // Arithmetic contract (candle-core/src/quantized/k_quants.rs, the reference's
 // vendored candle): every output is
 //     sumf = 0; for b in blocks: sumf += ((float)S_b * d_w[b]) * d_x[b]
-// where S_b is the exact integer dot of the weight's Q4_0 codes (nib - 8) and
-// the activation's Q8_0 codes (vec_dot_unopt, k_quants.rs:312-329), and the
-// activation row is quantised by BlockQ8_0::from_float (k_quants.rs:676-705).
-// The integer dot is exact in any order, and every kernel below performs the
-// float steps in exactly that order with separate roundings (the library is
-// built with -ffp-contract=off), so results are bit-identical to the
-// reference's x86_64 scalar path for every row count.
+// where S_b is the exact integer dot of the weight's codes (q4_0: nib - 8,
+// vec_dot_unopt k_quants.rs:312-329; q8_0: the int8 codes, k_quants.rs:738-757)
+// and the activation's Q8_0 codes, and the activation row is quantised by
+// BlockQ8_0::from_float (k_quants.rs:676-705) -- Q8_0 is the VecDotType of
+// both weight formats. The integer dot is exact in any order, and every kernel
+// below performs the float steps in exactly that order with separate
+// roundings (the library is built with -ffp-contract=off), so results are
+// bit-identical to the reference's x86_64 scalar path for every row count.
 #include "tn_common.h"
 
 namespace tn {
 namespace {
 
 constexpr int QK = 32;
+
+// Weight formats. On the device a weight is two planes: the codes of every
+// block back to back in row-major block order (q4_0: the 16 nibble bytes of
+// the GGML block; q8_0: its 32 int8 codes) and the f16 block scales.
+enum WeightFormat { FMT_Q4_0 = 0, FMT_Q8_0 = 1 };
+template <int FMT>
+struct Fmt;
+template <>
+struct Fmt<FMT_Q4_0> {
+    static constexpr int CODE_BYTES = 16, BLOB_BYTES = 18;
+    static constexpr int GEMV_ITEMS = 3;  // (row, block) items per GEMV thread: 3 streamed best on C1 (76% of HBM, 71% for 4)
+    static constexpr const char* name = "q4_0";
+};
+template <>
+struct Fmt<FMT_Q8_0> {
+    static constexpr int CODE_BYTES = 32, BLOB_BYTES = 34;
+    static constexpr int GEMV_ITEMS = 2;  // 32-byte items: 64 bytes in flight per thread
+    static constexpr const char* name = "q8_0";
+};
 
 // ---- Rust cast semantics ---------------------------------------------------
 
@@ -57,35 +78,49 @@ __device__ inline int q8_0_lane(float v, float* dx) {
 
 // ---- layout conversion --------------------------------------------------------
 
+// GGML blocks (f16 d, then the codes) <-> the two planes, one thread per block.
+template <int FMT>
 __global__ void k_from_blob(const uint8_t* __restrict__ blob, int64_t nblocks, uint8_t* __restrict__ qs,
                             uint16_t* __restrict__ d) {
+    constexpr int CB = Fmt<FMT>::CODE_BYTES;
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
-    const uint8_t* s = blob + i * 18;
+    const uint8_t* s = blob + i * Fmt<FMT>::BLOB_BYTES;
     d[i] = (uint16_t)(s[0] | (s[1] << 8));
-    uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-        w[j] = (uint32_t)s[2 + 4 * j] | ((uint32_t)s[3 + 4 * j] << 8) | ((uint32_t)s[4 + 4 * j] << 16) |
-               ((uint32_t)s[5 + 4 * j] << 24);
-    *reinterpret_cast<uint4*>(qs + i * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    for (int c = 0; c < CB / 16; c++) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint8_t* b = s + 2 + 16 * c + 4 * j;
+            w[j] = (uint32_t)b[0] | ((uint32_t)b[1] << 8) | ((uint32_t)b[2] << 16) | ((uint32_t)b[3] << 24);
+        }
+        reinterpret_cast<uint4*>(qs + i * CB)[c] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
 }
 
+template <int FMT>
 __global__ void k_to_blob(const uint8_t* __restrict__ qs, const uint16_t* __restrict__ d, int64_t nblocks,
                           uint8_t* __restrict__ blob) {
+    constexpr int CB = Fmt<FMT>::CODE_BYTES;
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
-    uint8_t* o = blob + i * 18;
+    uint8_t* o = blob + i * Fmt<FMT>::BLOB_BYTES;
     uint16_t h = d[i];
     o[0] = (uint8_t)(h & 0xff);
     o[1] = (uint8_t)(h >> 8);
-    uint4 w = *reinterpret_cast<const uint4*>(qs + i * 16);
-    uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int j = 0; j < 16; j++) o[2 + j] = (uint8_t)(ws[j >> 2] >> (8 * (j & 3)));
+    for (int c = 0; c < CB / 16; c++) {
+        const uint4 w = reinterpret_cast<const uint4*>(qs + i * CB)[c];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 16; j++) o[2 + 16 * c + j] = (uint8_t)(ws[j >> 2] >> (8 * (j & 3)));
+    }
 }
 
-// BlockQ4_0::from_float (k_quants.rs:241-277), one thread per block.
+// BlockQ4_0::from_float (k_quants.rs:241-277) and BlockQ8_0::from_float
+// (k_quants.rs:676-705), one thread per block.
+template <int FMT>
 __global__ void k_quantize_w(const float* __restrict__ w, int64_t nblocks, uint8_t* __restrict__ qs,
                              uint16_t* __restrict__ d) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -97,48 +132,73 @@ __global__ void k_quantize_w(const float* __restrict__ w, int64_t nblocks, uint8
         float4 t = *reinterpret_cast<const float4*>(xs + j);
         v[j] = t.x; v[j + 1] = t.y; v[j + 2] = t.z; v[j + 3] = t.w;
     }
-    float amax = 0.0f, mx = 0.0f;
+    if constexpr (FMT == FMT_Q8_0) {
+        float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < QK; j++) {
-        float a = fabsf(v[j]);
-        if (amax < a) { amax = a; mx = v[j]; }  // first of the largest |x|, sign kept
-    }
-    float dd = mx / -8.0f;
-    float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
-    d[i] = f16_from_f32(dd);
-    uint32_t out[4] = {0, 0, 0, 0};
+        for (int j = 0; j < QK; j++) amax = fmaxf(amax, fabsf(v[j]));
+        const float dd = amax / 127.0f;
+        const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;  // the f32 d, not the f16 one
+        d[i] = f16_from_f32(dd);
+        uint32_t out[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < QK / 2; j++) {
-        int q0 = sat_u8(v[j] * id + 8.5f);
-        int q1 = sat_u8(v[j + QK / 2] * id + 8.5f);
-        q0 = q0 < 15 ? q0 : 15;
-        q1 = q1 < 15 ? q1 : 15;
-        out[j >> 2] |= (uint32_t)(q0 | (q1 << 4)) << (8 * (j & 3));
+        for (int j = 0; j < QK; j++) out[j >> 2] |= ((uint32_t)sat_i8(roundf(v[j] * id)) & 0xffu) << (8 * (j & 3));
+        uint4* o = reinterpret_cast<uint4*>(qs + i * QK);
+        o[0] = make_uint4(out[0], out[1], out[2], out[3]);
+        o[1] = make_uint4(out[4], out[5], out[6], out[7]);
+    } else {
+        float amax = 0.0f, mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < QK; j++) {
+            float a = fabsf(v[j]);
+            if (amax < a) { amax = a; mx = v[j]; }  // first of the largest |x|, sign kept
+        }
+        float dd = mx / -8.0f;
+        float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
+        d[i] = f16_from_f32(dd);
+        uint32_t out[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < QK / 2; j++) {
+            int q0 = sat_u8(v[j] * id + 8.5f);
+            int q1 = sat_u8(v[j + QK / 2] * id + 8.5f);
+            q0 = q0 < 15 ? q0 : 15;
+            q1 = q1 < 15 ? q1 : 15;
+            out[j >> 2] |= (uint32_t)(q0 | (q1 << 4)) << (8 * (j & 3));
+        }
+        *reinterpret_cast<uint4*>(qs + i * 16) = make_uint4(out[0], out[1], out[2], out[3]);
     }
-    *reinterpret_cast<uint4*>(qs + i * 16) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
-// BlockQ4_0::to_float (k_quants.rs:219-239): (nib - 8) as f32 * f32(d), exact.
+// BlockQ4_0::to_float (k_quants.rs:219-239): (nib - 8) as f32 * f32(d);
+// BlockQ8_0::to_float (k_quants.rs:659-674): q as f32 * f32(d). Both exact.
+template <int FMT>
 __global__ void k_dequantize(const uint8_t* __restrict__ qs, const uint16_t* __restrict__ d, int64_t nblocks,
                              float* __restrict__ out) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
     float s = f16_to_f32(d[i]);
-    uint4 w = *reinterpret_cast<const uint4*>(qs + i * 16);
-    uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    float lo[16], hi[16];
+    float e[QK];
+    if constexpr (FMT == FMT_Q8_0) {
+        const uint4* src = reinterpret_cast<const uint4*>(qs + i * QK);
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-        uint32_t byte = (ws[j >> 2] >> (8 * (j & 3))) & 0xffu;
-        lo[j] = (float)((int)(byte & 0xf) - 8) * s;
-        hi[j] = (float)((int)(byte >> 4) - 8) * s;
+        for (int c = 0; c < 2; c++) {
+            const uint4 w = src[c];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int j = 0; j < 16; j++) e[16 * c + j] = (float)(int8_t)(ws[j >> 2] >> (8 * (j & 3))) * s;
+        }
+    } else {
+        uint4 w = *reinterpret_cast<const uint4*>(qs + i * 16);
+        uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            uint32_t byte = (ws[j >> 2] >> (8 * (j & 3))) & 0xffu;
+            e[j] = (float)((int)(byte & 0xf) - 8) * s;
+            e[j + 16] = (float)((int)(byte >> 4) - 8) * s;
+        }
     }
     float4* o = reinterpret_cast<float4*>(out + i * QK);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        o[j] = make_float4(lo[4 * j], lo[4 * j + 1], lo[4 * j + 2], lo[4 * j + 3]);
-        o[4 + j] = make_float4(hi[4 * j], hi[4 * j + 1], hi[4 * j + 2], hi[4 * j + 3]);
-    }
+    for (int j = 0; j < QK / 4; j++) o[j] = make_float4(e[4 * j], e[4 * j + 1], e[4 * j + 2], e[4 * j + 3]);
 }
 
 // ---- decode GEMV (m <= GEMV_MAX_M) ---------------------------------------------
@@ -146,13 +206,13 @@ __global__ void k_dequantize(const uint8_t* __restrict__ qs, const uint16_t* __r
 // One workgroup owns `rows` consecutive weight rows. Phase 1 quantises the MR
 // activation rows into LDS (every workgroup repeats this: x is a few KB and
 // L2-resident). Phase 2 streams the weight: the (row, block) items of the
-// workgroup are a contiguous range of the qs plane, so consecutive lanes issue
-// consecutive 16-byte loads; each item's exact integer dot is 8 v_dot4_i32_i8
-// on the unsigned nibbles minus 8 * sum(x codes), and its scaled term goes to
-// LDS. Phase 3 adds each output's terms in block order.
+// workgroup are a contiguous range of the codes plane, so consecutive lanes
+// issue consecutive 16-byte loads (two per q8_0 item); each item's exact
+// integer dot is 8 v_dot4_i32_i8 (q4_0: on the unsigned nibbles, minus
+// 8 * sum(x codes)), and its scaled term goes to LDS. Phase 3 adds each
+// output's terms in block order.
 
 constexpr int GEMV_THREADS = 256;
-constexpr int GEMV_ITEMS = 3;  // (row, block) items per thread (3 streamed best: 76% of HBM on C1, against 71% for 4)
 constexpr int GEMV_MAX_M = 4;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -173,6 +233,20 @@ __device__ inline int dot_block(uint4 w, const int* __restrict__ xw) {
     return s;
 }
 
+__device__ inline int dot_block_q8(const uint4& w0, const uint4& w1, const int* __restrict__ xw) {
+    // both operands hold the 32 int8 codes in natural order, 4 per dword
+    int s = 0;
+    s = __builtin_amdgcn_sdot4((int)w0.x, xw[0], s, false);
+    s = __builtin_amdgcn_sdot4((int)w0.y, xw[1], s, false);
+    s = __builtin_amdgcn_sdot4((int)w0.z, xw[2], s, false);
+    s = __builtin_amdgcn_sdot4((int)w0.w, xw[3], s, false);
+    s = __builtin_amdgcn_sdot4((int)w1.x, xw[4], s, false);
+    s = __builtin_amdgcn_sdot4((int)w1.y, xw[5], s, false);
+    s = __builtin_amdgcn_sdot4((int)w1.z, xw[6], s, false);
+    s = __builtin_amdgcn_sdot4((int)w1.w, xw[7], s, false);
+    return s;
+}
+
 // Phase 1 gives each 32-element block to 8 lanes, a float4 each: lane l of
 // the workgroup holds elements 4 (l % 8) .. 4 (l % 8) + 3 of block l / 8 + 32 p
 // in pass p, so for one row thread t holds elements 1024p + 4t .. 1024p + 4t + 3.
@@ -190,7 +264,7 @@ __device__ inline int dot_block(uint4 w, const int* __restrict__ xw) {
 // output's thread reads its residual before writing it), never x. x must be 16-byte aligned.
 constexpr int GEMV_HOLD = 4;  // passes of 32 blocks held in registers (K <= 4096 per row at once)
 
-template <int MR, typename XT, int PRO>
+template <int FMT, int MR, typename XT, int PRO>
 __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x, int K, int nb,
                                                      const uint8_t* __restrict__ qs,
                                                      const uint16_t* __restrict__ dw, int N, int rows,
@@ -198,6 +272,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                                                      int y_bf16, const GemvPro po) {
     static_assert(PRO == PRO_NONE || (MR == 1 && sizeof(XT) == 4), "prologues take one f32 row");
     constexpr int HOLD = PRO == PRO_COMBINE ? 1 : GEMV_HOLD;
+    constexpr int ITEMS = Fmt<FMT>::GEMV_ITEMS, NV = Fmt<FMT>::CODE_BYTES / 16;
     extern __shared__ __align__(16) char smem[];
     __shared__ float red[4];
     int* xq = reinterpret_cast<int*>(smem);               // [MR][K/4] packed int8 codes
@@ -212,21 +287,24 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
     const int tstride = (int)gridDim.x;
     // two register buffers: the tile being computed and the next one in flight
     // (a third, two tiles ahead, measured slower: fewer resident waves)
-    uint4 wv[GEMV_ITEMS], wn[GEMV_ITEMS];
-    uint16_t dv[GEMV_ITEMS], dn[GEMV_ITEMS];
-    auto gload = [&](int tile, uint4* wr, uint16_t* dr) {
+    uint4 wv[ITEMS][NV], wn[ITEMS][NV];
+    uint16_t dv[ITEMS], dn[ITEMS];
+    auto gload = [&](int tile, uint4 (*wr)[NV], uint16_t* dr) {
         const int64_t row0 = (int64_t)tile * rows;
         const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
         const int total = nrows * nb;
-        const uint4* qbase = reinterpret_cast<const uint4*>(qs) + row0 * nb;
+        const uint4* qbase = reinterpret_cast<const uint4*>(qs) + row0 * nb * NV;
         const uint16_t* dbase = dw + row0 * nb;
 #pragma unroll
-        for (int it = 0; it < GEMV_ITEMS; it++) {
+        for (int it = 0; it < ITEMS; it++) {
             const int g = tid + it * GEMV_THREADS;
             if (g < total) {
                 // streamed once: a non-temporal load keeps it from evicting x and the terms
-                const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(qbase + g));
-                wr[it] = make_uint4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(qbase + g * NV + v));
+                    wr[it][v] = make_uint4(t[0], t[1], t[2], t[3]);
+                }
                 dr[it] = dbase[g];
             }
         }
@@ -380,14 +458,19 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
         const int total = nrows * nb;
         float* tb = terms + buf * rows * MR * nbp;
 #pragma unroll
-        for (int it = 0; it < GEMV_ITEMS; it++) {
+        for (int it = 0; it < ITEMS; it++) {
             const int g = tid + it * GEMV_THREADS;
             if (g < total) {
                 const int r = g / nb, b = g - r * nb;
                 const float dwf = f16_bits_hw(dv[it]);
 #pragma unroll
                 for (int mr = 0; mr < MR; mr++) {
-                    int s = dot_block(wv[it], xq + mr * (K / 4) + b * 8) - 8 * sxs[mr * nb + b];
+                    const int* xw = xq + mr * (K / 4) + b * 8;
+                    int s;
+                    if constexpr (FMT == FMT_Q8_0)
+                        s = dot_block_q8(wv[it][0], wv[it][1], xw);
+                    else
+                        s = dot_block(wv[it][0], xw) - 8 * sxs[mr * nb + b];
                     float t = (float)s * dwf;
                     t = t * dxs[mr * nb + b];
                     tb[(r * MR + mr) * nbp + b] = t;
@@ -431,8 +514,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                 reinterpret_cast<float*>(y)[(int64_t)mr * N + n] = acc;
         }
 #pragma unroll
-        for (int it = 0; it < GEMV_ITEMS; it++) {
-            wv[it] = wn[it];
+        for (int it = 0; it < ITEMS; it++) {
+#pragma unroll
+            for (int v = 0; v < NV; v++) wv[it][v] = wn[it][v];
             dv[it] = dn[it];
         }
     }
@@ -674,33 +758,210 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
     }
 }
 
-tn_status check_weight(const char* op, int64_t n, int64_t k) {
+
+// ---- q8_0 prefill GEMM on integer MFMA -----------------------------------------
+//
+// With q8_0 weights both operands are int8 codes, so the block dot S_b is one
+// v_mfma_i32_16x16x32_i8 per 16x16 output tile and K block: an exact i32
+// result with no offset correction and no code conversion. The tile shape,
+// the XCD-aware tile order, the LDS double buffer and the four register sets
+// in flight are k_gemm's; the float steps are the same (S_b * d_w) * d_x and
+// ordered addition.
+//
+// Prepass: the activation rows' Q8_0 codes as int8 in natural element order
+// ([M_pad][nb][32]) and the f32 block scales transposed [nb][M_pad].
+//
+// LDS holds each 128 x 32-byte operand tile in MFMA fragment order: for row
+// tile t (16 rows) and lane group g, the 16 rows' bytes 8g..8g+7 are 128
+// consecutive bytes, so a fragment read is one conflict-free ds_read_b64 of
+// 512 contiguous bytes per wave. Lane l of the MFMA holds row l % 16, block
+// elements 8 (l / 16) .. 8 (l / 16) + 7 of both operands.
+
+template <typename XT>
+__global__ __launch_bounds__(256) void k_q8_rows_i8(const XT* __restrict__ x, int M, int M_pad, int K, int nb,
+                                                   int8_t* __restrict__ xc, float* __restrict__ dxT) {
+    // one 32-lane group per (row, block); rows >= M become zero codes, zero scale
+    const int64_t blk = (int64_t)blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5);
+    const int lane = threadIdx.x & 31;
+    if (blk >= (int64_t)M_pad * nb) return;
+    const int row = (int)(blk / nb), b = (int)(blk - (int64_t)row * nb);
+    float dx = 0.0f;
+    int q = 0;
+    if (row < M) {
+        float v = load_x<XT>(x + (int64_t)row * K + b * QK + lane);
+        q = q8_0_lane(v, &dx);
+    }
+    xc[blk * QK + lane] = (int8_t)q;
+    if (lane == 0) dxT[(int64_t)b * M_pad + row] = dx;
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline int frag_offset(int r, int g) {  // byte offset of row r, bytes 8g..8g+7, in a fragment-ordered tile
+    return ((r >> 4) * 4 + g) * 128 + (r & 15) * 8;
+}
+
+__global__ __launch_bounds__(GM_THREADS) void k_gemm_q8(const int8_t* __restrict__ xc, const float* __restrict__ dxT,
+                                                       int M, int M_pad, int nb, const uint8_t* __restrict__ qs,
+                                                       const uint16_t* __restrict__ dw, int N,
+                                                       const float* __restrict__ bias, void* __restrict__ y,
+                                                       int y_bf16) {
+    __shared__ __align__(16) uint8_t sA[2][GM_BM * QK];
+    __shared__ __align__(16) uint8_t sB[2][GM_BN * QK];
+    __shared__ __align__(16) float sdx[2][GM_BM];
+    __shared__ __align__(16) float sdw[2][GM_BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;  // wave's 64x64 sub-tile
+    const int lrow = lane & 15, lgrp = lane >> 4;
+
+    const int mt = (int)gridDim.y;
+    const int ntot = (int)(gridDim.x * gridDim.y);
+    const int id = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    int tile = id;
+    if (ntot % NUM_XCD == 0) tile = (id % NUM_XCD) * (ntot / NUM_XCD) + id / NUM_XCD;
+    const int m0 = (tile % mt) * GM_BM, n0 = (tile / mt) * GM_BN;
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    // one register set: 16 bytes of activation codes (row tid / 2, half tid % 2),
+    // 16 bytes of weight codes (column tid / 2), and (threads < GM_BM) the
+    // row's Q8_0 scale or (threads >= GM_BM) the column's f16 weight scale
+    const int prow = tid >> 1, phalf = tid & 1;
+    const int so0 = frag_offset(prow, 2 * phalf), so1 = frag_offset(prow, 2 * phalf + 1);
+    auto gload = [&](int b, uint4& a, uint4& w, float& dx, uint32_t& dws) {
+        a = *reinterpret_cast<const uint4*>(xc + ((int64_t)(m0 + prow) * nb + b) * QK + phalf * 16);
+        w = make_uint4(0u, 0u, 0u, 0u);
+        if (n0 + prow < N) w = *reinterpret_cast<const uint4*>(qs + ((int64_t)(n0 + prow) * nb + b) * QK + phalf * 16);
+        dx = 0.0f;
+        dws = 0;
+        if (tid < GM_BM) {
+            dx = dxT[(int64_t)b * M_pad + m0 + tid];
+        } else {
+            const int n = n0 + tid - GM_BM;
+            dws = (n < N) ? dw[(int64_t)n * nb + b] : 0u;
+        }
+    };
+    auto lstore = [&](int buf, const uint4& a, const uint4& w, float dx, uint32_t dws) {
+        *reinterpret_cast<uint2*>(&sA[buf][so0]) = make_uint2(a.x, a.y);
+        *reinterpret_cast<uint2*>(&sA[buf][so1]) = make_uint2(a.z, a.w);
+        *reinterpret_cast<uint2*>(&sB[buf][so0]) = make_uint2(w.x, w.y);
+        *reinterpret_cast<uint2*>(&sB[buf][so1]) = make_uint2(w.z, w.w);
+        if (tid < GM_BM)
+            sdx[buf][tid] = dx;
+        else
+            sdw[buf][tid - GM_BM] = f16_bits_hw((uint16_t)dws);
+    };
+    auto compute = [&](int buf) {
+        long afr[4], bfr[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) afr[i] = *reinterpret_cast<const long*>(&sA[buf][frag_offset(wm * 64 + i * 16 + lrow, lgrp)]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const long*>(&sB[buf][frag_offset(wn * 64 + j * 16 + lrow, lgrp)]);
+        float dwv[4];
+        f32x4 dxv[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) dwv[j] = sdw[buf][wn * 64 + j * 16 + lrow];
+#pragma unroll
+        for (int i = 0; i < 4; i++) dxv[i] = *reinterpret_cast<const f32x4*>(&sdx[buf][wm * 64 + i * 16 + lgrp * 4]);
+        const i32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                // C[row][col]: col = lane & 15 (weight column), row = 4*(lane>>4) + r
+                const i32x4 sv = __builtin_amdgcn_mfma_i32_16x16x32_i8(afr[i], bfr[j], zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float t = (float)sv[r] * dwv[j];
+                    t = t * dxv[i][r];
+                    acc[i][j][r] = acc[i][j][r] + t;
+                }
+            }
+        }
+    };
+    uint4 a_0, a_1, a_2, a_3, w_0, w_1, w_2, w_3;
+    float dx_0, dx_1, dx_2, dx_3;
+    uint32_t dw_0, dw_1, dw_2, dw_3;
+    static_assert(GM_RS == 4, "the unrolled K loop below names four register sets");
+#define TN_GQ_SET(S) a_##S, w_##S, dx_##S, dw_##S
+#define TN_GQ_STEP(S, NEXT, B)                                    \
+    {                                                             \
+        if ((B) + GM_RS < nb) gload((B) + GM_RS, TN_GQ_SET(S));   \
+        compute((B)&1);                                           \
+        if ((B) + 1 < nb) lstore(((B) + 1) & 1, TN_GQ_SET(NEXT)); \
+        __syncthreads();                                          \
+    }
+    gload(0, TN_GQ_SET(0));
+    if (1 < nb) gload(1, TN_GQ_SET(1));
+    if (2 < nb) gload(2, TN_GQ_SET(2));
+    if (3 < nb) gload(3, TN_GQ_SET(3));
+    lstore(0, TN_GQ_SET(0));
+    __syncthreads();
+    for (int b = 0; b < nb; b += GM_RS) {
+        TN_GQ_STEP(0, 1, b)
+        if (b + 1 < nb) TN_GQ_STEP(1, 2, b + 1)
+        if (b + 2 < nb) TN_GQ_STEP(2, 3, b + 2)
+        if (b + 3 < nb) TN_GQ_STEP(3, 0, b + 3)
+    }
+#undef TN_GQ_STEP
+#undef TN_GQ_SET
+
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int n = n0 + wn * 64 + j * 16 + lrow;
+            if (n >= N) continue;
+            const float bv = bias ? bias[n] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * 64 + i * 16 + lgrp * 4 + r;
+                if (m >= M) continue;
+                float v = acc[i][j][r];
+                if (bias) v = v + bv;
+                if (y_bf16)
+                    reinterpret_cast<uint16_t*>(y)[(int64_t)m * N + n] = bf16_from_f32(v);
+                else
+                    reinterpret_cast<float*>(y)[(int64_t)m * N + n] = v;
+            }
+        }
+    }
+}
+
+tn_status check_weight(const char* op, const char* fmt, int64_t n, int64_t k) {
     if (n < 0 || k <= 0 || k % QK != 0) {
         char buf[384];
         std::snprintf(buf, sizeof buf,
-                      "%s: q4_0 stores 32 elements per block, so it must have their last dim divisible by "
+                      "%s: %s stores 32 elements per block, so it must have their last dim divisible by "
                       "block size -- got %lld, which is not a multiple of 32 (shape [%lld, %lld])",
-                      op, (long long)k, (long long)n, (long long)k);
+                      op, fmt, (long long)k, (long long)n, (long long)k);
         return fail(TN_ENOTIMPL, buf);
     }
     if (n * (k / QK) > ((int64_t)1 << 40)) return fail(TN_EVALUE, std::string(op) + ": weight too large");
     return TN_OK;
 }
 
-template <int MR, typename XT, int PRO = PRO_NONE>
+template <int FMT, int MR, typename XT, int PRO = PRO_NONE>
 tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, const uint16_t* dw, int N,
                       const float* bias, void* y, int y_bf16, const float* resid = nullptr,
                       const GemvPro& po = GemvPro()) {
     const int nb = K / QK;
-    // rows per tile: as many as GEMV_ITEMS items per thread allow, but no more
+    constexpr int ITEMS = Fmt<FMT>::GEMV_ITEMS;
+    // rows per tile: as many as ITEMS items per thread allow, but no more
     // than it takes to give every CU a tile of a small matrix
-    int rows = (GEMV_THREADS * GEMV_ITEMS) / nb;
+    int rows = (GEMV_THREADS * ITEMS) / nb;
     const int spread = (int)cdiv(N, 256);
     if (rows > spread) rows = spread;
     if (rows < 1) rows = 1;
     if (rows > N) rows = N;
     // two term buffers (double-buffered across tiles)
-    if (bias && resid) return fail(TN_EINVAL, "q4_0 GEMV: bias and residual together are not supported");
+    if (bias && resid) return fail(TN_EINVAL, "quantised GEMV: bias and residual together are not supported");
     const int nbp = (nb + 3) & ~3;
     auto lds_of = [&](int r) {
         return (((size_t)MR * K + (size_t)MR * nb * 8 + 15) & ~(size_t)15) + 2 * (size_t)r * MR * nbp * 4;
@@ -711,31 +972,31 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
         lds = lds_of(rows);
     }
     if (lds > 64 * 1024) return TN_ENOTIMPL;  // caller falls through to the GEMM path
-    // (row, block) items must fit GEMV_ITEMS per thread
-    if ((int64_t)rows * nb > GEMV_THREADS * GEMV_ITEMS) return TN_ENOTIMPL;
+    // (row, block) items must fit ITEMS per thread
+    if ((int64_t)rows * nb > GEMV_THREADS * ITEMS) return TN_ENOTIMPL;
     const int64_t ntiles = cdiv(N, rows);
     // persistent: exactly as many workgroups as the device holds at once (a
     // workgroup that had to wait for a slot would start its whole share of
     // tiles late)
     int resident = 0;
     tn_status s =
-        resident_workgroups(reinterpret_cast<const void*>(&k_gemv<MR, XT, PRO>), GEMV_THREADS, lds, &resident);
+        resident_workgroups(reinterpret_cast<const void*>(&k_gemv<FMT, MR, XT, PRO>), GEMV_THREADS, lds, &resident);
     if (s != TN_OK) return s;
     const unsigned grid = (unsigned)(ntiles < resident ? ntiles : resident);
-    hipLaunchKernelGGL((k_gemv<MR, XT, PRO>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N, rows,
+    hipLaunchKernelGGL((k_gemv<FMT, MR, XT, PRO>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N, rows,
                        bias, resid, y, y_bf16, po);
     TN_LAUNCHED();
     return TN_OK;
 }
 
-template <typename XT>
+template <int FMT, typename XT>
 tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const uint8_t* qs, const uint16_t* d,
                       int64_t n, const float* bias, void* y, int y_bf16) {
     if (m == 0 || n == 0) return TN_OK;
     const int nb = (int)(k / QK);
     const size_t ysz = y_bf16 ? 2 : 4;
     // the GEMV reads x in 16-byte pieces; an unaligned x takes the GEMM path
-    if (m <= GEMV_MAX_M && nb <= GEMV_THREADS * GEMV_ITEMS && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+    if (m <= GEMV_MAX_M && nb <= GEMV_THREADS * Fmt<FMT>::GEMV_ITEMS && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
         // decode: GEMV in chunks of up to 4 rows of x (a row's result does not
         // depend on the chunking: every output is the same recurrence)
         int64_t r = 0;
@@ -745,10 +1006,10 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
             const XT* xr = x + r * k;
             void* yr = static_cast<char*>(y) + r * n * ysz;
             switch (c) {
-                case 4: s = launch_gemv<4, XT>(st, xr, (int)k, qs, d, (int)n, bias, yr, y_bf16); break;
-                case 3: s = launch_gemv<3, XT>(st, xr, (int)k, qs, d, (int)n, bias, yr, y_bf16); break;
-                case 2: s = launch_gemv<2, XT>(st, xr, (int)k, qs, d, (int)n, bias, yr, y_bf16); break;
-                default: s = launch_gemv<1, XT>(st, xr, (int)k, qs, d, (int)n, bias, yr, y_bf16); break;
+                case 4: s = launch_gemv<FMT, 4, XT>(st, xr, (int)k, qs, d, (int)n, bias, yr, y_bf16); break;
+                case 3: s = launch_gemv<FMT, 3, XT>(st, xr, (int)k, qs, d, (int)n, bias, yr, y_bf16); break;
+                case 2: s = launch_gemv<FMT, 2, XT>(st, xr, (int)k, qs, d, (int)n, bias, yr, y_bf16); break;
+                default: s = launch_gemv<FMT, 1, XT>(st, xr, (int)k, qs, d, (int)n, bias, yr, y_bf16); break;
             }
             r += c;
         }
@@ -759,26 +1020,95 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
     }
     const int64_t M_pad = cdiv(m, GM_BM) * GM_BM;
     if (M_pad > INT32_MAX || n > INT32_MAX) return fail(TN_EVALUE, "torch._C._quantized_linear: shape too large");
-    const size_t xc_bytes = (size_t)M_pad * k * 2;
+    const int64_t blocks = M_pad * nb;
+    const unsigned pgrid = (unsigned)cdiv(blocks, 8);
+    const dim3 grid((unsigned)cdiv(n, GM_BN), (unsigned)(M_pad / GM_BM));
     const size_t dx_bytes = (size_t)M_pad * nb * 4;
     void* ws = nullptr;
-    tn_status s = workspace(st, xc_bytes + 2 * dx_bytes, &ws);
-    if (s != TN_OK) return s;
-    uint16_t* xc = static_cast<uint16_t*>(ws);
-    float* dxT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes);
-    float* corrT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes + dx_bytes);
-    {
-        const int64_t blocks = M_pad * nb;
-        const unsigned grid = (unsigned)cdiv(blocks, 8);
-        hipLaunchKernelGGL((k_q8_rows<XT>), dim3(grid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
+    if constexpr (FMT == FMT_Q8_0) {
+        const size_t xc_bytes = (size_t)M_pad * k;
+        tn_status s = workspace(st, xc_bytes + dx_bytes, &ws);
+        if (s != TN_OK) return s;
+        int8_t* xc = static_cast<int8_t*>(ws);
+        float* dxT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes);
+        hipLaunchKernelGGL((k_q8_rows_i8<XT>), dim3(pgrid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
+                           dxT);
+        TN_LAUNCHED();
+        hipLaunchKernelGGL(k_gemm_q8, grid, dim3(GM_THREADS), 0, st, xc, dxT, (int)m, (int)M_pad, nb, qs, d, (int)n,
+                           bias, y, y_bf16);
+        TN_LAUNCHED();
+    } else {
+        const size_t xc_bytes = (size_t)M_pad * k * 2;
+        tn_status s = workspace(st, xc_bytes + 2 * dx_bytes, &ws);
+        if (s != TN_OK) return s;
+        uint16_t* xc = static_cast<uint16_t*>(ws);
+        float* dxT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes);
+        float* corrT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes + dx_bytes);
+        hipLaunchKernelGGL((k_q8_rows<XT>), dim3(pgrid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
                            dxT, corrT);
         TN_LAUNCHED();
+        hipLaunchKernelGGL(k_gemm, grid, dim3(GM_THREADS), 0, st, xc, dxT, corrT, (int)m, (int)M_pad, nb, qs, d,
+                           (int)n, bias, y, y_bf16);
+        TN_LAUNCHED();
     }
-    dim3 grid((unsigned)cdiv(n, GM_BN), (unsigned)(M_pad / GM_BM));
-    hipLaunchKernelGGL(k_gemm, grid, dim3(GM_THREADS), 0, st, xc, dxT, corrT, (int)m, (int)M_pad, nb, qs, d, (int)n,
-                       bias, y, y_bf16);
+    return TN_OK;
+}
+
+// The codec entry points of one format.
+template <int FMT>
+tn_status codec_launch(const char* op, void* stream, int64_t n, int64_t k, int kind, const void* in0,
+                       const void* in1, void* out0, void* out1) {
+    tn_status s = check_weight(op, Fmt<FMT>::name, n, k);
+    if (s != TN_OK) return s;
+    const int64_t nblocks = n * (k / QK);
+    if (!nblocks) return TN_OK;
+    if (!in0 || !out0 || (kind >= 2 ? !in1 : !out1)) return fail(TN_EVALUE, std::string(op) + ": null pointer");
+    const dim3 grid((unsigned)cdiv(nblocks, 256));
+    hipStream_t st = (hipStream_t)stream;
+    switch (kind) {
+        case 0:  // blob -> planes
+            hipLaunchKernelGGL(k_from_blob<FMT>, grid, dim3(256), 0, st, static_cast<const uint8_t*>(in0), nblocks,
+                               static_cast<uint8_t*>(out0), static_cast<uint16_t*>(out1));
+            break;
+        case 1:  // f32 -> planes
+            hipLaunchKernelGGL(k_quantize_w<FMT>, grid, dim3(256), 0, st, static_cast<const float*>(in0), nblocks,
+                               static_cast<uint8_t*>(out0), static_cast<uint16_t*>(out1));
+            break;
+        case 2:  // planes -> blob
+            hipLaunchKernelGGL(k_to_blob<FMT>, grid, dim3(256), 0, st, static_cast<const uint8_t*>(in0),
+                               static_cast<const uint16_t*>(in1), nblocks, static_cast<uint8_t*>(out0));
+            break;
+        default:  // planes -> f32
+            hipLaunchKernelGGL(k_dequantize<FMT>, grid, dim3(256), 0, st, static_cast<const uint8_t*>(in0),
+                               static_cast<const uint16_t*>(in1), nblocks, static_cast<float*>(out0));
+            break;
+    }
     TN_LAUNCHED();
     return TN_OK;
+}
+
+template <int FMT>
+tn_status linear_entry(void* stream, const void* x, int x_dtype, int64_t m, int64_t k, const uint8_t* qs,
+                       const uint16_t* d, int64_t n, const float* bias, void* y, int y_dtype) {
+    const char* OP = "torch._C._quantized_linear";
+    if (x_dtype != TN_F32 && x_dtype != TN_BF16)
+        return fail(TN_ENOTIMPL, std::string(OP) +
+                                     ": the activation must be float32 (or bfloat16, widened exactly in-kernel) "
+                                     "on the hip device");
+    if (y_dtype != TN_F32 && y_dtype != TN_BF16)
+        return fail(TN_ENOTIMPL, std::string(OP) + ": the output must be float32 or bfloat16");
+    if (k <= 0 || k % QK != 0 || m < 0 || n < 0) {
+        char buf[256];
+        std::snprintf(buf, sizeof buf, "%s: mat1 and mat2 shapes cannot be multiplied ([%lld, %lld] and %lldx%lld)",
+                      OP, (long long)m, (long long)k, (long long)k, (long long)n);
+        return fail(TN_EINVAL, buf);
+    }
+    if (m > 0 && n > 0 && (!x || !qs || !d || !y)) return fail(TN_EVALUE, std::string(OP) + ": null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    const int yb = y_dtype == TN_BF16;
+    if (x_dtype == TN_F32)
+        return linear_impl<FMT, float>(st, static_cast<const float*>(x), m, k, qs, d, n, bias, y, yb);
+    return linear_impl<FMT, uint16_t>(st, static_cast<const uint16_t*>(x), m, k, qs, d, n, bias, y, yb);
 }
 
 }  // namespace
@@ -788,22 +1118,22 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
 // running tn_rmsnorm / tn_silu_mul, then tn_q4_0_linear, then tn_add.
 tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, const GemvPro& po, const uint8_t* qs,
                         const uint16_t* d, int64_t n, const float* resid, float* y) {
-    tn_status s = check_weight("linear_decode", n, k);
+    tn_status s = check_weight("linear_decode", "q4_0", n, k);
     if (s != TN_OK) return s;
     if (k > LINEAR_DECODE_MAX_K || n > INT32_MAX) return fail(TN_ENOTIMPL, "linear_decode: shape too large");
     if (n == 0) return TN_OK;
     switch (pro) {
         case PRO_RMSNORM:
-            s = launch_gemv<1, float, PRO_RMSNORM>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po);
+            s = launch_gemv<FMT_Q4_0, 1, float, PRO_RMSNORM>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po);
             break;
-        case PRO_SILU: s = launch_gemv<1, float, PRO_SILU>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po); break;
+        case PRO_SILU: s = launch_gemv<FMT_Q4_0, 1, float, PRO_SILU>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po); break;
         case PRO_COMBINE:
             if (po.head_dim < 4 || po.head_dim % 4 != 0 || k % po.head_dim != 0 || po.nsplit < 1 ||
                 po.nsplit > STEP_MAX_SPLITS || !po.part_o || !po.part_ml || !po.len)
                 return fail(TN_EINVAL, "linear_decode: bad attention partials");
-            s = launch_gemv<1, float, PRO_COMBINE>(st, po.part_o, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po);
+            s = launch_gemv<FMT_Q4_0, 1, float, PRO_COMBINE>(st, po.part_o, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po);
             break;
-        default: s = launch_gemv<1, float, PRO_NONE>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po); break;
+        default: s = launch_gemv<FMT_Q4_0, 1, float, PRO_NONE>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po); break;
     }
     if (s == TN_ENOTIMPL) return fail(TN_ENOTIMPL, "linear_decode: the activation row does not fit the GEMV");
     return s;
@@ -816,51 +1146,35 @@ using namespace tn;
 extern "C" {
 
 tn_status tn_q4_0_from_blob(void* stream, const uint8_t* blob, int64_t n, int64_t k, uint8_t* qs, uint16_t* d) {
-    tn_status s = check_weight("torch._C._quantized_to", n, k);
-    if (s != TN_OK) return s;
-    const int64_t nblocks = n * (k / QK);
-    if (!nblocks) return TN_OK;
-    if (!blob || !qs || !d) return fail(TN_EVALUE, "tn_q4_0_from_blob: null pointer");
-    hipLaunchKernelGGL(k_from_blob, dim3((unsigned)cdiv(nblocks, 256)), dim3(256), 0, (hipStream_t)stream, blob,
-                       nblocks, qs, d);
-    TN_LAUNCHED();
-    return TN_OK;
+    return codec_launch<FMT_Q4_0>("torch._C._quantized_to", stream, n, k, 0, blob, nullptr, qs, d);
 }
 
 tn_status tn_q4_0_to_blob(void* stream, const uint8_t* qs, const uint16_t* d, int64_t n, int64_t k, uint8_t* blob) {
-    tn_status s = check_weight("torch._C._quantized_blob", n, k);
-    if (s != TN_OK) return s;
-    const int64_t nblocks = n * (k / QK);
-    if (!nblocks) return TN_OK;
-    if (!blob || !qs || !d) return fail(TN_EVALUE, "tn_q4_0_to_blob: null pointer");
-    hipLaunchKernelGGL(k_to_blob, dim3((unsigned)cdiv(nblocks, 256)), dim3(256), 0, (hipStream_t)stream, qs, d,
-                       nblocks, blob);
-    TN_LAUNCHED();
-    return TN_OK;
+    return codec_launch<FMT_Q4_0>("torch._C._quantized_blob", stream, n, k, 2, qs, d, blob, nullptr);
 }
 
 tn_status tn_q4_0_quantize(void* stream, const float* w, int64_t n, int64_t k, uint8_t* qs, uint16_t* d) {
-    tn_status s = check_weight("torch._C._quantize", n, k);
-    if (s != TN_OK) return s;
-    const int64_t nblocks = n * (k / QK);
-    if (!nblocks) return TN_OK;
-    if (!w || !qs || !d) return fail(TN_EVALUE, "tn_q4_0_quantize: null pointer");
-    hipLaunchKernelGGL(k_quantize_w, dim3((unsigned)cdiv(nblocks, 256)), dim3(256), 0, (hipStream_t)stream, w,
-                       nblocks, qs, d);
-    TN_LAUNCHED();
-    return TN_OK;
+    return codec_launch<FMT_Q4_0>("torch._C._quantize", stream, n, k, 1, w, nullptr, qs, d);
 }
 
 tn_status tn_q4_0_dequantize(void* stream, const uint8_t* qs, const uint16_t* d, int64_t n, int64_t k, float* out) {
-    tn_status s = check_weight("torch._C._dequantize", n, k);
-    if (s != TN_OK) return s;
-    const int64_t nblocks = n * (k / QK);
-    if (!nblocks) return TN_OK;
-    if (!out || !qs || !d) return fail(TN_EVALUE, "tn_q4_0_dequantize: null pointer");
-    hipLaunchKernelGGL(k_dequantize, dim3((unsigned)cdiv(nblocks, 256)), dim3(256), 0, (hipStream_t)stream, qs, d,
-                       nblocks, out);
-    TN_LAUNCHED();
-    return TN_OK;
+    return codec_launch<FMT_Q4_0>("torch._C._dequantize", stream, n, k, 3, qs, d, out, nullptr);
+}
+
+tn_status tn_q8_0_from_blob(void* stream, const uint8_t* blob, int64_t n, int64_t k, int8_t* qs, uint16_t* d) {
+    return codec_launch<FMT_Q8_0>("torch._C._quantized_to", stream, n, k, 0, blob, nullptr, qs, d);
+}
+
+tn_status tn_q8_0_to_blob(void* stream, const int8_t* qs, const uint16_t* d, int64_t n, int64_t k, uint8_t* blob) {
+    return codec_launch<FMT_Q8_0>("torch._C._quantized_blob", stream, n, k, 2, qs, d, blob, nullptr);
+}
+
+tn_status tn_q8_0_quantize(void* stream, const float* w, int64_t n, int64_t k, int8_t* qs, uint16_t* d) {
+    return codec_launch<FMT_Q8_0>("torch._C._quantize", stream, n, k, 1, w, nullptr, qs, d);
+}
+
+tn_status tn_q8_0_dequantize(void* stream, const int8_t* qs, const uint16_t* d, int64_t n, int64_t k, float* out) {
+    return codec_launch<FMT_Q8_0>("torch._C._dequantize", stream, n, k, 3, qs, d, out, nullptr);
 }
 
 tn_status tn_q4_0_linear_decode(void* stream, const float* x, int64_t k, int prologue, const float* prologue_w,
@@ -889,25 +1203,13 @@ tn_status tn_q4_0_linear_decode(void* stream, const float* x, int64_t k, int pro
 
 tn_status tn_q4_0_linear(void* stream, const void* x, int x_dtype, int64_t m, int64_t k, const uint8_t* qs,
                          const uint16_t* d, int64_t n, const float* bias, void* y, int y_dtype) {
-    const char* OP = "torch._C._quantized_linear";
-    if (x_dtype != TN_F32 && x_dtype != TN_BF16)
-        return fail(TN_ENOTIMPL, std::string(OP) +
-                                     ": the activation must be float32 (or bfloat16, widened exactly in-kernel) "
-                                     "on the hip device");
-    if (y_dtype != TN_F32 && y_dtype != TN_BF16)
-        return fail(TN_ENOTIMPL, std::string(OP) + ": the output must be float32 or bfloat16");
-    if (k <= 0 || k % QK != 0 || m < 0 || n < 0) {
-        char buf[256];
-        std::snprintf(buf, sizeof buf, "%s: mat1 and mat2 shapes cannot be multiplied ([%lld, %lld] and %lldx%lld)",
-                      OP, (long long)m, (long long)k, (long long)k, (long long)n);
-        return fail(TN_EINVAL, buf);
-    }
-    if (m > 0 && n > 0 && (!x || !qs || !d || !y)) return fail(TN_EVALUE, std::string(OP) + ": null pointer");
-    hipStream_t st = (hipStream_t)stream;
-    const int yb = y_dtype == TN_BF16;
-    if (x_dtype == TN_F32)
-        return linear_impl<float>(st, static_cast<const float*>(x), m, k, qs, d, n, bias, y, yb);
-    return linear_impl<uint16_t>(st, static_cast<const uint16_t*>(x), m, k, qs, d, n, bias, y, yb);
+    return linear_entry<FMT_Q4_0>(stream, x, x_dtype, m, k, qs, d, n, bias, y, y_dtype);
+}
+
+tn_status tn_q8_0_linear(void* stream, const void* x, int x_dtype, int64_t m, int64_t k, const int8_t* qs,
+                         const uint16_t* d, int64_t n, const float* bias, void* y, int y_dtype) {
+    return linear_entry<FMT_Q8_0>(stream, x, x_dtype, m, k, reinterpret_cast<const uint8_t*>(qs), d, n, bias, y,
+                                  y_dtype);
 }
 
 }  // extern "C"

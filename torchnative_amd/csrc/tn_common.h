@@ -229,7 +229,7 @@ struct GemvPro {
     int nsplit = 0, head_dim = 0, cap = 0;
 };
 
-// One f32 row through a q4_0 linear (q4_0.hip), y[n] = Q8_0(pro(x)) . W^T
+// One f32 row through a q4_0 linear (qlinear.hip), y[n] = Q8_0(pro(x)) . W^T
 // (+ resid[n]): pro is a LinearPrologue (PRO_RMSNORM scales by po.w with
 // po.eps; PRO_SILU reads x as [gate | up], 2k floats; PRO_COMBINE ignores x
 // and merges po's attention partials). Bit-identical to the separate ops in
