@@ -41,6 +41,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
+INT8_PEAK_TOPS = 5000.0
+
+# weight format -> (GGML bytes per block, device code bytes per block)
+_BLOCK = {"q4_0": (18, 16), "q8_0": (34, 32)}
 
 
 def _synth_q4_0_blob(n, k, sigma, seed):
@@ -54,6 +58,22 @@ def _synth_q4_0_blob(n, k, sigma, seed):
     blob[:, :, 0:2] = d.view(np.uint8).reshape(n, nb, 2)
     blob[:, :, 2:] = nib[:, :, :16] | (nib[:, :, 16:] << 4)
     return blob.reshape(-1)
+
+
+def _synth_q8_0_blob(n, k, sigma, seed):
+    """Q8_0 blob: codes uniform in [-127, 127], d = f16_rne(|N(0, sigma)| / 127)."""
+    rng = np.random.default_rng(seed)
+    nb = k // 32
+    codes = rng.integers(-127, 128, size=(n, nb, 32), dtype=np.int8)
+    d = (np.abs(rng.standard_normal((n, nb))) * sigma / 127.0).astype(np.float32).astype(np.float16)
+    blob = np.empty((n, nb, 34), dtype=np.uint8)
+    blob[:, :, 0:2] = d.view(np.uint8).reshape(n, nb, 2)
+    blob[:, :, 2:] = codes.view(np.uint8)
+    return blob.reshape(-1)
+
+
+def _synth_blob(fmt, n, k, sigma, seed):
+    return (_synth_q8_0_blob if fmt == "q8_0" else _synth_q4_0_blob)(n, k, sigma, seed)
 
 
 class Timer:
@@ -103,25 +123,27 @@ def bench_sdpa(tn, L, dtype, steps, warmup, B=1, Hq=9, Hkv=3, S=2048, D=64, seed
                          "traffic": None}}
 
 
-def bench_gemv(tn, L, steps, warmup, copies=1024):
+def bench_gemv(tn, L, steps, warmup, copies=1024, fmt="q4_0"):
     n, k = 1536, 576
     lib = L.lib()
+    blob_b, code_b = _BLOCK[fmt]
+    from_blob, linear = getattr(lib, f"tn_{fmt}_from_blob"), getattr(lib, f"tn_{fmt}_linear")
     rng = np.random.default_rng(1)
     x = tn.tensor(rng.standard_normal((1, k)).astype(np.float32), device="hip")
     # 1,024 distinct [1536, 576] weights, contiguous: one launch streams all of them
-    qs = tn.empty((copies * n * k // 2,), "uint8", "hip")
+    qs = tn.empty((copies * n * k // 32 * code_b,), "uint8", "hip")
     dd = tn.empty((copies * n * k // 32 * 2,), "uint8", "hip")
     chunk = 64
     for c0 in range(0, copies, chunk):
-        blob = _synth_q4_0_blob(chunk * n, k, 0.02, 1000 + c0)
+        blob = _synth_blob(fmt, chunk * n, k, 0.02, 1000 + c0)
         bt = tn.tensor(blob, device="hip")
-        off_q = c0 * n * k // 2
+        off_q = c0 * n * k // 32 * code_b
         off_d = c0 * n * k // 32 * 2
-        L.check(lib.tn_q4_0_from_blob(None, bt.data_ptr(), chunk * n, k, qs.data_ptr() + off_q, dd.data_ptr() + off_d))
+        L.check(from_blob(None, bt.data_ptr(), chunk * n, k, qs.data_ptr() + off_q, dd.data_ptr() + off_d))
     y = tn.empty((1, copies * n), "float32", "hip")
 
     def step_all():
-        st = lib.tn_q4_0_linear(None, x.data_ptr(), L.TN_F32, 1, k, qs.data_ptr(), dd.data_ptr(), copies * n, None,
+        st = linear(None, x.data_ptr(), L.TN_F32, 1, k, qs.data_ptr(), dd.data_ptr(), copies * n, None,
                                 y.data_ptr(), L.TN_F32)
         if st:
             L.check(st)
@@ -129,7 +151,7 @@ def bench_gemv(tn, L, steps, warmup, copies=1024):
     # C1 is the first GPU work of a run: a longer warm-up (about 10 ms) lets
     # the clocks settle before the timed region
     ms, kern_ms = Timer(tn).run(step_all, steps, max(warmup, 100))
-    w_bytes = n * (k // 32) * 18
+    w_bytes = n * (k // 32) * blob_b
     per_copy = w_bytes + n * 4
     total_bytes = copies * per_copy + k * 4
     ach = total_bytes / (kern_ms * 1e-3) / 1e9
@@ -139,7 +161,7 @@ def bench_gemv(tn, L, steps, warmup, copies=1024):
     def step_one():
         c = idx[0] % copies
         idx[0] += 1
-        st = lib.tn_q4_0_linear(None, x.data_ptr(), L.TN_F32, 1, k, qs.data_ptr() + c * n * k // 2,
+        st = linear(None, x.data_ptr(), L.TN_F32, 1, k, qs.data_ptr() + c * n * k // 32 * code_b,
                                 dd.data_ptr() + c * n * k // 16, n, None, y.data_ptr(), L.TN_F32)
         if st:
             L.check(st)
@@ -153,16 +175,17 @@ def bench_gemv(tn, L, steps, warmup, copies=1024):
                          "frac": ach / HBM_PEAK_GBS, "traffic": None}}
 
 
-def bench_gemm(tn, L, steps, warmup):
+def bench_gemm(tn, L, steps, warmup, fmt="q4_0"):
     m, k, n = 512, 4096, 14336
     lib = L.lib()
+    linear = getattr(lib, f"tn_{fmt}_linear")
     rng = np.random.default_rng(3)
     x = tn.tensor(rng.standard_normal((m, k)).astype(np.float32), dtype="bfloat16", device="hip")
-    q = tn._quantized_from_blob(_synth_q4_0_blob(n, k, 0.01, 33).tobytes(), (n, k), "q4_0", device="hip")
+    q = tn._quantized_from_blob(_synth_blob(fmt, n, k, 0.01, 33).tobytes(), (n, k), fmt, device="hip")
     y = tn.empty((m, n), "bfloat16", "hip")
 
     def step():
-        st = lib.tn_q4_0_linear(None, x.data_ptr(), L.TN_BF16, m, k, q._qs.data_ptr(), q._d.data_ptr(), n, None,
+        st = linear(None, x.data_ptr(), L.TN_BF16, m, k, q._qs.data_ptr(), q._d.data_ptr(), n, None,
                                 y.data_ptr(), L.TN_BF16)
         if st:
             L.check(st)
@@ -170,10 +193,12 @@ def bench_gemm(tn, L, steps, warmup):
     ms, kern_ms = Timer(tn).run(step, steps, warmup)
     flops = 2.0 * m * k * n
     ach = flops / (kern_ms * 1e-3) / 1e12
+    # the block dots run on bf16 MFMA for q4_0 and on int8 MFMA for q8_0
+    peak, unit = (INT8_PEAK_TOPS, "TOP/s") if fmt == "q8_0" else (BF16_PEAK_TFLOPS, "TFLOP/s")
     return {"ms_per_step": ms, "kernel_ms": kern_ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
-            "bytes": n * (k // 32) * 18 + m * k * 2 + m * n * 2,
-            "roofline": {"bound": "mfma", "achieved": ach, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": ach / BF16_PEAK_TFLOPS, "traffic": None}}
+            "bytes": n * (k // 32) * _BLOCK[fmt][0] + m * k * 2 + m * n * 2,
+            "roofline": {"bound": "mfma", "achieved": ach, "peak": peak, "unit": unit,
+                         "frac": ach / peak, "traffic": None}}
 
 
 def bench_decode(tn, L, steps, warmup, sets=3):
@@ -349,7 +374,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c3,c4,c5)")
+    ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c3,c4,c5,q8c1,q8c3)")
     ap.add_argument("--no-graph", action="store_true",
                     help="c5: time the decode steps as separate launches only (no HIP graph)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -380,6 +405,12 @@ def main():
     if want("c3"):
         print("bench: c3 q4_0 GEMM", file=sys.stderr, flush=True)
         parts["c3_q4_gemm"] = bench_gemm(tn, L, args.steps, args.warmup)
+    if want("q8c1"):
+        print("bench: q8_0 GEMV at the c1 shape", file=sys.stderr, flush=True)
+        parts["q8_0_gemv_c1_shape"] = bench_gemv(tn, L, args.steps, args.warmup, fmt="q8_0")
+    if want("q8c3"):
+        print("bench: q8_0 GEMM at the c3 shape", file=sys.stderr, flush=True)
+        parts["q8_0_gemm_c3_shape"] = bench_gemm(tn, L, args.steps, args.warmup, fmt="q8_0")
     if want("c4"):
         print("bench: c4 decode attention", file=sys.stderr, flush=True)
         parts["c4_decode_attention"] = bench_decode(tn, L, args.steps, args.warmup)

@@ -14,7 +14,7 @@ from .tensor import Tensor
 
 
 class QuantizedLinear:
-    """nn.Linear with a q4_0 weight [out_features, in_features]."""
+    """nn.Linear with a block-quantised (q4_0 or q8_0) weight [out_features, in_features]."""
 
     def __init__(self, qweight: "_C.QTensor", bias: Tensor | None = None):
         self.qweight = qweight
@@ -29,9 +29,9 @@ class QuantizedLinear:
 
     @classmethod
     def from_blob(cls, blob: bytes, out_features: int, in_features: int, bias: Tensor | None = None,
-                  device="hip") -> "QuantizedLinear":
-        """A layer over an existing GGML q4_0 blob (a GGUF file's own blocks)."""
-        return cls(_C._quantized_from_blob(blob, (out_features, in_features), "q4_0", device), bias)
+                  device="hip", format: str = "q4_0") -> "QuantizedLinear":
+        """A layer over an existing GGML blob (a GGUF file's own blocks)."""
+        return cls(_C._quantized_from_blob(blob, (out_features, in_features), format, device), bias)
 
     def to(self, device) -> "QuantizedLinear":
         """quant/__init__.py:221-237: blocks move byte for byte."""
