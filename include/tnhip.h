@@ -165,6 +165,35 @@ tn_status tn_q8_0_linear(void* stream, const void* x, int x_dtype, int64_t m, in
                          const int8_t* qs, const uint16_t* d, int64_t n, const float* bias,
                          void* y, int y_dtype);
 
+/* ---- GGML q4_k weights ----
+ * `_quantize(t, "q4_k")` and its matmul (k_quants.rs:1442-1746): 256-element
+ * super-blocks of 144 bytes (f16 d, f16 dmin, 12 bytes of packed 6-bit scales
+ * and mins, 128 nibble bytes), whose VecDotType is Q8_K (k_quants.rs:2336-2413).
+ * On the device a q4_k weight [N, K] (K % 256 == 0) is ONE plane `w` of
+ * N * K/256 super-blocks of 144 bytes, row-major. Each keeps its first 16
+ * bytes; in each of its four 32-byte nibble chunks, GGML byte 8g + l
+ * (g = 0..3, l = 0..7) is stored at byte 4l + g, so a dword holds the four
+ * elements of one position mod 8 (the operands of one lane of the reference's
+ * dot). Pointers must be 16-byte aligned.
+ *   from_blob / to_blob: `_quantized_to` / `_quantized_blob` (quant.rs:384-405,
+ *     :213-221): GGML bytes <-> the device layout, byte for byte;
+ *   quantize: BlockQ4K::from_float (k_quants.rs:1570-1654; llama.cpp's
+ *     quantize_row_q4_K_ref with make_qkx2_quants), bit-exact, x f32 [n, k];
+ *   dequantize: BlockQ4K::to_float (k_quants.rs:1722-1746);
+ *   linear: `_quantized_linear` with each row of x quantised to Q8_K
+ *     (BlockQ8K::from_float, k_quants.rs:2375-2413) and every output
+ *     BlockQ4K::vec_dot_unopt (k_quants.rs:1478-1558): eight f32 lane sums
+ *     sums[l] += (d_w*d_x) * aux32[l] and sumf -= (dmin_w*d_x) * sumi, in
+ *     super-block order, result sumf + (sums[0] + ... + sums[7]) summed in
+ *     order (+ bias[n]); bit-identical for every m.
+ * Refuses k % 256 != 0 with the reference's block-size message. */
+tn_status tn_q4_k_from_blob(void* stream, const uint8_t* blob, int64_t n, int64_t k, uint8_t* w);
+tn_status tn_q4_k_to_blob(void* stream, const uint8_t* w, int64_t n, int64_t k, uint8_t* blob);
+tn_status tn_q4_k_quantize(void* stream, const float* x, int64_t n, int64_t k, uint8_t* w);
+tn_status tn_q4_k_dequantize(void* stream, const uint8_t* w, int64_t n, int64_t k, float* out);
+tn_status tn_q4_k_linear(void* stream, const void* x, int x_dtype, int64_t m, int64_t k,
+                         const uint8_t* w, int64_t n, const float* bias, void* y, int y_dtype);
+
 /* ---- scaled dot-product attention ----
  * `aten._scaled_dot_product_flash_attention_for_cpu(q, k, v, dropout_p=0.,
  * is_causal=False, *, attn_mask=None, scale=None) -> (out, logsumexp)`

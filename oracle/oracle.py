@@ -19,7 +19,9 @@ __all__ = [
     "f16_from_f32", "f16_to_f32", "bf16_from_f32", "bf16_to_f32",
     "q4_0_quantize", "q4_0_dequantize", "q8_0_quantize", "q8_0_dequantize",
     "vec_dot_q4_0_q8_0", "q4_0_linear", "vec_dot_q8_0_q8_0", "q8_0_linear", "sdpa", "sdpa_bf16",
-    "q4_0_parts", "q8_0_parts", "exact_linear_q4_0", "exact_linear_q8_0", "synth_q8_0_weight", "gamma", "accumulation_k",
+    "q4_0_parts", "q8_0_parts", "exact_linear_q4_0", "exact_linear_q8_0", "synth_q8_0_weight",
+    "q4_k_quantize", "q4_k_dequantize", "q8_k_quantize", "vec_dot_q4_k_q8_k", "q4_k_linear", "q4_k_parts",
+    "q8_k_parts", "exact_linear_q4_k", "accumulation_k_q4_k", "synth_q4_k_weight", "gamma", "accumulation_k",
     "linear_bound", "sdpa_closed_form", "sdpa_det", "q8_0_ties", "signed_max_ties",
     "synth_q4_0_weight", "sdpa_tolerance",
 ]
@@ -29,6 +31,9 @@ LIB_PATH = os.path.join(HERE, "libtnref.so")
 QK = 32
 Q4_0_BYTES = 18
 Q8_0_BYTES = 34
+QK_K = 256
+Q4_K_BYTES = 144
+Q8_K_BYTES = 292
 U32 = 2.0 ** -24
 U64 = 2.0 ** -53
 
@@ -66,6 +71,12 @@ def lib():
     L.tnref_vec_dot_q8_0_q8_0.restype = ctypes.c_float
     L.tnref_vec_dot_q8_0_q8_0.argtypes = [I64, P, P]
     L.tnref_q8_0_linear.argtypes = [I64, I64, I64, P, P, P, P, I]
+    for name in ("tnref_q4_k_quantize", "tnref_q8_k_quantize"):
+        getattr(L, name).argtypes = [P, I64, P]
+    L.tnref_q4_k_dequantize.argtypes = [P, I64, P]
+    L.tnref_vec_dot_q4_k_q8_k.restype = ctypes.c_float
+    L.tnref_vec_dot_q4_k_q8_k.argtypes = [I64, P, P]
+    L.tnref_q4_k_linear.argtypes = [I64, I64, I64, P, P, P, P, I]
     for name in ("tnref_sdpa_f32", "tnref_sdpa_f64"):
         fn = getattr(L, name)
         fn.restype = I
@@ -148,6 +159,35 @@ def vec_dot_q4_0_q8_0(k, w_row: bytes, xq_row: bytes) -> float:
     return float(np.float32(lib().tnref_vec_dot_q4_0_q8_0(k, _p(w), _p(x))))
 
 
+def q4_k_quantize(x) -> bytes:
+    """BlockQ4K::from_float (K:1570-1654): 144-byte super-blocks of 256."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size // QK_K * Q4_K_BYTES, dtype=np.uint8)
+    lib().tnref_q4_k_quantize(_p(x), x.size, _p(out))
+    return out.tobytes()
+
+
+def q4_k_dequantize(blob, n) -> np.ndarray:
+    b = np.frombuffer(bytes(blob), dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    lib().tnref_q4_k_dequantize(_p(b), n, _p(out))
+    return out
+
+
+def q8_k_quantize(x) -> bytes:
+    """BlockQ8K::from_float (K:2375-2413): 292-byte blocks of 256."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size // QK_K * Q8_K_BYTES, dtype=np.uint8)
+    lib().tnref_q8_k_quantize(_p(x), x.size, _p(out))
+    return out.tobytes()
+
+
+def vec_dot_q4_k_q8_k(k, w_row: bytes, xq_row: bytes) -> float:
+    w = np.frombuffer(bytes(w_row), dtype=np.uint8)
+    x = np.frombuffer(bytes(xq_row), dtype=np.uint8)
+    return float(np.float32(lib().tnref_vec_dot_q4_k_q8_k(k, _p(w), _p(x))))
+
+
 def vec_dot_q8_0_q8_0(k, w_row: bytes, xq_row: bytes) -> float:
     w = np.frombuffer(bytes(w_row), dtype=np.uint8)
     x = np.frombuffer(bytes(xq_row), dtype=np.uint8)
@@ -177,6 +217,19 @@ def q4_0_linear(x, w_blob, n, bias=None, threads=1) -> np.ndarray:
 def q8_0_linear(x, w_blob, n, bias=None, threads=1) -> np.ndarray:
     """The same with a Q8_0 weight blob (34-byte blocks, K:738-757)."""
     return _linear(lib().tnref_q8_0_linear, Q8_0_BYTES, x, w_blob, n, bias, threads)
+
+
+def q4_k_linear(x, w_blob, n, bias=None, threads=1) -> np.ndarray:
+    """A Q4_K weight blob: Q8_K activations and BlockQ4K::vec_dot_unopt."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    m = x.size // k if k else 0
+    w = np.frombuffer(bytes(w_blob), dtype=np.uint8)
+    assert w.size == n * (k // QK_K) * Q4_K_BYTES, "blob size does not match [N, K]"
+    y = np.empty(x.shape[:-1] + (n,), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    assert lib().tnref_q4_k_linear(m, k, n, _p(x), _p(w), _p(b), _p(y), int(threads)) == 0
+    return y
 
 
 # --- SDPA -------------------------------------------------------------------
@@ -270,6 +323,59 @@ def _exact_linear(dw, qw, xq_blob, m, n, k):
         rel = nb * U64 / (1.0 - nb * U64)
     abs_sum = (absints.astype(np.float64) * np.abs(scale)).sum(axis=2)
     return value, abs_sum, rel * abs_sum
+
+
+def q4_k_parts(blob, n, k):
+    """(d, dmin float64 [n, nb], sc, mn int64 [n, nb, 8], q int64 [n, nb, 256])
+    straight from the bytes (K:153-159 layout; the 6-bit packing of
+    get_scale_min_k4, utils.rs:50-60, written out independently)."""
+    raw = np.frombuffer(bytes(blob), dtype=np.uint8).reshape(n, k // QK_K, Q4_K_BYTES)
+    d = raw[..., 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
+    dmin = raw[..., 2:4].copy().view(np.float16).astype(np.float64)[..., 0]
+    s = raw[..., 4:16].astype(np.int64)
+    sc = np.concatenate([s[..., 0:4] & 63, (s[..., 8:12] & 15) | ((s[..., 0:4] >> 6) << 4)], axis=-1)
+    mn = np.concatenate([s[..., 4:8] & 63, (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)], axis=-1)
+    qs = raw[..., 16:].astype(np.int64).reshape(n, k // QK_K, 4, 32)
+    q = np.stack([qs & 15, qs >> 4], axis=3).reshape(n, k // QK_K, QK_K)
+    return d, dmin, sc, mn, q
+
+
+def q8_k_parts(blob, m, k):
+    raw = np.frombuffer(bytes(blob), dtype=np.uint8).reshape(m, k // QK_K, Q8_K_BYTES)
+    d = raw[..., 0:4].copy().view(np.float32).astype(np.float64)[..., 0]
+    q = raw[..., 4:4 + QK_K].copy().view(np.int8).astype(np.int64)
+    return d, q
+
+
+def exact_linear_q4_k(xq_blob, w_blob, m, n, k):
+    """(value, abs_sum, ref_err) float64 [m, n]: the exact value of
+    sum over super-blocks of (d_w*d_x) * sum_j sc_j * <q8, nib>_j - (dmin_w*d_x)
+    * sum_j m_j * sum(q8)_j, from the two blobs. Each super-block term is exact
+    in float64 only to rounding of its products, which ref_err bounds."""
+    d, dmin, sc, mn, q = q4_k_parts(w_blob, n, k)
+    dx, qx = q8_k_parts(xq_blob, m, k)
+    nb = k // QK_K
+    qx8 = qx.reshape(m, nb, 8, 32)
+    q8w = q.reshape(n, nb, 8, 32)
+    dots = np.einsum("rbjk,objk->robj", qx8, q8w)               # per sub-block integer dots
+    sums = qx8.sum(axis=-1)                                      # [m, nb, 8]
+    ints = (dots * sc[None]).sum(-1)                             # sum_j sc_j * dot_j
+    absints = (np.einsum("rbjk,objk->robj", np.abs(qx8), q8w) * sc[None]).sum(-1)
+    mins = (sums[:, None] * mn[None]).sum(-1)                    # sum_j m_j * sum(q8)_j
+    absmins = (np.abs(sums)[:, None] * mn[None]).sum(-1)
+    dd = dx[:, None, :] * d[None]
+    dm = dx[:, None, :] * dmin[None]
+    terms = ints * dd - mins * dm
+    value = terms.sum(-1)
+    abs_sum = (absints * np.abs(dd) + absmins * np.abs(dm)).sum(-1)
+    return value, abs_sum, nb * 4 * U64 * abs_sum
+
+
+def accumulation_k_q4_k(k):
+    """Roundings on a term's path in K:1478-1558: d_w*d_x, the product with
+    aux32 or sumi, the addition into its lane (up to nb of them), and the
+    final 8-lane sum and the addition to sumf: nb + 12 (spares included)."""
+    return k // QK_K + 12
 
 
 def gamma(kk):
@@ -375,6 +481,20 @@ def synth_q8_0_weight(n, k, sigma, seed):
     blob[:, :, 0] = (dh & 0xFF).astype(np.uint8)
     blob[:, :, 1] = (dh >> 8).astype(np.uint8)
     blob[:, :, 2:] = codes.astype(np.int8).view(np.uint8)
+    return blob.tobytes()
+
+
+def synth_q4_k_weight(n, k, seed):
+    """A Q4_K weight blob built directly in the format: random nibbles and
+    6-bit scales and mins, d and dmin f16 of |N(0, 0.02)| / 63 and / 630."""
+    rng = np.random.default_rng(seed)
+    nb = k // QK_K
+    blob = np.empty((n, nb, Q4_K_BYTES), dtype=np.uint8)
+    d = (np.abs(rng.standard_normal((n, nb))) * 0.02 / 63).astype(np.float32)
+    dmin = (np.abs(rng.standard_normal((n, nb))) * 0.002 / 63).astype(np.float32)
+    blob[..., 0:2] = f16_from_f32(d).view(np.uint8).reshape(n, nb, 2)
+    blob[..., 2:4] = f16_from_f32(dmin).view(np.uint8).reshape(n, nb, 2)
+    blob[..., 4:] = rng.integers(0, 256, size=(n, nb, Q4_K_BYTES - 4), dtype=np.uint8)
     return blob.tobytes()
 
 

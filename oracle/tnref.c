@@ -295,6 +295,318 @@ int tnref_q8_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uin
 }
 
 /* ------------------------------------------------------------------------ */
+/* Q4_K weights with Q8_K activations                                        */
+/* ------------------------------------------------------------------------ */
+/* Layouts (K:153-190): Q4_K super-block of 256 = f16 d, f16 dmin, 12 bytes of
+ * 6-bit scales and mins, 128 nibble bytes (144 bytes); Q8_K = f32 d, 256 int8
+ * codes, 16 int16 sums of 16 codes (292 bytes). */
+#define QKK 256
+
+/* get_scale_min_k4, utils.rs:50-60. */
+static void scale_min_k4(int j, const uint8_t* q, int* sc, int* m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0x0f) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* BlockQ4K::to_float, K:1722-1746: y = d*sc * nib - dmin*m per 32-element
+ * sub-block; sub-blocks 2c and 2c+1 are the low and high nibbles of bytes
+ * 32c..32c+31. */
+void tnref_q4_k_dequantize(const uint8_t* blob, int64_t n, float* y) {
+    for (int64_t b = 0; b < n / QKK; b++) {
+        const uint8_t* in = blob + b * 144;
+        const float d = tnref_f16_to_f32((uint16_t)(in[0] | (in[1] << 8)));
+        const float dmin = tnref_f16_to_f32((uint16_t)(in[2] | (in[3] << 8)));
+        const uint8_t* scales = in + 4;
+        const uint8_t* qs = in + 16;
+        float* out = y + b * QKK;
+        for (int c = 0; c < 4; c++) {
+            int sc, m;
+            scale_min_k4(2 * c, scales, &sc, &m);
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+            scale_min_k4(2 * c + 1, scales, &sc, &m);
+            const float d2 = d * (float)sc, m2 = dmin * (float)m;
+            for (int l = 0; l < 32; l++) out[64 * c + l] = d1 * (float)(qs[32 * c + l] & 0x0f) - m1;
+            for (int l = 0; l < 32; l++) out[64 * c + 32 + l] = d2 * (float)(qs[32 * c + l] >> 4) - m2;
+        }
+    }
+}
+
+/* BlockQ8K::from_float, K:2375-2413 (the non-NEON path): the first element of
+ * the largest |x| sets iscale = -127/max; q = round-half-away(iscale*x)
+ * clamped to [-128, 127] (NaN -> 0); d = 1/iscale in f32. */
+void tnref_q8_k_quantize(const float* x, int64_t n, uint8_t* blob) {
+    for (int64_t b = 0; b < n / QKK; b++) {
+        const float* xs = x + b * QKK;
+        uint8_t* out = blob + b * 292;
+        float mx = 0.0f, amax = 0.0f;
+        for (int j = 0; j < QKK; j++) {
+            if (amax < fabsf(xs[j])) { amax = fabsf(xs[j]); mx = xs[j]; }
+        }
+        int8_t q[QKK];
+        float d = 0.0f;
+        if (amax == 0.0f) {
+            memset(q, 0, sizeof q);
+        } else {
+            const float iscale = -127.0f / mx;
+            for (int j = 0; j < QKK; j++) {
+                float v = roundf(iscale * xs[j]);
+                q[j] = (v != v) ? 0 : (v < -128.0f ? -128 : (v > 127.0f ? 127 : (int8_t)v));
+            }
+            d = 1.0f / iscale;
+        }
+        memcpy(out, &d, 4);
+        memcpy(out + 4, q, QKK);
+        for (int j = 0; j < QKK / 16; j++) {
+            int s = 0;
+            for (int i = 0; i < 16; i++) s += q[16 * j + i];
+            int16_t s16 = (int16_t)(amax == 0.0f ? 0 : s);
+            memcpy(out + 4 + QKK + 2 * j, &s16, 2);
+        }
+    }
+}
+
+/* BlockQ4K::vec_dot_unopt, K:1478-1558: per super-block, 8 exact i32 lane
+ * sums aux32[l] = sum_j sc_j * sum_g q8[32j+8g+l] * nib[32j+8g+l], and
+ * sumi = sum_j bsums[j] * m_{j/2}; then, in f32, sums[l] += (d_w*d_x) *
+ * aux32[l] and sumf -= (dmin_w*d_x) * sumi; the result is
+ * sumf + (((sums[0] + sums[1]) + ...) + sums[7]). */
+float tnref_vec_dot_q4_k_q8_k(int64_t k, const uint8_t* w, const uint8_t* xq) {
+    float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < k / QKK; b++) {
+        const uint8_t* wb = w + b * 144;
+        const uint8_t* xb = xq + b * 292;
+        float yd;
+        memcpy(&yd, xb, 4);
+        const int8_t* q8 = (const int8_t*)(xb + 4);
+        int32_t aux32[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int32_t sumi = 0;
+        for (int j = 0; j < 8; j++) {
+            int sc, m;
+            scale_min_k4(j, wb + 4, &sc, &m);
+            for (int h = 0; h < 2; h++) {
+                int16_t bs;
+                memcpy(&bs, xb + 4 + QKK + 2 * (2 * j + h), 2);
+                sumi += (int32_t)bs * m;
+            }
+            const uint8_t* qb = wb + 16 + 32 * (j / 2);
+            for (int g = 0; g < 4; g++)
+                for (int l = 0; l < 8; l++) {
+                    const int e = 8 * g + l;
+                    const int nib = (j & 1) ? (qb[e] >> 4) : (qb[e] & 0x0f);
+                    aux32[l] += sc * (int32_t)(int16_t)(q8[32 * j + e] * nib);
+                }
+        }
+        const float d = tnref_f16_to_f32((uint16_t)(wb[0] | (wb[1] << 8))) * yd;
+        for (int l = 0; l < 8; l++) sums[l] = sums[l] + d * (float)aux32[l];
+        const float dmin = tnref_f16_to_f32((uint16_t)(wb[2] | (wb[3] << 8))) * yd;
+        sumf = sumf - dmin * (float)sumi;
+    }
+    float tot = 0.0f;
+    for (int l = 0; l < 8; l++) tot = tot + sums[l];
+    return sumf + tot;
+}
+
+/* llama.cpp's nearest_int (utils.rs:292-295): the 1.5*2^23 bit trick,
+ * round to nearest, ties to even. */
+static inline int nearest_int_even(float f) {
+    const float v = f + 12582912.0f;
+    return (int)(f32_bits(v) & 0x007fffff) - 0x00400000;
+}
+
+/* make_qkx2_quants, utils.rs:308-397, with rmin, rdelta, nstep, use_mad =
+ * -1.0, 0.1, 20, false as BlockQ4K::from_float calls it. Every f32 operation
+ * is separate and in the Rust order; `min` is overwritten by each better
+ * candidate and used by the later steps; `l` keeps the best candidate's
+ * levels. Returns the scale, *the_min = -min. */
+static float make_qkx2(int nmax, const float* x, const float* w, uint8_t* l, float* the_min) {
+    const int n = 32;
+    const float rmin = -1.0f, rdelta = 0.1f;
+    const int nstep = 20;
+    float mn = x[0], mxv = x[0];
+    float sum_w = w[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < n; i++) {
+        if (x[i] < mn) mn = x[i];
+        if (x[i] > mxv) mxv = x[i];
+        sum_w = sum_w + w[i];
+        sum_x = sum_x + w[i] * x[i];
+    }
+    if (mn > 0.0f) mn = 0.0f;
+    if (mxv == mn) {
+        memset(l, 0, (size_t)n);
+        *the_min = -mn;
+        return 0.0f;
+    }
+    float iscale = (float)nmax / (mxv - mn);
+    float scale = 1.0f / iscale;
+    float best = 0.0f;
+    for (int i = 0; i < n; i++) {
+        int li = nearest_int_even(iscale * (x[i] - mn));
+        li = li < 0 ? 0 : (li > nmax ? nmax : li);
+        l[i] = (uint8_t)li;
+        float diff = scale * (float)l[i] + mn - x[i];
+        diff = diff * diff;
+        best = best + w[i] * diff;
+    }
+    uint8_t laux[32];
+    for (int is = 0; is <= nstep; is++) {
+        iscale = (rmin + rdelta * (float)is + (float)nmax) / (mxv - mn);
+        float sum_l = 0.0f, sum_l2 = 0.0f, sum_xl = 0.0f;
+        for (int i = 0; i < n; i++) {
+            int li = nearest_int_even(iscale * (x[i] - mn));
+            li = li < 0 ? 0 : (li > nmax ? nmax : li);
+            laux[i] = (uint8_t)li;
+            const float lf = (float)li;
+            sum_l = sum_l + w[i] * lf;
+            sum_l2 = sum_l2 + w[i] * lf * lf;
+            sum_xl = sum_xl + w[i] * lf * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0.0f) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0.0f) {
+                this_min = 0.0f;
+                this_scale = sum_xl / sum_l2;
+            }
+            float cur = 0.0f;
+            for (int i = 0; i < n; i++) {
+                float diff = this_scale * (float)laux[i] + this_min - x[i];
+                diff = diff * diff;
+                cur = cur + w[i] * diff;
+            }
+            if (cur < best) {
+                memcpy(l, laux, (size_t)n);
+                best = cur;
+                scale = this_scale;
+                mn = this_min;
+            }
+        }
+    }
+    *the_min = -mn;
+    return scale;
+}
+
+/* BlockQ4K::from_float, K:1570-1654 (llama.cpp's quantize_row_q4_K_ref):
+ * weights av_x + |x| with av_x = sqrt(sum(x^2)/32) per sub-block, the
+ * make_qkx2 search per sub-block, 6-bit scales and mins as
+ * min(63, (uint8_t)nearest_int(63/max * v)), then the final levels
+ * nearest_int((x + dm)/d) clamped to [0, 15] for sub-blocks whose d is not
+ * zero (the others keep the search's levels). */
+void tnref_q4_k_quantize(const float* x, int64_t n, uint8_t* blob) {
+    for (int64_t b = 0; b < n / QKK; b++) {
+        const float* xs = x + b * QKK;
+        uint8_t* out = blob + b * 144;
+        uint8_t L[QKK];
+        float scales[8], mins[8];
+        float max_scale = 0.0f, max_min = 0.0f;
+        for (int j = 0; j < 8; j++) {
+            const float* xj = xs + 32 * j;
+            float sum_x2 = 0.0f;
+            for (int i = 0; i < 32; i++) sum_x2 = sum_x2 + xj[i] * xj[i];
+            const float av_x = sqrtf(sum_x2 / 32.0f);
+            float wts[32];
+            for (int i = 0; i < 32; i++) wts[i] = av_x + fabsf(xj[i]);
+            scales[j] = make_qkx2(15, xj, wts, L + 32 * j, &mins[j]);
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
+        }
+        const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+        const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+        uint8_t sc[12];
+        memset(sc, 0, sizeof sc);
+        for (int j = 0; j < 8; j++) {
+            uint8_t ls = (uint8_t)nearest_int_even(inv_scale * scales[j]);
+            uint8_t lm = (uint8_t)nearest_int_even(inv_min * mins[j]);
+            if (ls > 63) ls = 63;
+            if (lm > 63) lm = 63;
+            if (j < 4) {
+                sc[j] = ls;
+                sc[j + 4] = lm;
+            } else {
+                sc[j + 4] = (uint8_t)((ls & 0x0f) | ((lm & 0x0f) << 4));
+                sc[j - 4] |= (uint8_t)((ls >> 4) << 6);
+                sc[j] |= (uint8_t)((lm >> 4) << 6);
+            }
+        }
+        const uint16_t dh = tnref_f16_from_f32(max_scale / 63.0f);
+        const uint16_t mh = tnref_f16_from_f32(max_min / 63.0f);
+        for (int j = 0; j < 8; j++) {
+            int s6, m6;
+            scale_min_k4(j, sc, &s6, &m6);
+            const float d = tnref_f16_to_f32(dh) * (float)s6;
+            if (d == 0.0f) continue;
+            const float dm = tnref_f16_to_f32(mh) * (float)m6;
+            for (int i = 0; i < 32; i++) {
+                int lv = nearest_int_even((xs[32 * j + i] + dm) / d);
+                L[32 * j + i] = (uint8_t)(lv < 0 ? 0 : (lv > 15 ? 15 : lv));
+            }
+        }
+        out[0] = (uint8_t)(dh & 0xff);
+        out[1] = (uint8_t)(dh >> 8);
+        out[2] = (uint8_t)(mh & 0xff);
+        out[3] = (uint8_t)(mh >> 8);
+        memcpy(out + 4, sc, 12);
+        for (int c = 0; c < 4; c++)
+            for (int i = 0; i < 32; i++)
+                out[16 + 32 * c + i] = (uint8_t)(L[64 * c + i] | (L[64 * c + 32 + i] << 4));
+    }
+}
+
+/* The Q4_K matmul: activation rows to Q8_K (its VecDotType, K:1445), then
+ * the vec_dot above per output, the driver of K:2430-2582. */
+typedef struct {
+    int64_t m, k, n, c0, c1;
+    const uint8_t* xq;
+    const uint8_t* w;
+    float* y;
+} lin_k_job;
+
+static void* lin_k_worker(void* arg) {
+    lin_k_job* j = (lin_k_job*)arg;
+    const int64_t nb = j->k / QKK;
+    for (int64_t c = j->c0; c < j->c1; c++)
+        for (int64_t r = 0; r < j->m; r++)
+            j->y[r * j->n + c] = tnref_vec_dot_q4_k_q8_k(j->k, j->w + c * nb * 144, j->xq + r * nb * 292);
+    return NULL;
+}
+
+int tnref_q4_k_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w, const float* bias,
+                      float* y, int threads) {
+    if (m < 0 || n < 0 || k <= 0 || k % QKK) return -1;
+    const int64_t nb = k / QKK;
+    uint8_t* xq = (uint8_t*)malloc((size_t)(m * nb * 292 + 1));
+    if (!xq) return -1;
+    for (int64_t r = 0; r < m; r++) tnref_q8_k_quantize(x + r * k, k, xq + r * nb * 292);
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    int64_t per = (n + threads - 1) / threads;
+    pthread_t tid[256];
+    int live[256];
+    lin_k_job jobs[256];
+    for (int t = 0; t < threads; t++) {
+        int64_t c0 = t * per, c1 = (t + 1) * per;
+        if (c0 > n) c0 = n;
+        if (c1 > n) c1 = n;
+        jobs[t] = (lin_k_job){m, k, n, c0, c1, xq, w, y};
+        live[t] = threads > 1 && pthread_create(&tid[t], NULL, lin_k_worker, &jobs[t]) == 0;
+        if (!live[t]) lin_k_worker(&jobs[t]);
+    }
+    for (int t = 0; t < threads; t++) if (live[t]) pthread_join(tid[t], NULL);
+    free(xq);
+    if (bias)
+        for (int64_t r = 0; r < m; r++)
+            for (int64_t c = 0; c < n; c++) y[r * n + c] = y[r * n + c] + bias[c];
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* SDPA default path                                                         */
 /* ------------------------------------------------------------------------ */
 

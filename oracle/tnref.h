@@ -50,6 +50,14 @@ float tnref_vec_dot_q8_0_q8_0(int64_t k, const uint8_t* w_row, const uint8_t* xq
 int tnref_q8_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w_blob,
                       const float* bias, float* y, int threads);
 
+/* ---- Q4_K weights (144-byte super-blocks of 256) with Q8_K activations (292 bytes) ---- */
+void tnref_q4_k_quantize(const float* x, int64_t n, uint8_t* blob);   /* K:1570-1654 */
+void tnref_q4_k_dequantize(const uint8_t* blob, int64_t n, float* y); /* K:1722-1746 */
+void tnref_q8_k_quantize(const float* x, int64_t n, uint8_t* blob);   /* K:2375-2413 */
+float tnref_vec_dot_q4_k_q8_k(int64_t k, const uint8_t* w_row, const uint8_t* xq_row); /* K:1478-1558 */
+int tnref_q4_k_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w_blob,
+                      const float* bias, float* y, int threads);
+
 /* ---- SDPA, the default (flat) path: A:10330-10423 ----
  * q [B,Hq,L,D], k/v [B,Hkv,S,D] row-major; mask nullable, [B,Hq,L,S] row-major
  * in the accumulate type; out [B,Hq,L,D]; lse nullable [B,Hq,L]. GQA: query

@@ -68,6 +68,13 @@ def test_linear_refusals_use_the_reference_wording(L):
     for fn in (L.tn_q8_0_quantize, L.tn_q8_0_from_blob):
         assert fn(None, None, 4, 48, None, None) == _lib.TN_ENOTIMPL
         assert "q8_0 stores 32 elements per block" in _lib.last_error()
+    # q4_k: 256-element super-blocks
+    assert L.tn_q4_k_quantize(None, None, 4, 512 + 32, None) == _lib.TN_ENOTIMPL
+    assert "q4_k stores 256 elements per block, so it must have their last dim divisible by block size -- got 544" \
+        in _lib.last_error()
+    st = L.tn_q4_k_linear(None, None, _lib.TN_F32, 2, 288, None, 8, None, None, _lib.TN_F32)
+    assert st == _lib.TN_EINVAL and "cannot be multiplied ([2, 288]" in _lib.last_error()
+    assert L.tn_q4_k_from_blob(None, None, 4, 256, None) == _lib.TN_EVALUE
     assert L.tn_q8_0_dequantize(None, None, None, 4, 96, None) == _lib.TN_EVALUE  # null planes
     assert "null pointer" in _lib.last_error()
     with pytest.raises(NotImplementedError):
@@ -124,9 +131,9 @@ def test_python_mirror_refuses_host_operands_instead_of_falling_back():
         tn._quantized_from_blob(b"\0" * 17, (1, 32), "q4_0")
     with pytest.raises(ValueError, match="q8_0 stores 32 elements in 34 bytes.*needs 68 bytes; got 36"):
         tn._quantized_from_blob(b"\0" * 36, (1, 64), "q8_0")
-    with pytest.raises(NotImplementedError, match="'q4_k' is not implemented on the hip device"):
-        tn._quantize(x, "q4_k")
-    assert tn._quantized_formats() == ["q4_0", "q8_0"]
+    with pytest.raises(NotImplementedError, match="'q5_k' is not implemented on the hip device"):
+        tn._quantize(x, "q5_k")
+    assert tn._quantized_formats() == ["q4_0", "q8_0", "q4_k"]
     q = tn._quantized_from_blob(b"\0" * 36, (1, 64), "q4_0")  # stays on the host: no compute
     assert tn._quantized_blob(q) == b"\0" * 36 and tn._quantized_nbytes(q) == 36
     with pytest.raises(NotImplementedError, match="hip device"):

@@ -30,6 +30,8 @@ def _rand_blocks(gtype, nblocks, seed):
     size = G.GGML_TYPES[gtype][2]
     raw = np.random.default_rng(seed).integers(0, 256, size=(nblocks, size), dtype=np.uint8)
     raw[:, 1] &= 0x3B  # exponent below all-ones: finite, and |d| < 1
+    if gtype == 12:
+        raw[:, 3] &= 0x3B  # q4_k's dmin too
     return raw.tobytes()
 
 
@@ -98,7 +100,7 @@ def test_inconsistent_descriptors_refuse_by_name(tmp_path):
 
 
 def test_every_type_not_loaded_here_refuses_by_name(tmp_path):
-    loaded = {0, 1, 2, 8, 30}
+    loaded = {0, 1, 2, 8, 12, 30}
     for gtype, (name, blk, size, kind, why) in G.GGML_TYPES.items():
         assert (gtype in loaded) == (kind != "refused"), name
         if gtype in loaded:
@@ -118,7 +120,7 @@ def test_every_type_not_loaded_here_refuses_by_name(tmp_path):
     with G.GGUFFile(_path(tmp_path, "u.gguf", gguf_bytes([], [("t", 99, [4], b"")]))) as f:
         with pytest.raises(G.UnsupportedGGUF, match="type id 99"):
             f.raw("t")
-    assert "activation-side" in str(G.refusal(9)) and "only q4_0 and q8_0" in str(G.refusal(12))
+    assert "activation-side" in str(G.refusal(9)) and "only q4_0, q8_0 and q4_k" in str(G.refusal(13))
 
 
 def test_the_type_table_is_ggmls():
@@ -136,10 +138,11 @@ def test_the_type_table_is_ggmls():
 
 
 def test_kept_blocks_stay_the_files_bytes_on_the_host(tmp_path):
-    w4, w8 = _rand_blocks(2, 6, 4), _rand_blocks(8, 6, 5)
-    path = write(str(tmp_path / "k.gguf"), [], [("a", 2, [64, 3], w4), ("b", 8, [96, 2], w8)])
+    w4, w8, wk = _rand_blocks(2, 6, 4), _rand_blocks(8, 6, 5), _rand_blocks(12, 4, 6)
+    path = write(str(tmp_path / "k.gguf"), [], [("a", 2, [64, 3], w4), ("b", 8, [96, 2], w8),
+                                                 ("c", 12, [512, 2], wk)])
     with G.GGUFFile(path) as f:
-        for name, raw, fmt in (("a", w4, "q4_0"), ("b", w8, "q8_0")):
+        for name, raw, fmt in (("a", w4, "q4_0"), ("b", w8, "q8_0"), ("c", wk, "q4_k")):
             q = G.load_tensor(f, name, keep_blocks=True, device="cpu")
             assert q.format == fmt and q.shape == f.info(name).shape
             import torchnative_amd as tn
@@ -197,13 +200,14 @@ def test_blocks_reach_the_device_unchanged_and_dequantise_as_llama_cpp(tn, tmp_p
         want[f"{fmt}.{name}"] = (bytes.fromhex(c["blob"]), bytes.fromhex(c["dequant_f32"]))
     tensors.append(("rand4", 2, [256, 40], _rand_blocks(2, 320, 7)))
     tensors.append(("rand8", 8, [128, 33], _rand_blocks(8, 132, 8)))
+    tensors.append(("rand4k", 12, [512, 6], _rand_blocks(12, 12, 9)))
     path = write(str(tmp_path / "g.gguf"), [], tensors)
     with G.GGUFFile(path) as f:
         for name, gtype, _, raw in tensors:
             q = G.load_tensor(f, name, keep_blocks=True)
             assert q.device == "hip" and tn._quantized_blob(q) == raw, name
             dq = G.load_tensor(f, name).numpy().reshape(-1).tobytes()
-            deq = O.q4_0_dequantize if gtype == 2 else O.q8_0_dequantize
+            deq = {2: O.q4_0_dequantize, 8: O.q8_0_dequantize, 12: O.q4_k_dequantize}[gtype]
             assert dq == deq(raw, f.info(name).n_elements).tobytes(), name
             if name in want:
                 assert dq == want[name][1], name
@@ -225,14 +229,15 @@ def test_dense_types_read_back_exactly_in_their_own_dtype(tn, tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("gtype", [2, 8])
+@pytest.mark.parametrize("gtype", [2, 8, 12])
 def test_a_gguf_linear_holds_the_file_bytes_and_multiplies_as_the_oracle(tn, tmp_path, gtype):
     n, k = 96, 512
-    raw = (O.synth_q4_0_weight if gtype == 2 else O.synth_q8_0_weight)(n, k, 0.02, 10)
+    raw = {2: lambda: O.synth_q4_0_weight(n, k, 0.02, 10), 8: lambda: O.synth_q8_0_weight(n, k, 0.02, 10),
+           12: lambda: O.synth_q4_k_weight(n, k, 10)}[gtype]()
     bias = np.random.default_rng(11).standard_normal(n).astype(np.float32)
     path = write(str(tmp_path / "l.gguf"), [], [("blk.0.ffn_down.weight", gtype, [k, n], raw)])
     x = np.random.default_rng(12).standard_normal((3, k)).astype(np.float32)
-    lin_fn = O.q4_0_linear if gtype == 2 else O.q8_0_linear
+    lin_fn = {2: O.q4_0_linear, 8: O.q8_0_linear, 12: O.q4_k_linear}[gtype]
     with G.GGUFFile(path) as f:
         lin = G.quantized_linear(f, "blk.0.ffn_down.weight", bias=tn.tensor(bias, device="hip"))
     assert (lin.out_features, lin.in_features) == (n, k)

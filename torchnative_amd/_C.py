@@ -26,6 +26,7 @@ Q4_0_TYPE_SIZE = 18
 _LAYOUT = {
     "q4_0": (32, 18, 16, "tn_q4_0"),
     "q8_0": (32, 34, 32, "tn_q8_0"),
+    "q4_k": (256, 144, 144, "tn_q4_k"),  # one plane: the super-blocks, nibbles repacked (include/tnhip.h)
 }
 _FORMATS = tuple(_LAYOUT)
 _REFERENCE_FORMATS = ("f32", "f16", "bf16", "q4_0", "q4_1", "q5_0", "q5_1", "q8_0", "q8_1",
@@ -64,6 +65,10 @@ class QTensor:
     def _fn(self, op):
         return getattr(lib(), f"{_LAYOUT[self.format][3]}_{op}")
 
+    def _planes(self):
+        """The device plane pointers as the format's C functions take them."""
+        return (self._qs.data_ptr(),) if self._d is None else (self._qs.data_ptr(), self._d.data_ptr())
+
     def __repr__(self):
         return f"QTensor(shape={self.shape}, format={self.format}, device={self.device})"
 
@@ -84,10 +89,12 @@ def _shape2(shape, fmt="q4_0"):
 
 
 def _planes(n, k, fmt):
-    """Empty device planes for an [n, k] weight: (codes, f16 scales as bytes)."""
+    """Empty device planes for an [n, k] weight: (codes, f16 scales as bytes),
+    or (super-blocks, None) for q4_k."""
     blk, _, code_bytes, _ = _LAYOUT[fmt]
     nb = n * k // blk
-    return Tensor((nb * code_bytes,), "uint8", "hip"), Tensor((nb * 2,), "uint8", "hip")
+    codes = Tensor((nb * code_bytes,), "uint8", "hip")
+    return codes, (None if fmt == "q4_k" else Tensor((nb * 2,), "uint8", "hip"))
 
 
 def _quantized_formats():
@@ -127,7 +134,7 @@ def _quantize(t: Tensor, fmt: str) -> QTensor:
     n, k = _shape2(t.shape, fmt)
     qs, d = _planes(n, k, fmt)
     q = QTensor((n, k), fmt, "hip", qs=qs, d=d)
-    check(q._fn("quantize")(current_stream(), t.data_ptr(), n, k, qs.data_ptr(), d.data_ptr()))
+    check(q._fn("quantize")(current_stream(), t.data_ptr(), n, k, *q._planes()))
     return q
 
 
@@ -161,7 +168,7 @@ def _quantized_to(t: QTensor, device) -> QTensor:
         blob = Tensor.from_numpy(np.frombuffer(t._blob, dtype=np.uint8), device="hip")
         qs, d = _planes(n, k, t.format)
         q = QTensor(t.shape, t.format, "hip", qs=qs, d=d)
-        check(q._fn("from_blob")(current_stream(), blob.data_ptr(), n, k, qs.data_ptr(), d.data_ptr()))
+        check(q._fn("from_blob")(current_stream(), blob.data_ptr(), n, k, *q._planes()))
         return q
     return QTensor(t.shape, t.format, "cpu", blob=_quantized_blob(t))
 
@@ -172,7 +179,7 @@ def _quantized_blob(t: QTensor) -> bytes:
         return t._blob
     n, k = t.shape
     blob = Tensor((t.nblocks * _LAYOUT[t.format][1],), "uint8", "hip")
-    check(t._fn("to_blob")(current_stream(), t._qs.data_ptr(), t._d.data_ptr(), n, k, blob.data_ptr()))
+    check(t._fn("to_blob")(current_stream(), *t._planes(), n, k, blob.data_ptr()))
     return blob.bits().tobytes()
 
 
@@ -191,7 +198,7 @@ def _dequantize(t: QTensor) -> Tensor:
     _require_hip(op, t)
     n, k = t.shape
     out = Tensor((n, k), "float32", "hip")
-    check(t._fn("dequantize")(current_stream(), t._qs.data_ptr(), t._d.data_ptr(), n, k, out.data_ptr()))
+    check(t._fn("dequantize")(current_stream(), *t._planes(), n, k, out.data_ptr()))
     return out
 
 
@@ -231,7 +238,7 @@ def _quantized_linear(input: Tensor, weight: QTensor, bias: Tensor | None = None
     odt = out_dtype or "float32"
     out = Tensor(input.shape[:-1] + (out_features,), odt, "hip")
     check(weight._fn("linear")(current_stream(), input.data_ptr(), _dt(input.dtype), m, in_features,
-                               weight._qs.data_ptr(), weight._d.data_ptr(), out_features,
+                               *weight._planes(), out_features,
                                bias.data_ptr() if bias is not None else None, out.data_ptr(), _dt(odt)))
     return out
 

@@ -12,7 +12,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libtnhip.so")
-SOURCES = ["runtime.hip", "qlinear.hip", "sdpa.hip", "decode.hip"]
+SOURCES = ["runtime.hip", "qlinear.hip", "qk.hip", "sdpa.hip", "decode.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: the q4 recurrence and the SDPA softmax are written with the

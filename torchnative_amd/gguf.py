@@ -7,7 +7,7 @@ the GGML type table and its refusals (reader.py:111-166), `load_tensor`
 reference, block tensors are never decoded or re-encoded on the way in: the
 file's GGML blocks go byte for byte to `_quantized_from_blob`, which on this
 backend splits them into the device's code and scale planes
-(tn_q4_0_from_blob / tn_q8_0_from_blob), so `_quantized_blob` of a loaded
+(tn_q4_0_from_blob / tn_q8_0_from_blob / tn_q4_k_from_blob), so `_quantized_blob` of a loaded
 weight returns the file's bytes.
 
 The container is read with `mmap` and `struct` only. Layout (GGUF v2/v3,
@@ -52,8 +52,8 @@ _WHY = {
                   "model to q8_0 or q4_0 for this backend."),
     "not_wired": "is a plain numeric type no checkpoint uses for weights; it is not wired and not guessed at.",
     "removed": "is a repacked layout ggml dropped from the file format; a file carrying it is not read.",
-    "not_on_hip": ("is a block format the reference holds, but the hip device implements only q4_0 and q8_0 "
-                   "blocks; re-quantise to one of them."),
+    "not_on_hip": ("is a block format the reference holds, but the hip device implements only q4_0, q8_0 and "
+                   "q4_k blocks; re-quantise to one of them."),
 }
 
 # GGML type id -> (name, elements per block, bytes per block, kind, dtype / format / refusal key).
@@ -69,7 +69,7 @@ GGML_TYPES = {
     7: ("Q5_1", 32, 24, "refused", "not_on_hip"),
     10: ("Q2_K", 256, 84, "refused", "not_on_hip"),
     11: ("Q3_K", 256, 110, "refused", "not_on_hip"),
-    12: ("Q4_K", 256, 144, "refused", "not_on_hip"),
+    12: ("Q4_K", 256, 144, "block", "q4_k"),
     13: ("Q5_K", 256, 176, "refused", "not_on_hip"),
     14: ("Q6_K", 256, 210, "refused", "not_on_hip"),
     9: ("Q8_1", 32, 36, "refused", "activation"),
