@@ -43,8 +43,8 @@ BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 INT8_PEAK_TOPS = 5000.0
 
-# weight format -> (GGML bytes per block, device code bytes per block)
-_BLOCK = {"q4_0": (18, 16), "q8_0": (34, 32)}
+# weight format -> (GGML bytes per block, device code bytes per block, elements per block)
+_BLOCK = {"q4_0": (18, 16, 32), "q8_0": (34, 32, 32), "q4_k": (144, 144, 256)}
 
 
 def _synth_q4_0_blob(n, k, sigma, seed):
@@ -72,8 +72,21 @@ def _synth_q8_0_blob(n, k, sigma, seed):
     return blob.reshape(-1)
 
 
+def _synth_q4_k_blob(n, k, sigma, seed):
+    """Q4_K blob: random nibbles and 6-bit scales/mins, d = f16(|N(0, sigma)|/63),
+    dmin = f16(|N(0, sigma/10)|/63)."""
+    rng = np.random.default_rng(seed)
+    nb = k // 256
+    blob = rng.integers(0, 256, size=(n, nb, 144), dtype=np.uint8)
+    d = (np.abs(rng.standard_normal((n, nb))) * sigma / 63).astype(np.float32).astype(np.float16)
+    dm = (np.abs(rng.standard_normal((n, nb))) * sigma / 630).astype(np.float32).astype(np.float16)
+    blob[:, :, 0:2] = d.view(np.uint8).reshape(n, nb, 2)
+    blob[:, :, 2:4] = dm.view(np.uint8).reshape(n, nb, 2)
+    return blob.reshape(-1)
+
+
 def _synth_blob(fmt, n, k, sigma, seed):
-    return (_synth_q8_0_blob if fmt == "q8_0" else _synth_q4_0_blob)(n, k, sigma, seed)
+    return {"q8_0": _synth_q8_0_blob, "q4_0": _synth_q4_0_blob, "q4_k": _synth_q4_k_blob}[fmt](n, k, sigma, seed)
 
 
 class Timer:
@@ -124,34 +137,36 @@ def bench_sdpa(tn, L, dtype, steps, warmup, B=1, Hq=9, Hkv=3, S=2048, D=64, seed
 
 
 def bench_gemv(tn, L, steps, warmup, copies=1024, fmt="q4_0"):
-    n, k = 1536, 576
+    # q4_k needs K % 256 == 0: its leg uses K = 768 (C1's 576 rounded up)
+    n, k = 1536, (768 if fmt == "q4_k" else 576)
     lib = L.lib()
-    blob_b, code_b = _BLOCK[fmt]
+    blob_b, code_b, blk = _BLOCK[fmt]
     from_blob, linear = getattr(lib, f"tn_{fmt}_from_blob"), getattr(lib, f"tn_{fmt}_linear")
+    planes = (lambda q, d: (q,)) if fmt == "q4_k" else (lambda q, d: (q, d))
     rng = np.random.default_rng(1)
     x = tn.tensor(rng.standard_normal((1, k)).astype(np.float32), device="hip")
     # 1,024 distinct [1536, 576] weights, contiguous: one launch streams all of them
-    qs = tn.empty((copies * n * k // 32 * code_b,), "uint8", "hip")
-    dd = tn.empty((copies * n * k // 32 * 2,), "uint8", "hip")
+    qs = tn.empty((copies * n * k // blk * code_b,), "uint8", "hip")
+    dd = tn.empty((copies * n * k // blk * 2,), "uint8", "hip")
     chunk = 64
     for c0 in range(0, copies, chunk):
         blob = _synth_blob(fmt, chunk * n, k, 0.02, 1000 + c0)
         bt = tn.tensor(blob, device="hip")
-        off_q = c0 * n * k // 32 * code_b
-        off_d = c0 * n * k // 32 * 2
-        L.check(from_blob(None, bt.data_ptr(), chunk * n, k, qs.data_ptr() + off_q, dd.data_ptr() + off_d))
+        off_q = c0 * n * k // blk * code_b
+        off_d = c0 * n * k // blk * 2
+        L.check(from_blob(None, bt.data_ptr(), chunk * n, k, *planes(qs.data_ptr() + off_q, dd.data_ptr() + off_d)))
     y = tn.empty((1, copies * n), "float32", "hip")
 
     def step_all():
-        st = linear(None, x.data_ptr(), L.TN_F32, 1, k, qs.data_ptr(), dd.data_ptr(), copies * n, None,
-                                y.data_ptr(), L.TN_F32)
+        st = linear(None, x.data_ptr(), L.TN_F32, 1, k, *planes(qs.data_ptr(), dd.data_ptr()), copies * n, None,
+                    y.data_ptr(), L.TN_F32)
         if st:
             L.check(st)
 
     # C1 is the first GPU work of a run: a longer warm-up (about 10 ms) lets
     # the clocks settle before the timed region
     ms, kern_ms = Timer(tn).run(step_all, steps, max(warmup, 100))
-    w_bytes = n * (k // 32) * blob_b
+    w_bytes = n * (k // blk) * blob_b
     per_copy = w_bytes + n * 4
     total_bytes = copies * per_copy + k * 4
     ach = total_bytes / (kern_ms * 1e-3) / 1e9
@@ -161,8 +176,9 @@ def bench_gemv(tn, L, steps, warmup, copies=1024, fmt="q4_0"):
     def step_one():
         c = idx[0] % copies
         idx[0] += 1
-        st = linear(None, x.data_ptr(), L.TN_F32, 1, k, qs.data_ptr() + c * n * k // 32 * code_b,
-                                dd.data_ptr() + c * n * k // 16, n, None, y.data_ptr(), L.TN_F32)
+        st = linear(None, x.data_ptr(), L.TN_F32, 1, k,
+                    *planes(qs.data_ptr() + c * n * k // blk * code_b, dd.data_ptr() + c * n * k // blk * 2), n,
+                    None, y.data_ptr(), L.TN_F32)
         if st:
             L.check(st)
 
@@ -185,7 +201,7 @@ def bench_gemm(tn, L, steps, warmup, fmt="q4_0"):
     y = tn.empty((m, n), "bfloat16", "hip")
 
     def step():
-        st = linear(None, x.data_ptr(), L.TN_BF16, m, k, q._qs.data_ptr(), q._d.data_ptr(), n, None,
+        st = linear(None, x.data_ptr(), L.TN_BF16, m, k, *q._planes(), n, None,
                                 y.data_ptr(), L.TN_BF16)
         if st:
             L.check(st)
@@ -193,10 +209,11 @@ def bench_gemm(tn, L, steps, warmup, fmt="q4_0"):
     ms, kern_ms = Timer(tn).run(step, steps, warmup)
     flops = 2.0 * m * k * n
     ach = flops / (kern_ms * 1e-3) / 1e12
-    # the block dots run on bf16 MFMA for q4_0 and on int8 MFMA for q8_0
+    # the block dots run on bf16 MFMA for q4_0 and on int8 MFMA for q8_0; q4_k
+    # is priced against the bf16 peak
     peak, unit = (INT8_PEAK_TOPS, "TOP/s") if fmt == "q8_0" else (BF16_PEAK_TFLOPS, "TFLOP/s")
     return {"ms_per_step": ms, "kernel_ms": kern_ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
-            "bytes": n * (k // 32) * _BLOCK[fmt][0] + m * k * 2 + m * n * 2,
+            "bytes": n * (k // _BLOCK[fmt][2]) * _BLOCK[fmt][0] + m * k * 2 + m * n * 2,
             "roofline": {"bound": "mfma", "achieved": ach, "peak": peak, "unit": unit,
                          "frac": ach / peak, "traffic": None}}
 
@@ -374,7 +391,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c3,c4,c5,q8c1,q8c3)")
+    ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c3,c4,c5,q8c1,q8c3,q4kc1,q4kc3)")
     ap.add_argument("--no-graph", action="store_true",
                     help="c5: time the decode steps as separate launches only (no HIP graph)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -411,6 +428,12 @@ def main():
     if want("q8c3"):
         print("bench: q8_0 GEMM at the c3 shape", file=sys.stderr, flush=True)
         parts["q8_0_gemm_c3_shape"] = bench_gemm(tn, L, args.steps, args.warmup, fmt="q8_0")
+    if want("q4kc1"):
+        print("bench: q4_k GEMV at the c1 shape (K 768)", file=sys.stderr, flush=True)
+        parts["q4_k_gemv_c1_shape"] = bench_gemv(tn, L, args.steps, args.warmup, fmt="q4_k")
+    if want("q4kc3"):
+        print("bench: q4_k prefill at the c3 shape", file=sys.stderr, flush=True)
+        parts["q4_k_gemm_c3_shape"] = bench_gemm(tn, L, args.steps, args.warmup, fmt="q4_k")
     if want("c4"):
         print("bench: c4 decode attention", file=sys.stderr, flush=True)
         parts["c4_decode_attention"] = bench_decode(tn, L, args.steps, args.warmup)
