@@ -112,11 +112,32 @@ def test_scales_across_every_f16_regime_and_activation_extremes(tn):
     x[1, 600] = np.inf
     x[2, :256] *= np.float32(3e37)
     x[3, 256:512] *= np.float32(1e-38)
-    want = O.q4_k_linear(x, blob, n, threads=8)
-    got = tn._quantized_linear(tn.tensor(x, device="hip"), q).numpy()
-    assert np.array_equal(got, want, equal_nan=True)
-    fin = np.isfinite(want)
-    assert got[fin].tobytes() == want[fin].tobytes()
+    x6 = np.concatenate([x, rng.standard_normal((2, k)).astype(np.float32)])
+    want = O.q4_k_linear(x6, blob, n, threads=8)
+    for m in (4, 6):  # the GEMV, then the MFMA GEMM
+        got = tn._quantized_linear(tn.tensor(x6[:m], device="hip"), q).numpy()
+        assert np.array_equal(got, want[:m], equal_nan=True), m
+        fin = np.isfinite(want[:m])
+        assert got[fin].tobytes() == want[:m][fin].tobytes(), m
+
+
+def test_prefill_gemm_at_the_config3_shape(tn):
+    """x bf16 [512, 4096] against W [14336, 4096] q4_k, bf16 out: sampled rows
+    bit for bit against the oracle, and rows of a separate smaller call equal
+    to the same rows of the full call."""
+    rng = np.random.default_rng(3)
+    m, k, n = 512, 4096, 14336
+    xb = tn.tensor(rng.standard_normal((m, k)).astype(np.float32), dtype="bfloat16", device="hip")
+    xw = xb.numpy()
+    blob = O.synth_q4_k_weight(n, k, 33)
+    q = _qweight(tn, blob, n, k)
+    y32 = tn._quantized_linear(xb, q).numpy()
+    rows = [0, 1, 31, 32, 255, 300, 511]
+    assert y32[rows].tobytes() == O.q4_k_linear(xw[rows], blob, n, threads=16).tobytes()
+    ybits = tn._quantized_linear(xb, q, out_dtype="bfloat16").bits()
+    assert np.array_equal(O.bf16_from_f32(y32), ybits)
+    part = tn._quantized_linear(tn.tensor(xw[300:309], device="hip"), q).numpy()
+    assert part.tobytes() == y32[300:309].tobytes()
 
 
 def test_lossless_operands_give_the_exact_integer_matmul(tn):

@@ -485,6 +485,257 @@ __global__ __launch_bounds__(QG_THREADS) void k_gemv_qk(const XT* __restrict__ x
     }
 }
 
+// ---- prefill GEMM on f16 MFMA (m > 4) --------------------------------------------
+//
+// The reference keeps nine f32 accumulators per output (sums[0..7], sumf), so
+// a wave owns a 32x16 output tile (8 outputs per lane, 72 accumulators). A
+// workgroup is four waves side by side: 32 rows x 64 weight columns, the
+// activation rows shared through LDS.
+//
+// Exactness. For residue l the K dimension is the 32 elements 32j + 8g + l
+// (j = 0..7, g = 0..3); with the weight operand sc_j * nib (an integer <= 945,
+// exact in f16) and the activation operand the Q8_K code (exact in f16),
+// one v_mfma_f32_16x16x32_f16 returns aux32[l] exactly (|aux32| < 2^22). The
+// nibbles become f16 through the 0x6400 | nib pattern (1024 + nib) minus
+// 1024, both exact. sumi is one v_mfma_f32_16x16x16_f16 of the 16 code sums
+// (|sum| <= 2048, exact in f16) against m_{j/2}. The f32 steps are then the
+// reference's, in its order.
+//
+// Operand order. MFMA lane group G (lanes 16G..16G+15) holds K slots
+// 8G..8G+7 = sub-blocks j = 2G (slots 0-3) and 2G+1 (slots 4-7), positions
+// g = 0, 2, 1, 3 in that order: the order in which two shifts and masks of a
+// weight dword (chunk G, word l) yield nibble pairs. The prepass writes the
+// activation codes in the same order.
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4q __attribute__((ext_vector_type(4)));
+
+constexpr int QM_ROWS = 32, QM_COLS = 64, QM_THREADS = 256;
+constexpr int QM_AS = 512 + 16;  // LDS row stride (bytes) of the activation codes: conflict-free b128 reads
+constexpr int QM_XCD = 8;
+
+__device__ inline int gslot(int g) { return ((g & 1) << 1) | (g >> 1); }  // g -> slot within a half: 0,2,1,3 -> 0,1,2,3
+
+// Q8_K of every activation row (rows >= M: zero codes, sums and scale), one
+// wave per (row, super-block), into the MFMA operand layout:
+//   xa  f16 [M_pad][nsb][l][G][8]   codes, slot 4h + gslot(g) for sub-block 2G + h
+//   xbs f16 [M_pad][nsb][16]         sums of 16 codes
+//   xd  f32 [nsb][M_pad]             d = 1 / iscale
+template <typename XT>
+__global__ __launch_bounds__(256) void k_q8k_rows(const XT* __restrict__ x, int M, int M_pad, int K, int nsb,
+                                                 uint16_t* __restrict__ xa, uint16_t* __restrict__ xbs,
+                                                 float* __restrict__ xd) {
+    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (blk >= (int64_t)M_pad * nsb) return;
+    const int row = (int)(blk / nsb), sb = (int)(blk - (int64_t)row * nsb);
+    float e[4] = {0.f, 0.f, 0.f, 0.f};
+    if (row < M) {
+        const float4 v4 = load4<XT>(x + (int64_t)row * K + sb * QKK + 4 * lane);
+        e[0] = v4.x; e[1] = v4.y; e[2] = v4.z; e[3] = v4.w;
+    }
+    float am = 0.0f, mv = 0.0f;
+    int idx = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (am < fabsf(e[i])) { am = fabsf(e[i]); mv = e[i]; idx = 4 * lane + i; }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float oa = __shfl_xor(am, off, 64), ov = __shfl_xor(mv, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (oa > am || (oa == am && oi < idx)) { am = oa; mv = ov; idx = oi; }
+    }
+    int q[4] = {0, 0, 0, 0};
+    float d = 0.0f;
+    if (am != 0.0f) {
+        const float iscale = -127.0f / mv;
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[i] = sat_i8k(roundf(iscale * e[i]));
+        d = 1.0f / iscale;
+    }
+    uint16_t* dst = xa + blk * QKK;
+    const int j = lane >> 3, G = j >> 1, h = j & 1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 4 * (lane & 7) + i, g = r >> 3, l = r & 7;
+        dst[(l * 4 + G) * 8 + 4 * h + gslot(g)] = __builtin_bit_cast(uint16_t, (_Float16)(float)q[i]);
+    }
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if ((lane & 3) == 0) xbs[blk * 16 + (lane >> 2)] = __builtin_bit_cast(uint16_t, (_Float16)(float)s);
+    if (lane == 0) xd[(int64_t)sb * M_pad + row] = d;
+}
+
+// byte k (0..11) of the three scale words, by selects (a lane-dependent
+// index into an array would go through scratch memory)
+__device__ inline uint32_t byte_of(uint32_t w0, uint32_t w1, uint32_t w2, int k) {
+    const uint32_t wd = k < 4 ? w0 : (k < 8 ? w1 : w2);
+    return (wd >> (8 * (k & 3))) & 0xffu;
+}
+
+__global__ __launch_bounds__(QM_THREADS, 2) void k_gemm_qk(const uint16_t* __restrict__ xa,
+                                                         const uint16_t* __restrict__ xbs,
+                                                         const float* __restrict__ xd, int M, int M_pad, int nsb,
+                                                         const uint8_t* __restrict__ w, int N,
+                                                         const float* __restrict__ bias, void* __restrict__ y,
+                                                         int y_bf16) {
+    __shared__ __align__(16) uint8_t sA[2][QM_ROWS * QM_AS];
+    __shared__ __align__(16) uint16_t sBS[2][QM_ROWS * 16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lrow = lane & 15, G = lane >> 4;
+
+    const int mt = (int)gridDim.y;
+    const int ntot = (int)(gridDim.x * gridDim.y);
+    const int id = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    int tile = id;
+    if (ntot % QM_XCD == 0) tile = (id % QM_XCD) * (ntot / QM_XCD) + id / QM_XCD;
+    const int m0 = (tile % mt) * QM_ROWS, n0 = (tile / mt) * QM_COLS;
+    const int col = n0 + wave * 16 + lrow;  // this lane's weight column
+
+    float sums[8][2][4], sumf[2][4];
+#pragma unroll
+    for (int l = 0; l < 8; l++)
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sums[l][rt][r] = 0.0f;
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sumf[rt][r] = 0.0f;
+
+    // staging: the 32 activation rows' codes (1024 x 16 B: 4 per thread) and sums (64 x 16 B)
+    // thread tid stages rows tid/32 + 8i (i = 0..3), 16-byte part tid % 32
+    const int arow = tid >> 5, apart = tid & 31;
+    auto ga = [&](int sb, int i) {
+        return *reinterpret_cast<const uint4*>(xa + ((int64_t)(m0 + arow + 8 * i) * nsb + sb) * QKK + apart * 8);
+    };
+    auto sa = [&](int buf, int i, const uint4& v) {
+        *reinterpret_cast<uint4*>(&sA[buf][(arow + 8 * i) * QM_AS + apart * 16]) = v;
+    };
+    auto gbs = [&](int sb) {
+        return *reinterpret_cast<const uint4*>(xbs + ((int64_t)(m0 + (tid >> 1)) * nsb + sb) * 16 + (tid & 1) * 8);
+    };
+    auto sbs = [&](int buf, const uint4& v) {
+        *reinterpret_cast<uint4*>(&sBS[buf][(tid >> 1) * 16 + (tid & 1) * 8]) = v;
+    };
+    // this lane's weight bytes for a super-block: the 16-byte head and chunk G
+    auto load_b = [&](int sb, uint4& hd, uint4& c0, uint4& c1, float4& dx0, float4& dx1) {
+        hd = c0 = c1 = make_uint4(0u, 0u, 0u, 0u);
+        if (col < N) {
+            const uint4* blk = reinterpret_cast<const uint4*>(w + ((int64_t)col * nsb + sb) * QK4K_BYTES);
+            hd = blk[0];
+            c0 = blk[1 + 2 * G];
+            c1 = blk[2 + 2 * G];
+        }
+        dx0 = *reinterpret_cast<const float4*>(xd + (int64_t)sb * M_pad + m0 + 4 * G);
+        dx1 = *reinterpret_cast<const float4*>(xd + (int64_t)sb * M_pad + m0 + 16 + 4 * G);
+    };
+
+    uint4 ra0, ra1, ra2, ra3, rb = make_uint4(0u, 0u, 0u, 0u);
+    uint4 hd, c0, c1, nhd, nc0, nc1;
+    float4 dx0, dx1, ndx0, ndx1;
+    ra0 = ga(0, 0); ra1 = ga(0, 1); ra2 = ga(0, 2); ra3 = ga(0, 3);
+    if (tid < 64) rb = gbs(0);
+    load_b(0, hd, c0, c1, dx0, dx1);
+    sa(0, 0, ra0); sa(0, 1, ra1); sa(0, 2, ra2); sa(0, 3, ra3);
+    if (tid < 64) sbs(0, rb);
+    __syncthreads();
+    const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    for (int sb = 0; sb < nsb; sb++) {
+        const int buf = sb & 1;
+        if (sb + 1 < nsb) {
+            ra0 = ga(sb + 1, 0); ra1 = ga(sb + 1, 1); ra2 = ga(sb + 1, 2); ra3 = ga(sb + 1, 3);
+            if (tid < 64) rb = gbs(sb + 1);
+            load_b(sb + 1, nhd, nc0, nc1, ndx0, ndx1);
+        }
+        // the column's scales and mins for sub-blocks 2G, 2G + 1 (get_scale_min_k4)
+        int scv[2], mnv[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int jj = 2 * G + hh;
+            if (jj < 4) {
+                scv[hh] = (int)(byte_of(hd.y, hd.z, hd.w, jj) & 63);
+                mnv[hh] = (int)(byte_of(hd.y, hd.z, hd.w, jj + 4) & 63);
+            } else {
+                scv[hh] = (int)((byte_of(hd.y, hd.z, hd.w, jj + 4) & 0x0f) | ((byte_of(hd.y, hd.z, hd.w, jj - 4) >> 6) << 4));
+                mnv[hh] = (int)((byte_of(hd.y, hd.z, hd.w, jj + 4) >> 4) | ((byte_of(hd.y, hd.z, hd.w, jj) >> 6) << 4));
+            }
+        }
+        const half2v sc0 = {(_Float16)(float)scv[0], (_Float16)(float)scv[0]};
+        const half2v sc1 = {(_Float16)(float)scv[1], (_Float16)(float)scv[1]};
+        const float dwf = f16_bits_hw((uint16_t)(hd.x & 0xffffu));
+        const float dmwf = f16_bits_hw((uint16_t)(hd.x >> 16));
+        const float dxr[2][4] = {{dx0.x, dx0.y, dx0.z, dx0.w}, {dx1.x, dx1.y, dx1.z, dx1.w}};
+        float dd[2][4];
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) dd[rt][r] = dwf * dxr[rt][r];
+        const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const f32x4q zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const uint32_t dw = cw[l];
+            const half2v lo02 = (__builtin_bit_cast(half2v, (dw & 0x000f000fu) | 0x64006400u) - k1024) * sc0;
+            const half2v lo13 = (__builtin_bit_cast(half2v, ((dw >> 8) & 0x000f000fu) | 0x64006400u) - k1024) * sc0;
+            const half2v hi02 = (__builtin_bit_cast(half2v, ((dw >> 4) & 0x000f000fu) | 0x64006400u) - k1024) * sc1;
+            const half2v hi13 = (__builtin_bit_cast(half2v, ((dw >> 12) & 0x000f000fu) | 0x64006400u) - k1024) * sc1;
+            const half8 bop = {lo02[0], lo02[1], lo13[0], lo13[1], hi02[0], hi02[1], hi13[0], hi13[1]};
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) {
+                const half8 aop =
+                    *reinterpret_cast<const half8*>(&sA[buf][(rt * 16 + lrow) * QM_AS + (l * 4 + G) * 16]);
+                const f32x4q aux = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) sums[l][rt][r] = sums[l][rt][r] + dd[rt][r] * aux[r];
+            }
+        }
+        {
+            const half4v mop = {(_Float16)(float)mnv[0], (_Float16)(float)mnv[0], (_Float16)(float)mnv[1],
+                                (_Float16)(float)mnv[1]};
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) {
+                const half4v bsop = *reinterpret_cast<const half4v*>(&sBS[buf][(rt * 16 + lrow) * 16 + 4 * G]);
+                const f32x4q sumi = __builtin_amdgcn_mfma_f32_16x16x16f16(bsop, mop, zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float dm = dmwf * dxr[rt][r];
+                    sumf[rt][r] = sumf[rt][r] - dm * sumi[r];
+                }
+            }
+        }
+        if (sb + 1 < nsb) {
+            sa(buf ^ 1, 0, ra0); sa(buf ^ 1, 1, ra1); sa(buf ^ 1, 2, ra2); sa(buf ^ 1, 3, ra3);
+            if (tid < 64) sbs(buf ^ 1, rb);
+            hd = nhd; c0 = nc0; c1 = nc1; dx0 = ndx0; dx1 = ndx1;
+        }
+        __syncthreads();
+    }
+    if (col >= N) return;
+    const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = m0 + rt * 16 + 4 * G + r;
+            if (m >= M) continue;
+            float tot = 0.0f;
+#pragma unroll
+            for (int l = 0; l < 8; l++) tot = tot + sums[l][rt][r];
+            float v = sumf[rt][r] + tot;
+            if (bias) v = v + bv;
+            if (y_bf16)
+                reinterpret_cast<uint16_t*>(y)[(int64_t)m * N + col] = bf16_from_f32(v);
+            else
+                reinterpret_cast<float*>(y)[(int64_t)m * N + col] = v;
+        }
+    }
+}
+
 tn_status check_qk(const char* op, int64_t n, int64_t k) {
     if (n < 0 || k <= 0 || k % QKK != 0) {
         char buf[384];
@@ -532,7 +783,28 @@ tn_status linear_qk(hipStream_t st, const XT* x, int64_t m, int64_t k, const uin
     if (m == 0 || n == 0) return TN_OK;
     if (n > INT32_MAX || k > INT32_MAX) return fail(TN_EVALUE, "torch._C._quantized_linear: shape too large");
     const size_t ysz = y_bf16 ? 2 : 4;
-    // rows of x in chunks of up to 4 (every output is the same recurrence, so
+    if (m > 4) {
+        // prefill: Q8_K prepass, then the MFMA GEMM
+        const int nsb = (int)(k / QKK);
+        const int64_t M_pad = cdiv(m, QM_ROWS) * QM_ROWS;
+        if (M_pad > INT32_MAX) return fail(TN_EVALUE, "torch._C._quantized_linear: shape too large");
+        const size_t xa_bytes = (size_t)M_pad * nsb * QKK * 2, bs_bytes = (size_t)M_pad * nsb * 32;
+        void* ws = nullptr;
+        tn_status s = workspace(st, xa_bytes + bs_bytes + (size_t)M_pad * nsb * 4, &ws);
+        if (s != TN_OK) return s;
+        uint16_t* xa = static_cast<uint16_t*>(ws);
+        uint16_t* xbs = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + xa_bytes);
+        float* xdv = reinterpret_cast<float*>(static_cast<char*>(ws) + xa_bytes + bs_bytes);
+        hipLaunchKernelGGL((k_q8k_rows<XT>), dim3((unsigned)cdiv(M_pad * nsb, 4)), dim3(256), 0, st, x, (int)m,
+                           (int)M_pad, (int)k, nsb, xa, xbs, xdv);
+        TN_LAUNCHED();
+        const dim3 grid((unsigned)cdiv(n, QM_COLS), (unsigned)(M_pad / QM_ROWS));
+        hipLaunchKernelGGL(k_gemm_qk, grid, dim3(QM_THREADS), 0, st, xa, xbs, xdv, (int)m, (int)M_pad, nsb, w, (int)n,
+                           bias, y, y_bf16);
+        TN_LAUNCHED();
+        return TN_OK;
+    }
+    // decode: rows of x in chunks of up to 4 (every output is the same recurrence, so
     // the chunking changes no bit); the widest chunk whose activations fit LDS
     int64_t r = 0;
     while (r < m) {
