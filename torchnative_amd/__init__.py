@@ -4,7 +4,7 @@ scaled_dot_product_attention -- behind a C ABI (include/tnhip.h,
 libtnhip.so) and a Python mirror of the reference's `torch._C` entry points.
 """
 
-from . import _C, gguf, quant, tensor
+from . import _C, device, gguf, quant, tensor
 from ._C import (
     QTensor,
     _aten_dispatch,
