@@ -116,6 +116,15 @@ def test_default_scale_and_explicit_scale_agree(tn):
     assert np.array_equal(a.numpy(), b.numpy()) and np.array_equal(la.numpy(), lb.numpy())
 
 
+def test_negative_scale_is_refused_by_name(tn):
+    """The prefill kernels take the row maximum of the unscaled scores, right
+    only for scale >= 0; a negative scale refuses instead of returning wrong
+    numbers."""
+    q = tn.tensor(np.ones((1, 1, 4, 64), np.float32), device="hip")
+    with pytest.raises(NotImplementedError, match="negative scale"):
+        tn._aten_dispatch(OP, q, q, q, 0.0, False, scale=-0.125)
+
+
 def test_gqa_is_indexed_not_tiled(tn):
     """Query head i reads kv head i // n_rep: equal to running each head alone."""
     rng = np.random.default_rng(6)
@@ -131,7 +140,9 @@ def test_gqa_is_indexed_not_tiled(tn):
         assert np.array_equal(oh.numpy()[:, 0], full[:, h])
 
 
-def _decode_case(tn, B, Hq, Hkv, D, lens, cap, seed):
+def _decode_case(tn, B, Hq, Hkv, D, lens, cap, seed, max_len=None, scale=None):
+    """bf16 decode against the oracle per sequence; sequence b attends to keys
+    0 .. min(lens[b], max_len)-1 (a longer length is truncated at max_len)."""
     rng = np.random.default_rng(seed)
     q = rng.standard_normal((B, Hq, D)).astype(np.float32)
     kc = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
@@ -140,17 +151,21 @@ def _decode_case(tn, B, Hq, Hkv, D, lens, cap, seed):
     kb = tn.tensor(kc, dtype="bfloat16", device="hip")
     vb = tn.tensor(vc, dtype="bfloat16", device="hip")
     ln = tn.tensor(np.asarray(lens, np.int32), device="hip")
-    o, lse = tn.sdpa_decode(qb, kb, vb, ln, max(lens))
+    max_len = max(lens) if max_len is None else max_len
+    o, lse = tn.sdpa_decode(qb, kb, vb, ln, max_len, scale=scale)
     got = o.numpy().astype(np.float64)
     glse = lse.numpy().astype(np.float64)
     qw, kw, vw = qb.numpy(), kb.numpy(), vb.numpy()
     worst = 0.0
     for b in range(B):
-        L = lens[b]
+        L = min(lens[b], max_len)
+        if L == 0:  # no keys: 0/0, as the split combine has always returned
+            assert np.all(np.isnan(got[b])) and np.all(glse[b] == -np.inf)
+            continue
         args = (qw[b:b + 1, :, None, :], kw[b:b + 1, :, :L], vw[b:b + 1, :, :L])
-        r32, l32 = O.sdpa(*args)
-        r64, l64 = O.sdpa(*args, dtype=np.float64)
-        pav, _ = O.sdpa(args[0], args[1], np.abs(args[2]), dtype=np.float64)
+        r32, l32 = O.sdpa(*args, scale=scale)
+        r64, l64 = O.sdpa(*args, scale=scale, dtype=np.float64)
+        pav, _ = O.sdpa(args[0], args[1], np.abs(args[2]), scale=scale, dtype=np.float64)
         ref = O.bf16_to_f32(O.bf16_from_f32(r32)).astype(np.float64)
         tol = _bound(r32, r64, pav, bf16=True, got=got[b:b + 1, :, None, :])
         err = np.abs(got[b:b + 1, :, None, :] - ref)
@@ -165,6 +180,38 @@ def test_decode_small_and_ragged(tn):
     _decode_case(tn, 3, 8, 2, 128, [1, 77, 300], 320, 7)
     _decode_case(tn, 2, 4, 4, 64, [129, 64], 200, 8)
     _decode_case(tn, 2, 16, 1, 128, [513, 5], 600, 9)
+
+
+def test_decode_stream_partition_edges(tn):
+    """The stream-K decode cuts all sequences' keys into equal ranges per wave:
+    a range that starts or ends inside a sequence, one that covers many short
+    sequences, empty sequences between them, a single key, and lengths past
+    max_len (truncated)."""
+    rng = np.random.default_rng(11)
+    lens = [int(x) for x in rng.integers(0, 40, size=150)]
+    lens[0], lens[1], lens[-1] = 0, 1, 0
+    _decode_case(tn, 150, 8, 2, 128, lens, 48, 12)
+    _decode_case(tn, 3, 4, 1, 64, [0, 1, 0], 8, 13)
+    _decode_case(tn, 2, 4, 2, 64, [100, 50], 128, 14, max_len=64)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(8, 1, 128), (9, 3, 64), (6, 6, 128), (16, 2, 64), (24, 4, 128)])
+def test_decode_head_groups(tn, hq, hkv, d):
+    """Query heads per kv head 8, 3, 1, 8 and 6 (groups of 8, 3, 1, 8 and 3 heads
+    per wave)."""
+    _decode_case(tn, 3, hq, hkv, d, [700, 33, 1500], 1536, 15 + hq)
+
+
+def test_decode_scale_of_either_sign(tn):
+    _decode_case(tn, 2, 8, 2, 128, [300, 41], 320, 21, scale=0.3)
+    _decode_case(tn, 2, 8, 2, 128, [300, 41], 320, 22, scale=-0.2)
+
+
+def test_decode_above_the_stream_partition_batch_limit(tn):
+    """More than 1024 sequences take the per-split kernel."""
+    rng = np.random.default_rng(23)
+    lens = [int(x) for x in rng.integers(1, 20, size=1100)]
+    _decode_case(tn, 1100, 2, 1, 64, lens, 24, 24)
 
 
 def test_config4_decode_attention_at_full_size(tn):

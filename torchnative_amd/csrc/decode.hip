@@ -617,11 +617,6 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
     int32_t* len = m->state + 1;  // [1]: KV length after appending it
     int32_t* tok = m->state + 2;  // [2]: this token
     const double nan = std::nan("");
-#define TN_TRY(call)                   \
-    do {                               \
-        tn_status e_ = (call);         \
-        if (e_ != TN_OK) return e_;    \
-    } while (0)
     GemvPro none, ln1, ln2, fin, comb;
     ln1.eps = ln2.eps = fin.eps = eps;
     fin.w = m->norm;
@@ -684,7 +679,6 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
         hipLaunchKernelGGL((k_argmax<true, false>), dim3(1), dim3(ARGMAX_THREADS), 0, st, m->logits, (int)m->vocab,
                            nullptr, m->state, m->tokens, m->prompt, (int)m->prompt_len, (int)m->cap);
     TN_LAUNCHED();
-#undef TN_TRY
     return TN_OK;
 }
 

@@ -976,6 +976,402 @@ void k_decode_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restrict__
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode, bf16, stream-K over the cached keys of every sequence.
+// A segment is one (sequence b, kv head, group of NR query heads): its keys
+// are ceil(len_b / 16) units of 16. Laid end to end, the segments are cut
+// into W equal unit ranges, one per wave of a persistent grid, so every wave
+// streams the same number of bytes whatever the length mix. A wave walks its
+// range in chunks of up to 32 keys with the next chunk's K, V and q loads in
+// flight while it computes the current one (raw buffer loads whose range ends
+// at the segment's last key, so keys past it read as zero without a branch),
+// keeps an online softmax per query head, and writes one unnormalised
+// (O, m, l) partial each time its range leaves a segment. The partial of
+// (segment s, wave w) goes to slot s + w: walking the keys in order, neither
+// s nor w decreases and one of them grows, so the slots are distinct and fewer
+// than #segments + W. k_decode_sk_combine merges a segment's partials in wave
+// order. No barrier: every wave works alone.
+//   S^T : MFMA 16x16x32, A = K rows (lane: key lq, d 32c + 8g .. +7), B = q^T;
+//         lane l holds the scores of keys 16kt + 4g + r for head lq.
+//   P.V : VALU, lane (g, d slice DL*lq) over the same keys 16kt + 4g + r, whose
+//         probabilities for head h sit in lane 16g + h of the lane's own
+//         16-lane row: a DPP row_newbcast broadcasts them.
+// Scores are scaled before the row maximum, so any sign of scale is right.
+// ---------------------------------------------------------------------------
+constexpr int SK_UNIT = 16;    // keys per unit of the partition
+constexpr int SK_MAXB = 1024;  // sequences whose prefix sums a workgroup keeps in LDS
+// units per chunk and chunks in the register ring, by head dim: a ring slot
+// holds the chunk's K, V and q (48 VGPRs at D=128 with one unit, 40 at D=64
+// with two), and NB - 1 slots are in flight while one is computed
+template <int D, int NR>
+struct SkCfg {
+    static constexpr int CH = D == 128 ? 1 : 2;
+    static constexpr int NB = (D == 128 && NR > 4) ? 3 : 4;  // 8 heads' accumulators take a slot's registers
+};
+
+template <int D, int NR>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_decode_sk_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kc,
+                      const uint16_t* __restrict__ Vc, int B, int Hq, int Hkv, int nrep, int cap,
+                      const int32_t* __restrict__ lens, int max_len, float sl2, float* __restrict__ part_o,
+                      float2* __restrict__ part_ml, int* __restrict__ pref_out) {
+    static_assert(D == 128 || D == 64, "head dim");
+    constexpr int DL = D / 16;  // d values per lane in P.V
+    constexpr int CH = SkCfg<D, NR>::CH, NB = SkCfg<D, NR>::NB;
+    typedef typename std::conditional<DL == 8, uint4, uint2>::type vchunk;
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    __shared__ int s_len[SK_MAXB];
+    __shared__ int s_pre[SK_MAXB + 1];  // G * (units of sequences 0 .. b-1); the host checks it fits
+
+    const int groups = nrep / NR;
+    const int G = Hkv * groups;  // segments per sequence
+    // lengths clamped to [0, max_len] (a longer one is truncated) and their
+    // prefix sums in units, scaled by the segments per sequence
+    for (int i = threadIdx.x; i < B; i += blockDim.x) {
+        int len = lens[i];
+        s_len[i] = len < 0 ? 0 : (len > max_len ? max_len : len);
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        // one wave scans: 64 lanes take consecutive stripes of the sequences
+        const int per = (B + 63) / 64;
+        const int lo = min(B, (int)threadIdx.x * per), hi = min(B, lo + per);
+        int run = 0;
+        for (int i = lo; i < hi; i++) run += (s_len[i] + SK_UNIT - 1) / SK_UNIT;
+        int inc = run;  // inclusive scan over the lanes
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(inc, off, 64);
+            if ((int)threadIdx.x >= off) inc += t;
+        }
+        int acc = inc - run;
+        for (int i = lo; i < hi; i++) {
+            s_pre[i] = acc * G;
+            acc += (s_len[i] + SK_UNIT - 1) / SK_UNIT;
+        }
+        if (threadIdx.x == 63) s_pre[B] = inc * G;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i <= B; i += blockDim.x) pref_out[i] = s_pre[i];
+
+    // values every lane of a wave agrees on, moved to scalar registers so that
+    // the buffer descriptors built from them stay scalar
+    auto rfl = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+    const int lane = threadIdx.x & 63, lq = lane & 15, g = lane >> 4;
+    // W = min(waves of the grid, units): every working wave gets at least one
+    // unit, so the waves meeting a segment are consecutive
+    const int T = rfl(s_pre[B]);
+    const int64_t W = min((int64_t)gridDim.x * (blockDim.x >> 6), (int64_t)T);
+    const int wv = (int)blockIdx.x * (int)(blockDim.x >> 6) + rfl((int)threadIdx.x >> 6);
+    if (wv >= W) return;  // uniform over the wave
+    const int u_lo = rfl((int)((int64_t)wv * T / W)), u_hi = rfl((int)((int64_t)(wv + 1) * T / W));
+
+    // walking state, uniform over the wave: the segment (b, sg) holding unit u
+    int b, sg, n, len, seg0;
+    {
+        int lo = 0, hi = B;  // largest b with s_pre[b] <= u_lo (s_pre[B] = T > u_lo)
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (rfl(s_pre[mid]) <= u_lo) lo = mid; else hi = mid;
+        }
+        b = lo;
+        len = rfl(s_len[b]);
+        n = (len + SK_UNIT - 1) / SK_UNIT;  // > 0: u_lo lies in b's units
+        const int pb = rfl(s_pre[b]);
+        sg = (u_lo - pb) / n;
+        seg0 = pb + sg * n;
+    }
+    int u = u_lo;
+
+    struct Chunk {
+        int b, sg, key0, nk;
+        bool last;
+    };
+    // the next chunk of the range; past its end, an empty chunk (nk = 0) whose
+    // loads have a zero-byte range: they read zeros and touch no memory, so
+    // every ring step issues the same loads
+    auto make = [&]() {
+        Chunk c;
+        if (u >= u_hi) {
+            c.b = 0;
+            c.sg = 0;
+            c.key0 = 0;
+            c.nk = 0;
+            c.last = false;
+            return c;
+        }
+        const int seg_end = seg0 + n;
+        const int cu = min(CH, min(u_hi - u, seg_end - u));
+        c.b = b;
+        c.sg = sg;
+        c.key0 = (u - seg0) * SK_UNIT;
+        c.nk = min(cu * SK_UNIT, len - c.key0);
+        c.last = (u + cu == seg_end) || (u + cu == u_hi);
+        u += cu;
+        if (u == seg_end && u < u_hi) {  // on to the next segment that has keys
+            if (++sg == G) {
+                sg = 0;
+                do {
+                    ++b;
+                    len = rfl(s_len[b]);
+                } while (len == 0);
+                n = (len + SK_UNIT - 1) / SK_UNIT;
+            }
+            seg0 = seg_end;
+        }
+        return c;
+    };
+
+    struct Buf {
+        u32x4_t k[CH][D / 32];
+        vchunk v[CH][4];
+        u32x4_t q[D / 32];
+    };
+    auto load = [&](Buf& f, const Chunk& c) {
+        const int cb = rfl(c.b), csg = rfl(c.sg), ck0 = rfl(c.key0), cnk = rfl(c.nk);
+        const int kvh = csg / groups, grp = csg % groups;
+        const int64_t row0 = ((int64_t)cb * Hkv + kvh) * cap + ck0;
+        const uint32_t kbytes = (uint32_t)(cnk * D * 2);
+        const buf_rsrc rk = make_rsrc(Kc + row0 * D, kbytes);
+        const buf_rsrc rv = make_rsrc(Vc + row0 * D, kbytes);
+        const buf_rsrc rq = make_rsrc(Qg + ((int64_t)cb * Hq + kvh * nrep + grp * NR) * D,
+                                      cnk ? (uint32_t)(NR * D * 2) : 0u);
+#if __HIP_DEVICE_COMPILE__
+        constexpr int NT = 2;  // cache policy: non-temporal, the caches are read once
+#pragma unroll
+        for (int kt = 0; kt < CH; kt++) {
+#pragma unroll
+            for (int cc = 0; cc < D / 32; cc++)
+                f.k[kt][cc] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rk, (uint32_t)(((16 * kt + lq) * D + 32 * cc + 8 * g) * 2), 0, NT);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t off = (uint32_t)(((16 * kt + 4 * g + r) * D + DL * lq) * 2);
+                if constexpr (DL == 8)
+                    f.v[kt][r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, NT));
+                else
+                    f.v[kt][r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, NT));
+            }
+        }
+#pragma unroll
+        for (int cc = 0; cc < D / 32; cc++)
+            f.q[cc] = __builtin_amdgcn_raw_buffer_load_b128(rq, (uint32_t)((lq * D + 32 * cc + 8 * g) * 2), 0, 0);
+#else
+        (void)f;
+        (void)rk;
+        (void)rv;
+        (void)rq;
+#endif
+    };
+
+    float o[NR][DL];
+#pragma unroll
+    for (int hh = 0; hh < NR; hh++)
+#pragma unroll
+        for (int e = 0; e < DL; e++) o[hh][e] = 0.0f;
+    float m = -INFINITY, l = 0.0f;  // this lane's head lq; l is the lane's share
+
+    auto compute = [&](const Buf& f, const Chunk& c) {
+        f32x4 s[CH];
+#pragma unroll
+        for (int kt = 0; kt < CH; kt++) {
+            s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int cc = 0; cc < D / 32; cc++)
+                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.k[kt][cc]),
+                                                                __builtin_bit_cast(bf16x8, f.q[cc]), s[kt], 0, 0, 0);
+        }
+        float t[CH][4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < CH; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                t[kt][r] = (16 * kt + 4 * g + r < c.nk) ? s[kt][r] * sl2 : -INFINITY;
+                mx = fmaxf(mx, t[kt][r]);
+            }
+        mx = wave_xor_max(mx);
+        const float mn = fmaxf(m, mx);
+        const float alpha = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+        const float mu = (mn == -INFINITY) ? 0.0f : mn;
+        float p[CH][4];
+        float ps = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < CH; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                p[kt][r] = __builtin_amdgcn_exp2f(t[kt][r] - mu);
+                ps = ps + p[kt][r];
+            }
+        l = l * alpha + ps;
+        m = mn;
+#pragma unroll
+        for (int hh = 0; hh < NR; hh++) {
+            const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), hh));
+#pragma unroll
+            for (int e = 0; e < DL; e++) o[hh][e] = o[hh][e] * a;
+        }
+#pragma unroll
+        for (int kt = 0; kt < CH; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                uint32_t ws[DL / 2];
+                __builtin_memcpy(ws, &f.v[kt][r], sizeof(ws));
+                float vf[DL];
+#pragma unroll
+                for (int e = 0; e < DL / 2; e++) {
+                    vf[2 * e] = __builtin_bit_cast(float, ws[e] << 16);
+                    vf[2 * e + 1] = __builtin_bit_cast(float, ws[e] & 0xffff0000u);
+                }
+#pragma unroll
+                for (int hh = 0; hh < NR; hh++) {
+                    float pb;
+                    switch (hh) {  // lane 16g + hh of this lane's row
+                        case 0: pb = dpp_f<0x150>(p[kt][r]); break;
+                        case 1: pb = dpp_f<0x151>(p[kt][r]); break;
+                        case 2: pb = dpp_f<0x152>(p[kt][r]); break;
+                        case 3: pb = dpp_f<0x153>(p[kt][r]); break;
+                        case 4: pb = dpp_f<0x154>(p[kt][r]); break;
+                        case 5: pb = dpp_f<0x155>(p[kt][r]); break;
+                        case 6: pb = dpp_f<0x156>(p[kt][r]); break;
+                        default: pb = dpp_f<0x157>(p[kt][r]); break;
+                    }
+#pragma unroll
+                    for (int e = 0; e < DL; e++) o[hh][e] = __builtin_fmaf(pb, vf[e], o[hh][e]);
+                }
+            }
+        if (c.last) {
+            const int64_t slot = (int64_t)c.b * G + c.sg + wv;
+            const float lt = wave_xor_sum(l);
+#pragma unroll
+            for (int hh = 0; hh < NR; hh++) {
+                float ov[DL];
+#pragma unroll
+                for (int e = 0; e < DL; e++) ov[e] = wave_xor_sum(o[hh][e]);
+                if (g == 0) {
+                    float* dst = part_o + (slot * NR + hh) * D + DL * lq;
+#pragma unroll
+                    for (int e = 0; e < DL; e += 4)
+                        *reinterpret_cast<float4*>(dst + e) = make_float4(ov[e], ov[e + 1], ov[e + 2], ov[e + 3]);
+                }
+            }
+            if (g == 0 && lq < NR) part_ml[slot * NR + lq] = make_float2(m, lt);
+#pragma unroll
+            for (int hh = 0; hh < NR; hh++)
+#pragma unroll
+                for (int e = 0; e < DL; e++) o[hh][e] = 0.0f;
+            m = -INFINITY;
+            l = 0.0f;
+        }
+    };
+
+    // the ring: NB chunks issued up front; each step computes the oldest and
+    // refills its slot with the chunk NB ahead, so NB - 1 chunks are in flight
+    // while one is computed. The loop is unrolled NB times so that every slot
+    // keeps its registers, and no slot is ever free across the loop head
+    // (where a register reused as a temporary would make the compiler wait
+    // for every load in flight).
+    // The first PEEL turns of the ring run as straight-line code: at the loop
+    // head the compiler merges the entry and back-edge states and waits for
+    // every load in flight, so only waves with more chunks than that reach it.
+    Buf f[NB];
+    Chunk c[NB];
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        c[i] = make();
+        load(f[i], c[i]);
+    }
+    auto step = [&](int j) {
+        if (c[j].nk == 0) return false;
+        compute(f[j], c[j]);
+        c[j] = make();
+        load(f[j], c[j]);
+        __builtin_amdgcn_sched_barrier(0);
+        return true;
+    };
+    constexpr int PEEL = 3;
+#pragma unroll
+    for (int t = 0; t < PEEL * NB; t++)
+        if (!step(t % NB)) return;
+    for (;;) {
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+            if (!step(j)) return;
+    }
+}
+
+// Merges the stream-K partials of one (sequence, query head) in wave order:
+// the waves whose unit ranges meet the segment are those from the wave
+// holding its first unit to the wave holding its last (wave of unit u:
+// ceil((u+1) W / T) - 1 for ranges [w T / W, (w+1) T / W), with the kernel's
+// W = min(grid waves, T), so no wave in between is empty). A sequence with no
+// keys gives 0/0, as the split combine does.
+template <int D, int NR, typename OT>
+__global__ __launch_bounds__(D) void k_decode_sk_combine(const float* __restrict__ part_o,
+                                                         const float2* __restrict__ part_ml,
+                                                         const int* __restrict__ pref,
+                                                         const int32_t* __restrict__ lens, int B, int Hq, int Hkv,
+                                                         int nrep, int max_len, int64_t W, OT* __restrict__ out,
+                                                         float* __restrict__ lse) {
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const int groups = nrep / NR, G = Hkv * groups;
+    const int kvh = h / nrep, hr = h % nrep, grp = hr / NR, hh = hr % NR;
+    const int sg = kvh * groups + grp;
+    int len = lens[b];
+    len = len < 0 ? 0 : (len > max_len ? max_len : len);
+    const int n = (len + SK_UNIT - 1) / SK_UNIT;
+    const int64_t T = pref[B];
+    const int64_t u0 = pref[b] + (int64_t)sg * n;  // the kernel's int sums, widened here
+    W = W < T ? W : T;
+    const int64_t slot0 = (int64_t)b * G + sg;
+    float mm = -INFINITY, tl = 0.0f, acc = 0.0f;
+    int64_t w_lo = 0, w_hi = -1;
+    if (n > 0) {
+        w_lo = ((u0 + 1) * W + T - 1) / T - 1;
+        w_hi = ((u0 + n) * W + T - 1) / T - 1;
+    }
+    // batches of CB partials, every load of a batch in flight at once; the
+    // running sums are rescaled when a batch raises the maximum
+    constexpr int CB = 32;
+    for (int64_t w0 = w_lo; w0 <= w_hi; w0 += CB) {
+        float2 ml[CB];
+        float ov[CB];
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            ml[i] = make_float2(-INFINITY, 0.0f);
+            ov[i] = 0.0f;
+            if (w0 + i <= w_hi) {
+                const int64_t sl = (slot0 + w0 + i) * NR + hh;
+                ml[i] = part_ml[sl];
+                ov[i] = part_o[sl * D + d];
+            }
+        }
+        float bm = mm;
+#pragma unroll
+        for (int i = 0; i < CB; i++) bm = fmaxf(bm, ml[i].x);
+        const float mu = (bm == -INFINITY) ? 0.0f : bm;
+        if (mm != -INFINITY) {
+            const float a = exp2f(mm - mu);
+            tl = tl * a;
+            acc = acc * a;
+        }
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            const float f = exp2f(ml[i].x - mu);  // 0 for the padding entries
+            tl = tl + ml[i].y * f;
+            acc = acc + ov[i] * f;
+        }
+        mm = bm;
+    }
+    const float mu = (mm == -INFINITY) ? 0.0f : mm;
+    if constexpr (sizeof(OT) == 2)
+        out[((int64_t)b * Hq + h) * D + d] = bf16_from_f32(acc / tl);
+    else
+        out[((int64_t)b * Hq + h) * D + d] = acc / tl;
+    if (lse && d == 0) lse[(int64_t)b * Hq + h] = mu * LN2 + logf(tl);
+}
+
 // Decode, f32 (the precision the reference runs an f32 model in). Grid
 // (splits of 256 keys, Hq, B); thread t of a workgroup scores key t of the
 // split (a sequential f32 dot over D), the workgroup reduces max and sum,
@@ -1351,6 +1747,64 @@ tn_status decode_launch(hipStream_t st, int dtype, const void* q, const void* k_
 
 namespace {
 
+// The stream-K bf16 decode (k_decode_sk_bf16 + k_decode_sk_combine) for
+// B <= SK_MAXB, its partials, unit prefix sums and the grid in the stream's
+// workspace.
+template <int D, int NR>
+tn_status decode_sk_run(hipStream_t st, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t B,
+                        int64_t Hq, int64_t Hkv, int64_t cap, const int32_t* lens, int64_t max_len, float sl2,
+                        uint16_t* out, float* lse) {
+    const int nrep = (int)(Hq / Hkv);
+    const int64_t G = Hkv * (nrep / NR);
+    int wgs = 0;
+    TN_TRY(resident_workgroups(reinterpret_cast<const void*>(&k_decode_sk_bf16<D, NR>), 256, 0, &wgs));
+    const int64_t W = (int64_t)wgs * 4;
+    const int64_t slots = B * G + W;
+    const size_t po = (size_t)slots * NR * D * sizeof(float);
+    const size_t pm = (size_t)slots * NR * sizeof(float2);
+    const size_t pp = (size_t)(B + 1) * sizeof(int);
+    void* ws = nullptr;
+    TN_TRY(workspace(st, po + pm + pp, &ws));
+    float* part_o = static_cast<float*>(ws);
+    float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + po);
+    int* pref = reinterpret_cast<int*>(static_cast<char*>(ws) + po + pm);
+    hipLaunchKernelGGL((k_decode_sk_bf16<D, NR>), dim3((unsigned)wgs), dim3(256), 0, st, q, kc, vc, (int)B, (int)Hq,
+                       (int)Hkv, nrep, (int)cap, lens, (int)max_len, sl2, part_o, part_ml, pref);
+    TN_LAUNCHED();
+    hipLaunchKernelGGL((k_decode_sk_combine<D, NR, uint16_t>), dim3((unsigned)Hq, (unsigned)B), dim3(D), 0, st,
+                       part_o, part_ml, pref, lens, (int)B, (int)Hq, (int)Hkv, nrep, (int)max_len, W, out, lse);
+    TN_LAUNCHED();
+    return TN_OK;
+}
+
+tn_status decode_sk_launch(hipStream_t st, const void* q, const void* k_cache, const void* v_cache, int64_t B,
+                           int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens, int64_t max_len,
+                           double scale, void* out, float* lse) {
+    const int nrep = (int)(Hq / Hkv);
+    const int nr = nrep % 8 == 0 ? 8 : nrep % 4 == 0 ? 4 : nrep % 3 == 0 ? 3 : nrep % 2 == 0 ? 2 : 1;
+    const double sc = std::isnan(scale) ? 1.0 / std::sqrt((double)D) : scale;
+    const float sl2 = (float)sc * LOG2E;
+    auto qq = static_cast<const uint16_t*>(q);
+    auto kk = static_cast<const uint16_t*>(k_cache);
+    auto vv = static_cast<const uint16_t*>(v_cache);
+    auto oo = static_cast<uint16_t*>(out);
+#define TN_SK(DD, NR) return decode_sk_run<DD, NR>(st, qq, kk, vv, B, Hq, Hkv, cap, lens, max_len, sl2, oo, lse)
+#define TN_SK_D(DD)                    \
+    switch (nr) {                      \
+        case 8: TN_SK(DD, 8);          \
+        case 4: TN_SK(DD, 4);          \
+        case 3: TN_SK(DD, 3);          \
+        case 2: TN_SK(DD, 2);          \
+        default: TN_SK(DD, 1);         \
+    }
+    if (D == 128) {
+        TN_SK_D(128)
+    }
+    TN_SK_D(64)
+#undef TN_SK_D
+#undef TN_SK
+}
+
 tn_status refuse_head_dim(int64_t D) {
     char buf[256];
     std::snprintf(buf, sizeof buf,
@@ -1529,6 +1983,8 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     // 0 none, 1 f32, 2 bf16: the kernels' MASK parameter
     const int mk = !attn_mask ? 0 : mask_dtype == TN_F32 ? 1 : 2;
     if (D != 64 && D != 128) return refuse_head_dim(D);
+    // the kernels take the row maximum before scaling, which needs scale >= 0
+    if (scale < 0.0) return fail(TN_ENOTIMPL, std::string(OP) + ": a negative scale is not implemented on the hip device");
     if (B * Hq * L == 0) return TN_OK;  // nothing to write (aten.rs:10242-10259 returns empty zeros)
     if (!q || !k || !v || !out) return fail(TN_EVALUE, std::string(OP) + ": null pointer");
     if (L > INT32_MAX || S > INT32_MAX || Hq > 65535 || B > 65535)
@@ -1659,11 +2115,18 @@ tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_c
     // the f32 kernels move rows in 16-byte pieces
     if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) % 16 != 0)
         return fail(TN_EINVAL, "sdpa_decode: q, the caches and out must be 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    // the stream-K kernel counts 16-key units of all segments in an int
+    if (dtype == TN_BF16 && B <= SK_MAXB && B * Hq * cdiv(max_len, SK_UNIT) <= INT32_MAX)
+        return decode_sk_launch(st, q, k_cache, v_cache, B, Hq, Hkv, cap, D, lens, max_len, scale, out, lse);
+    // the split kernel below takes the row maximum before scaling
+    if (dtype == TN_BF16 && scale < 0.0)
+        return fail(TN_ENOTIMPL, "sdpa_decode: a negative scale is not implemented on the hip device for more than 1024 "
+                                 "bfloat16 sequences");
     const int64_t nsplit = cdiv(max_len, DEC_SPLIT);
     const size_t po = (size_t)B * Hq * nsplit * D * sizeof(float);
     const size_t pm = (size_t)B * Hq * nsplit * sizeof(float2);
     void* ws = nullptr;
-    hipStream_t st = (hipStream_t)stream;
     s = workspace(st, po + pm, &ws);
     if (s != TN_OK) return s;
     return decode_launch(st, dtype, q, k_cache, v_cache, B, Hq, Hkv, cap, D, lens, max_len, scale, out, lse,

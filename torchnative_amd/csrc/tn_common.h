@@ -59,6 +59,12 @@ constexpr int DECODE_SPLIT_KEYS = 256;  // keys per split of the decode attentio
         if (e_ != hipSuccess) return ::tn::hip_fail(e_, #call);  \
     } while (0)
 
+#define TN_TRY(call)                \
+    do {                            \
+        tn_status e_ = (call);      \
+        if (e_ != TN_OK) return e_; \
+    } while (0)
+
 #define TN_LAUNCHED()                                              \
     do {                                                           \
         ::tn::counters().dispatches.fetch_add(1);                  \
