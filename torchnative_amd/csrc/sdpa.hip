@@ -83,24 +83,6 @@ __device__ inline void wait_vmcnt() {
 }
 
 
-// Raw buffer descriptor over `bytes` bytes at `base`: offsets at or past the
-// end read as zero. Word 3 selects a 32-bit data format (any non-zero format
-// enables the access); all else is zero.
-#if __HIP_DEVICE_COMPILE__
-typedef __amdgpu_buffer_rsrc_t buf_rsrc;
-#else
-typedef struct { uint32_t w[4]; } buf_rsrc;  // the host pass never emits kernel code
-#endif
-
-__device__ inline buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
-#if __HIP_DEVICE_COMPILE__
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-#else
-    (void)base;
-    (void)bytes;
-    return buf_rsrc{};
-#endif
-}
 
 // 16 bytes per lane from a raw buffer straight into LDS (buffer_load_dwordx4
 // ... lds): lane l's bytes land at lds_wave_base + 16*l, which must be

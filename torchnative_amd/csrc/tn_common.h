@@ -72,6 +72,27 @@ constexpr int DECODE_SPLIT_KEYS = 256;  // keys per split of the decode attentio
         if (e_ != hipSuccess) return ::tn::hip_fail(e_, "launch"); \
     } while (0)
 
+// ---- raw buffer access ------------------------------------------------------
+
+// Raw buffer descriptor over `bytes` bytes at `base`: offsets at or past the
+// end read as zero. Word 3 selects a 32-bit data format (any non-zero format
+// enables the access); all else is zero.
+#if __HIP_DEVICE_COMPILE__
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
+#else
+typedef struct { uint32_t w[4]; } buf_rsrc;  // the host pass never emits kernel code
+#endif
+
+__device__ inline buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+#else
+    (void)base;
+    (void)bytes;
+    return buf_rsrc{};
+#endif
+}
+
 // ---- reduced floats (exact, identical on host and device) ---------------
 
 // f32 -> f16 round-to-nearest-even with subnormals and overflow to inf: the
