@@ -198,7 +198,8 @@ tn_status tn_q4_k_linear(void* stream, const void* x, int x_dtype, int64_t m, in
  * `aten._scaled_dot_product_flash_attention_for_cpu(q, k, v, dropout_p=0.,
  * is_causal=False, *, attn_mask=None, scale=None) -> (out, logsumexp)`
  * (aten.rs:10092-10440), device half.
- *   q [B,Hq,L,D], k/v [B,Hkv,S,D] in `dtype` (TN_F32 or TN_BF16), dense.
+ *   q [B,Hq,L,D], k/v [B,Hkv,S,D] in `dtype` (TN_F32, TN_BF16 or TN_F16),
+ *   dense; TN_F64 is refused by name.
  *   GQA: query head h reads key/value head h / (Hq/Hkv), indexed, not
  *   materialised (aten.rs:17106-17126); Hq % Hkv != 0 is refused by name.
  *   is_causal: upper-left aligned, row t attends keys 0..=t (aten.rs:10038-10041).
@@ -210,9 +211,10 @@ tn_status tn_q4_k_linear(void* stream, const void* x, int x_dtype, int64_t m, in
  *   scale: NaN selects 1/sqrt(D) (aten.rs:10216).
  *   out: [B,Hq,L,D] in `dtype` (row-major, aten.rs:10436-10437);
  *   lse: nullable f32 [B,Hq,L], logsumexp over the masked, scaled scores.
- * Accumulation is f32 for both dtypes (aten.rs:10196-10206); a bf16 run
- * narrows the probabilities to bf16 between the two products, as upstream's
- * blocked kernel does (flash.rs:503-516), and the output RNE.
+ * Accumulation is f32 for every dtype (the reference widens bf16 and f16 to
+ * f32, aten.rs:10196-10213); a bf16 or f16 run narrows the probabilities to
+ * its dtype between the two products, as upstream's blocked kernel does
+ * (flash.rs:503-516), and the output RNE.
  * Head dims 64 and 128 run; others are refused by name. */
 tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, const void* v,
                       int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t S, int64_t D,

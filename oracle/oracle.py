@@ -498,16 +498,23 @@ def synth_q4_k_weight(n, k, seed):
     return blob.tobytes()
 
 
-def sdpa_tolerance(ref32, ref64, kind="float32", p=None, got=None):
+def sdpa_tolerance(ref32, ref64, kind="float32", p=None, got=None, vsum=None):
     """Per-element bound on |gpu - ref32| for one SDPA output tensor.
 
     The rule (docs/numerics/AGREE.md section 2 of the reference, applied per
     tensor): 4x the reference's own fp32-vs-fp64 distance, floored at 10 ulp
-    (1.186e-6) of the tensor's scale. For a bf16 output add one bf16 ulp
-    (both sides round to bf16; the spacing is taken at max(|ref|, |got|), as a
-    value just under a power of two may round up across it) and, when ``p`` is
-    given, the P-narrowing term u * sum_j P_ij |V_jd| with u = 2^-8, bf16's
-    unit roundoff (pass ``p`` = that sum: the attention output with |V|)."""
+    (1.186e-6) of the tensor's scale. A 16-bit output (``kind`` "bfloat16" or
+    "float16") adds:
+
+    - one ulp of the output format (both sides round to it; the spacing is
+      taken at max(|ref|, |got|), as a value just under a power of two may
+      round up across it; f16 spacing stops shrinking at its subnormals);
+    - when ``p`` is given, the P-narrowing term u * sum_j P_ij |V_jd| with u
+      the format's unit roundoff (2^-8 bf16, 2^-11 f16): pass ``p`` = that
+      sum, the attention output with |V|;
+    - for f16, when ``vsum`` = sum_j |V_jd| over the attended keys is given,
+      2^-25 * vsum: probabilities below 2^-14 round in f16's subnormal range,
+      at most 2^-25 each, against a row sum of at least 1."""
     ref32 = np.asarray(ref32, np.float64)
     ref64 = np.asarray(ref64, np.float64)
     fin = np.isfinite(ref64)
@@ -515,10 +522,14 @@ def sdpa_tolerance(ref32, ref64, kind="float32", p=None, got=None):
     scale_ = float(np.max(np.abs(ref64[fin]))) if fin.any() else 0.0
     tol = max(4.0 * own, 1.186e-6 * scale_)
     tol = np.full(ref32.shape, tol)
-    if kind == "bfloat16":
+    if kind in ("bfloat16", "float16"):
+        mant, emin, tiny, u = (7, -126, 2.0 ** -133, 2.0 ** -8) if kind == "bfloat16" else \
+            (10, -14, 2.0 ** -24, 2.0 ** -11)
         mag = np.abs(ref64) if got is None else np.maximum(np.abs(ref64), np.abs(np.asarray(got, np.float64)))
-        e = np.floor(np.log2(np.where(mag > 0, mag, 1e-38)))
-        tol = tol + np.where(mag > 0, 2.0 ** (e - 7), 2.0 ** -133)
+        e = np.maximum(np.floor(np.log2(np.where(mag > 0, mag, 1e-38))), emin)
+        tol = tol + np.where(mag > 0, 2.0 ** (e - mant), tiny)
         if p is not None:
-            tol = tol + 2.0 ** -8 * np.asarray(p, np.float64)
+            tol = tol + u * np.asarray(p, np.float64)
+        if kind == "float16" and vsum is not None:
+            tol = tol + 2.0 ** -25 * np.asarray(vsum, np.float64)
     return tol

@@ -99,6 +99,7 @@ def test_sdpa_refusals_name_the_reason(L):
     assert call(mask=1, mask_dtype=_lib.TN_F16) == _lib.TN_EINVAL
     assert "Attention mask is the same data type as query" in _lib.last_error()
     assert call(dtype=_lib.TN_F32, mask=1, mask_dtype=_lib.TN_BF16) == _lib.TN_EINVAL
+    assert call(dtype=_lib.TN_F16, mask=1, mask_dtype=_lib.TN_BF16) == _lib.TN_EINVAL
     # empty batch: nothing to write, success without touching a pointer
     assert call(B=0) == _lib.TN_OK
     st = L.tn_sdpa_decode(None, _lib.TN_BF16, None, None, None, 2, 32, 8, 64, 128, None, 65, float("nan"),

@@ -6,7 +6,9 @@ scale (the reference's docs/numerics/AGREE.md section 2 rule). A bf16 run adds
 one bf16 ulp of max(|ref|, |gpu|) (both sides round to bf16) and the
 P-narrowing term u * sum_j P_ij |V_jd| with u = 2^-8, bf16's unit roundoff
 (upstream's blocked kernel narrows P to bf16 between the products,
-flash.rs:503-516). The lse is compared in f32 with the same base rule.
+flash.rs:503-516). An f16 run adds one f16 ulp, the same term with u = 2^-11
+and 2^-25 * sum_j |V_jd| over the attended keys (probabilities that round in
+f16's subnormal range). The lse is compared in f32 with the same base rule.
 """
 
 import math
@@ -32,38 +34,60 @@ def _det(shape, seed):
     return np.array(O.sdpa_det(int(np.prod(shape)), seed), dtype=np.float64).reshape(shape)
 
 
-def _bound(ref32, ref64, pav=None, bf16=False, got=None):
-    return O.sdpa_tolerance(ref32, ref64, "bfloat16" if bf16 else "float32", p=pav, got=got)
+def _bound(ref32, ref64, pav=None, bf16=False, got=None, kind=None, vsum=None):
+    kind = kind or ("bfloat16" if bf16 else "float32")
+    return O.sdpa_tolerance(ref32, ref64, kind, p=pav, got=got, vsum=vsum)
+
+
+def _dev(tn, dtype, a):
+    """A device tensor of `dtype` holding `a` rounded RNE to it."""
+    if dtype == "float16":
+        return tn.tensor(a.astype(np.float32).astype(np.float16), dtype="float16", device="hip")
+    return tn.tensor(a.astype(np.float32), dtype=dtype, device="hip")
+
+
+def _narrow(dtype, r32):
+    """The oracle's f32 answer narrowed RNE to the output dtype, widened back."""
+    if dtype == "bfloat16":
+        return O.bf16_to_f32(O.bf16_from_f32(r32)).astype(np.float64)
+    if dtype == "float16":
+        return np.asarray(r32, np.float32).astype(np.float16).astype(np.float64)
+    return np.asarray(r32, np.float64)
+
+
+def _vsum(vw, Hq, L, causal, mask=None):
+    """sum_j |V_jd| over the keys row i attends (upper-left causal, finite mask)."""
+    B, Hkv, S, D = vw.shape
+    av = np.repeat(np.abs(vw), Hq // Hkv, axis=1)
+    att = np.ones((B, Hq, L, S))
+    if causal:
+        att = att * np.tril(np.ones((L, S)))
+    if mask is not None:
+        att = att * np.isfinite(mask)
+    return att @ av
 
 
 def _run(tn, dtype, q, k, v, causal, threads=16):
     """GPU result plus the oracle's f32 and f64 answers on the same inputs."""
     B, Hq, L, D = q.shape
-    if dtype == "bfloat16":
-        qb, kb, vb = (tn.tensor(a.astype(np.float32), dtype="bfloat16", device="hip") for a in (q, k, v))
-        qw, kw, vw = (t.numpy().astype(np.float64) for t in (qb, kb, vb))  # exact widening
-        o, lse = tn._aten_dispatch(OP, qb, kb, vb, 0.0, causal)
-    else:
-        qw, kw, vw = (a.astype(np.float32).astype(np.float64) for a in (q, k, v))
-        o, lse = tn._aten_dispatch(OP, *(tn.tensor(a.astype(np.float32), device="hip") for a in (q, k, v)), 0.0,
-                                   causal)
+    qb, kb, vb = (_dev(tn, dtype, a) for a in (q, k, v))
+    qw, kw, vw = (t.numpy().astype(np.float64) for t in (qb, kb, vb))  # exact widening
+    o, lse = tn._aten_dispatch(OP, qb, kb, vb, 0.0, causal)
     r32, l32 = O.sdpa(qw, kw, vw, is_causal=causal, threads=threads)
     r64, l64 = O.sdpa(qw, kw, vw, is_causal=causal, threads=threads, dtype=np.float64)
-    pav = None
-    if dtype == "bfloat16":
+    pav = vsum = None
+    if dtype != "float32":
         pav, _ = O.sdpa(qw, kw, np.abs(vw), is_causal=causal, threads=threads, dtype=np.float64)
-    return o, lse, (r32, l32, r64, l64, pav)
+    if dtype == "float16":
+        vsum = _vsum(vw, Hq, L, causal)
+    return o, lse, (r32, l32, r64, l64, pav, vsum)
 
 
 def _check(tn, dtype, q, k, v, causal):
-    o, lse, (r32, l32, r64, l64, pav) = _run(tn, dtype, q, k, v, causal)
+    o, lse, (r32, l32, r64, l64, pav, vsum) = _run(tn, dtype, q, k, v, causal)
     got = o.numpy().astype(np.float64)
-    if dtype == "bfloat16":
-        ref = O.bf16_to_f32(O.bf16_from_f32(r32)).astype(np.float64)
-        tol = _bound(r32, r64, pav, bf16=True, got=got)
-    else:
-        ref = r32.astype(np.float64)
-        tol = _bound(r32, r64)
+    ref = _narrow(dtype, r32)
+    tol = _bound(r32, r64, pav, got=got, kind=dtype, vsum=vsum) if dtype != "float32" else _bound(r32, r64)
     err = np.abs(got - ref)
     assert np.all(np.isfinite(got))
     worst = float(np.max(err / tol))
@@ -86,7 +110,7 @@ SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("shape", SHAPES)
 def test_sdpa_matches_the_oracle_within_the_derived_bound(tn, shape, causal, dtype):
@@ -95,7 +119,7 @@ def test_sdpa_matches_the_oracle_within_the_derived_bound(tn, shape, causal, dty
     _check(tn, dtype, q, k, v, causal)
 
 
-@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
 def test_config2_causal_gqa_prefill_at_full_size(tn, dtype):
     """B=1, 9 q heads / 3 kv heads, D=64, S=2048, causal,
     Q/K/V ~ N(0,1), scale 1/8."""
@@ -230,11 +254,8 @@ def _check_masked(tn, dtype, q, k, v, mask, mask_dtype, causal=False, nan_rows=(
     in out and lse, as the reference's are (aten.rs:10392-10420)."""
     B, Hq, L, D = q.shape
     S = k.shape[2]
-    if dtype == "bfloat16":
-        qt, kt, vt = (tn.tensor(a.astype(np.float32), dtype="bfloat16", device="hip") for a in (q, k, v))
-    else:
-        qt, kt, vt = (tn.tensor(a.astype(np.float32), device="hip") for a in (q, k, v))
-    mt = tn.tensor(mask.astype(np.float32), dtype=mask_dtype, device="hip")
+    qt, kt, vt = (_dev(tn, dtype, a) for a in (q, k, v))
+    mt = _dev(tn, mask_dtype, mask)
     o, lse = tn._aten_dispatch(OP, qt, kt, vt, 0.0, causal, attn_mask=mt)
     qw, kw, vw = (t.numpy().astype(np.float64) for t in (qt, kt, vt))
     mw = np.ascontiguousarray(np.broadcast_to(mt.numpy().astype(np.float64), (B, Hq, L, S)))
@@ -242,7 +263,8 @@ def _check_masked(tn, dtype, q, k, v, mask, mask_dtype, causal=False, nan_rows=(
         r32, l32 = O.sdpa(qw, kw, vw, mask=mw, is_causal=causal, threads=16)
         r64, l64 = O.sdpa(qw, kw, vw, mask=mw, is_causal=causal, threads=16, dtype=np.float64)
         pav = O.sdpa(qw, kw, np.abs(vw), mask=mw, is_causal=causal, threads=16, dtype=np.float64)[0] \
-            if dtype == "bfloat16" else None
+            if dtype != "float32" else None
+    vsum = _vsum(vw, Hq, L, causal, mw) if dtype == "float16" else None
     got, gl = o.numpy().astype(np.float64), lse.numpy().astype(np.float64)
     nan = np.zeros((B, Hq, L), bool)
     for (b, h, i) in nan_rows:
@@ -250,11 +272,11 @@ def _check_masked(tn, dtype, q, k, v, mask, mask_dtype, causal=False, nan_rows=(
     assert np.array_equal(np.isnan(got).any(axis=-1), nan) and np.all(np.isnan(got[nan]))
     assert np.array_equal(np.isnan(gl), nan)
     keep = ~nan
-    if dtype == "bfloat16":
-        ref = O.bf16_to_f32(O.bf16_from_f32(r32)).astype(np.float64)
-        tol = _bound(r32[keep], r64[keep], pav[keep], bf16=True, got=got[keep])
+    ref = _narrow(dtype, r32)
+    if dtype != "float32":
+        tol = _bound(r32[keep], r64[keep], pav[keep], got=got[keep], kind=dtype,
+                     vsum=vsum[keep] if vsum is not None else None)
     else:
-        ref = r32.astype(np.float64)
         tol = _bound(r32[keep], r64[keep])
     worst = float(np.max(np.abs(got[keep] - ref[keep]) / tol))
     assert worst <= 1.0, f"{dtype} mask {mask_dtype} causal={causal}: {worst:.3g}x the bound"
@@ -264,7 +286,8 @@ def _check_masked(tn, dtype, q, k, v, mask, mask_dtype, causal=False, nan_rows=(
 
 @pytest.mark.parametrize("dtype,mask_dtype,D,causal", [
     ("bfloat16", "float32", 64, False), ("bfloat16", "bfloat16", 64, True), ("bfloat16", "float32", 128, True),
-    ("float32", "float32", 64, True), ("float32", "float32", 128, False)])
+    ("float32", "float32", 64, True), ("float32", "float32", 128, False),
+    ("float16", "float16", 64, True), ("float16", "float32", 128, False)])
 def test_additive_mask_within_the_derived_bound(tn, dtype, mask_dtype, D, causal):
     rng = np.random.default_rng(D + int(causal))
     B, Hq, Hkv, L, S = 2, 4, 2, 70, 90
@@ -294,6 +317,28 @@ def test_mask_on_split_rows_merged_in_kernel(tn):
     mask = rng.standard_normal((B, Hq, L, S))
     mask[:, :, :, 1024:1500] = -np.inf
     _check_masked(tn, "bfloat16", q, k, v, mask, "bfloat16")
+
+
+def test_f16_split_rows_with_an_f16_mask_and_a_fully_masked_row(tn):
+    """float16 through the in-kernel merge of split rows, with a float16 mask
+    that leaves one row with no key (NaN) and takes most of another."""
+    rng = np.random.default_rng(31)
+    B, Hq, Hkv, L, S, D = 1, 4, 2, 96, 2048, 128
+    q, k, v = (rng.standard_normal(s) for s in ((B, Hq, L, D), (B, Hkv, S, D), (B, Hkv, S, D)))
+    mask = rng.standard_normal((B, Hq, L, S))
+    mask[:, :, 40, :] = -np.inf
+    mask[:, :, 41, 3:] = -np.inf
+    _check_masked(tn, "float16", q, k, v, mask, "float16", nan_rows=[(0, h, 40) for h in range(Hq)])
+
+
+def test_f16_large_values_narrow_without_overflow(tn):
+    """Inputs near f16's range: scores are formed in f32 (no overflow), the
+    output lands in range and is narrowed RNE."""
+    rng = np.random.default_rng(32)
+    q = rng.standard_normal((1, 2, 64, 64)) * 200.0
+    k = rng.standard_normal((1, 2, 64, 64)) * 200.0
+    v = rng.standard_normal((1, 2, 64, 64)) * 3000.0
+    _check(tn, "float16", q, k, v, True)
 
 
 def test_mask_dtype_rule(tn):

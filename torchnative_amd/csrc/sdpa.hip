@@ -60,6 +60,39 @@ __device__ inline uint32_t pack2_bf16(float a, float b) {
 }
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// The 16-bit storage formats of the prefill kernel: bf16 or f16 inputs, the
+// f32-accumulating MFMA of that type, the narrowing of the probabilities to
+// it between the two products, and the narrowing of the output (RNE; f16 with
+// subnormals and overflow to inf, bf16 with NaN quieted).
+template <bool F16>
+struct El;
+template <>
+struct El<false> {
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    static __device__ inline f32x16 mfma(v8 a, v8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ inline uint32_t pack_p(float a, float b) { return pack2_bf16_hw(a, b); }
+    static __device__ inline uint32_t pack_out(float a, float b) { return pack2_bf16(a, b); }
+    static __device__ inline float widen(uint16_t h) { return bf16_to_f32(h); }
+};
+template <>
+struct El<true> {
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    static __device__ inline f32x16 mfma(v8 a, v8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    // v_cvt_f16_f32 rounds to nearest even (equal to f16_from_f32 for every float)
+    static __device__ inline uint32_t pack_p(float a, float b) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, v2));
+    }
+    static __device__ inline uint32_t pack_out(float a, float b) {
+        return (uint32_t)f16_from_f32(a) | ((uint32_t)f16_from_f32(b) << 16);
+    }
+    static __device__ inline float widen(uint16_t h) { return f16_to_f32(h); }
+};
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
@@ -153,7 +186,7 @@ __device__ inline float max3f(float a, float b, float c) {
 // No fence is needed: only the partials cross workgroups, and they never sit
 // in a non-coherent cache. The partial stride is nsplit (the launch's
 // maximum); rows of the block are contiguous from `row0`.
-template <int D>
+template <int D, bool F16>
 __device__ __attribute__((always_inline)) inline void merge_split_rows(float* part_o, float2* part_ml, uint32_t* tickets, int nsplit,
                                               int split, int ns, int64_t row0, int nrows, int64_t ticket,
                                               bool holder, int r, int hh, const f32x16 (&o)[D / 32], float m,
@@ -233,7 +266,7 @@ __device__ __attribute__((always_inline)) inline void merge_split_rows(float* pa
         const float inv = 1.0f / tl;
         const int64_t row = row0 + rr;
         *reinterpret_cast<uint2*>(Og + row * D + c4) =
-            make_uint2(pack2_bf16(a0 * inv, a1 * inv), pack2_bf16(a2 * inv, a3 * inv));
+            make_uint2(El<F16>::pack_out(a0 * inv, a1 * inv), El<F16>::pack_out(a2 * inv, a3 * inv));
         if (lse && c4 == 0) lse[row] = mm == -INFINITY ? NAN : mu * LN2 + logf(tl);  // a fully masked row is NaN (aten.rs:10392-10420)
     }
 #endif
@@ -272,8 +305,8 @@ struct FlashWork {
 
 // MASK: 0 none; 1 an f32 additive mask; 2 a bf16 one, dense [B, Hq, L, S]
 // (aten.rs:10383-10389: added to the scaled scores before the row maximum)
-template <int D, int MASK = 0>
-__global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
+template <int D, int MASK = 0, bool F16 = false>
+__global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash16(
     const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kg, const uint16_t* __restrict__ Vg, int Hq,
     int Hkv, int L, int S, float sl2, int causal, const FlashWork work, int nsplit, uint16_t* __restrict__ Og,
     float* __restrict__ lse, float* __restrict__ part_o, float2* __restrict__ part_ml, uint32_t* __restrict__ tickets,
@@ -331,12 +364,14 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
     // depends on r mod 16 only, so a tile's rows and the stage's rows agree)
     auto swz = [](int r, int c) { return D == 64 ? (c ^ ((r >> 1) & 7)) : (c ^ (r & 15)); };
 
-    bf16x8 qf[D / 16];
+    using E = El<F16>;
+    using V8 = typename E::v8;
+    V8 qf[D / 16];
 #pragma unroll
     for (int c = 0; c < D / 16; c++) {
         uint4 v = make_uint4(0, 0, 0, 0);
         if (qi < L) v = *reinterpret_cast<const uint4*>(qp + (int64_t)qi * D + 16 * c + 8 * hh);
-        qf[c] = __builtin_bit_cast(bf16x8, v);
+        qf[c] = __builtin_bit_cast(V8, v);
     }
 
     // this lane's byte offset in a stage for its i-th 16-byte load: LDS
@@ -406,8 +441,8 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
             const int row = kr + 32 * s2 + lq;
 #pragma unroll
             for (int c = 0; c < D / 16; c++) {
-                const bf16x8 ka = *reinterpret_cast<const bf16x8*>(tK + row * D + swz(row, 2 * c + hh) * 8);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[c], acc, 0, 0, 0);
+                const V8 ka = *reinterpret_cast<const V8*>(tK + row * D + swz(row, 2 * c + hh) * 8);
+                acc = E::mfma(ka, qf[c], acc);
             }
 #pragma unroll
             for (int r = 0; r < 16; r++) sv[s2][r] = acc[r];
@@ -436,7 +471,7 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
                             if constexpr (MASK == 1)
                                 mv = reinterpret_cast<const float*>(mask)[mrow + key];
                             else
-                                mv = bf16_to_f32(reinterpret_cast<const uint16_t*>(mask)[mrow + key]);
+                                mv = E::widen(reinterpret_cast<const uint16_t*>(mask)[mrow + key]);
                         }
                         v[r] = v[r] * sl2 + mv * LOG2E;
                     }
@@ -476,13 +511,12 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
 #pragma unroll
             for (int r = 0; r < 16; r += 4) ps = ps + ((p[r] + p[r + 1]) + (p[r + 2] + p[r + 3]));
             l = l + ps;
-            bf16x8 pf[2];
+            V8 pf[2];
 #pragma unroll
             for (int j = 0; j < 2; j++)
                 pf[j] = __builtin_bit_cast(
-                    bf16x8, make_uint4(pack2_bf16_hw(p[8 * j], p[8 * j + 1]), pack2_bf16_hw(p[8 * j + 2], p[8 * j + 3]),
-                                       pack2_bf16_hw(p[8 * j + 4], p[8 * j + 5]),
-                                       pack2_bf16_hw(p[8 * j + 6], p[8 * j + 7])));
+                    V8, make_uint4(E::pack_p(p[8 * j], p[8 * j + 1]), E::pack_p(p[8 * j + 2], p[8 * j + 3]),
+                                   E::pack_p(p[8 * j + 4], p[8 * j + 5]), E::pack_p(p[8 * j + 6], p[8 * j + 7])));
 #pragma unroll
             for (int dt = 0; dt < D / 32; dt++) {
 #pragma unroll
@@ -492,8 +526,8 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
                     const int col = 32 * dt + dcol;
                     const uint2 lo = lds_read_tr16(tV + r0 * D + swz(r0, col >> 3) * 8 + (col & 7));
                     const uint2 hi = lds_read_tr16(tV + r1 * D + swz(r1, col >> 3) * 8 + (col & 7));
-                    const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[j], o[dt], 0, 0, 0);
+                    const V8 va = __builtin_bit_cast(V8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    o[dt] = E::mfma(va, pf[j], o[dt]);
                 }
             }
         }
@@ -548,7 +582,7 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
     }
     const int64_t row = ((int64_t)b * Hq + h) * L + qi;
     if (nsplit_row > 1) {
-        merge_split_rows<D>(part_o, part_ml, tickets, nsplit, split, nsplit_row, (int64_t)bh * L + q0,
+        merge_split_rows<D, F16>(part_o, part_ml, tickets, nsplit, split, nsplit_row, (int64_t)bh * L + q0,
                             min(F3_BQ, L - q0), bh * nqb + qt, kg == 0 && qi < L, qi - q0, hh, o, m, l, Og, lse,
                             s_ticket);
         return;
@@ -562,8 +596,8 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash_bf16(
         for (int g4 = 0; g4 < 4; g4++)
             // O^T[d = 32dt + 8g4 + 4hh + e][q = lq]
             *reinterpret_cast<uint2*>(op + 32 * dt + 8 * g4 + 4 * hh) =
-                make_uint2(pack2_bf16(o[dt][4 * g4] * inv, o[dt][4 * g4 + 1] * inv),
-                           pack2_bf16(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv));
+                make_uint2(E::pack_out(o[dt][4 * g4] * inv, o[dt][4 * g4 + 1] * inv),
+                           E::pack_out(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv));
     if (lse && hh == 0) lse[row] = m == -INFINITY ? NAN : m * LN2 + logf(l);
 }
 
@@ -1933,11 +1967,11 @@ extern "C" {
 tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, const void* v, int64_t B, int64_t Hq,
                       int64_t Hkv, int64_t L, int64_t S, int64_t D, const void* attn_mask, int mask_dtype,
                       int is_causal, double scale, void* out, float* lse) {
-    if (dtype != TN_F32 && dtype != TN_BF16) {
-        const char* name = dtype == TN_F16 ? "Half" : dtype == TN_F64 ? "Double" : "an unknown type";
-        return fail(dtype == TN_F16 || dtype == TN_F64 ? TN_ENOTIMPL : TN_EINVAL,
+    if (dtype != TN_F32 && dtype != TN_BF16 && dtype != TN_F16) {
+        const char* name = dtype == TN_F64 ? "Double" : "an unknown type";
+        return fail(dtype == TN_F64 ? TN_ENOTIMPL : TN_EINVAL,
                     std::string("scaled_dot_product_attention_flash_attention: ") + name +
-                        " is not implemented on the hip device (float32 and bfloat16 are)");
+                        " is not implemented on the hip device (float32, bfloat16 and float16 are)");
     }
     if (B < 0 || Hq < 0 || L < 0 || S < 0 || D < 0 || Hkv < 0)
         return fail(TN_EINVAL, std::string(OP) + ": negative dimension");
@@ -1976,13 +2010,13 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     hipStream_t st = (hipStream_t)stream;
     const int c = is_causal ? 1 : 0;
     const int64_t rows = B * Hq * L;
-    if (dtype == TN_BF16) {
+    if (dtype == TN_BF16 || dtype == TN_F16) {
         // the key/value buffer descriptors cover one head's S*D elements
         if (S * D * 2 > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": key length too large");
         // resident workgroups of the prefill kernel: the slots the schedule is planned over
         int slots = 0;
-        tn_status sp = resident_workgroups(D == 64 ? reinterpret_cast<const void*>(&k_flash_bf16<64>)
-                                                    : reinterpret_cast<const void*>(&k_flash_bf16<128>),
+        tn_status sp = resident_workgroups(D == 64 ? reinterpret_cast<const void*>(&k_flash16<64>)
+                                                    : reinterpret_cast<const void*>(&k_flash16<128>),
                                            128 * FlashCfg<64>::KG, 0, &slots);
         if (sp != TN_OK) return sp;
         Plan plan;
@@ -2014,19 +2048,23 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         auto vv = static_cast<const uint16_t*>(v);
         auto oo = static_cast<uint16_t*>(out);
         // split rows are merged inside the kernel (merge_split_rows)
-#define TN_FLASH(DD, MK)                                                                                            \
-    hipLaunchKernelGGL((k_flash_bf16<DD, MK>), dim3((unsigned)nitems), dim3(128 * FlashCfg<DD>::KG), 0, st, qq, kk, \
+#define TN_FLASH(DD, MK, H)                                                                                      \
+    hipLaunchKernelGGL((k_flash16<DD, MK, H>), dim3((unsigned)nitems), dim3(128 * FlashCfg<DD>::KG), 0, st, qq, kk, \
                        vv, (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, work, nsplit, oo, lse, part_o, part_ml, tick,   \
                        attn_mask)
+#define TN_FLASH_MK(DD, H)              \
+    do {                                \
+        if (mk == 0) TN_FLASH(DD, 0, H); \
+        else if (mk == 1) TN_FLASH(DD, 1, H); \
+        else TN_FLASH(DD, 2, H);        \
+    } while (0)
+        const bool h16 = dtype == TN_F16;
         if (D == 64) {
-            if (mk == 0) TN_FLASH(64, 0);
-            else if (mk == 1) TN_FLASH(64, 1);
-            else TN_FLASH(64, 2);
+            if (h16) TN_FLASH_MK(64, true); else TN_FLASH_MK(64, false);
         } else {
-            if (mk == 0) TN_FLASH(128, 0);
-            else if (mk == 1) TN_FLASH(128, 1);
-            else TN_FLASH(128, 2);
+            if (h16) TN_FLASH_MK(128, true); else TN_FLASH_MK(128, false);
         }
+#undef TN_FLASH_MK
 #undef TN_FLASH
         TN_LAUNCHED();
         return TN_OK;
