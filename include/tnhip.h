@@ -215,7 +215,9 @@ tn_status tn_q4_k_linear(void* stream, const void* x, int x_dtype, int64_t m, in
  * f32, aten.rs:10196-10213); a bf16 or f16 run narrows the probabilities to
  * its dtype between the two products, as upstream's blocked kernel does
  * (flash.rs:503-516), and the output RNE.
- * Head dims 64 and 128 run; others are refused by name. */
+ * Head dims 64 and 128 with scale >= 0 run on MFMA kernels; any other head
+ * dim up to 256, or a negative scale, runs on a plain f32 kernel (f32
+ * probabilities); a head dim past 256 is refused by name. */
 tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, const void* v,
                       int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t S, int64_t D,
                       const void* attn_mask, int mask_dtype, int is_causal, double scale,

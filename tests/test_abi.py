@@ -91,7 +91,7 @@ def test_sdpa_refusals_name_the_reason(L):
         return L.tn_sdpa_fwd(None, dtype, None, None, None, a["B"], a["Hq"], a["Hkv"], a["L"], a["S"], a["D"],
                              mask, mask_dtype, 1, float("nan"), None, None)
 
-    assert call(D=16) == _lib.TN_ENOTIMPL and "head_dim 16" in _lib.last_error()
+    assert call(D=272) == _lib.TN_ENOTIMPL and "head_dim 272" in _lib.last_error()
     assert call(Hkv=4) == _lib.TN_ENOTIMPL and "do not divide" in _lib.last_error()
     assert call(S=0) == _lib.TN_ENOTIMPL and "zero key length" in _lib.last_error()
     assert call(dtype=_lib.TN_F64) == _lib.TN_ENOTIMPL and "Double" in _lib.last_error()

@@ -67,24 +67,24 @@ def _vsum(vw, Hq, L, causal, mask=None):
     return att @ av
 
 
-def _run(tn, dtype, q, k, v, causal, threads=16):
+def _run(tn, dtype, q, k, v, causal, threads=16, scale=None):
     """GPU result plus the oracle's f32 and f64 answers on the same inputs."""
     B, Hq, L, D = q.shape
     qb, kb, vb = (_dev(tn, dtype, a) for a in (q, k, v))
     qw, kw, vw = (t.numpy().astype(np.float64) for t in (qb, kb, vb))  # exact widening
-    o, lse = tn._aten_dispatch(OP, qb, kb, vb, 0.0, causal)
-    r32, l32 = O.sdpa(qw, kw, vw, is_causal=causal, threads=threads)
-    r64, l64 = O.sdpa(qw, kw, vw, is_causal=causal, threads=threads, dtype=np.float64)
+    o, lse = tn._aten_dispatch(OP, qb, kb, vb, 0.0, causal, scale=scale)
+    r32, l32 = O.sdpa(qw, kw, vw, is_causal=causal, scale=scale, threads=threads)
+    r64, l64 = O.sdpa(qw, kw, vw, is_causal=causal, scale=scale, threads=threads, dtype=np.float64)
     pav = vsum = None
     if dtype != "float32":
-        pav, _ = O.sdpa(qw, kw, np.abs(vw), is_causal=causal, threads=threads, dtype=np.float64)
+        pav, _ = O.sdpa(qw, kw, np.abs(vw), is_causal=causal, scale=scale, threads=threads, dtype=np.float64)
     if dtype == "float16":
         vsum = _vsum(vw, Hq, L, causal)
     return o, lse, (r32, l32, r64, l64, pav, vsum)
 
 
-def _check(tn, dtype, q, k, v, causal):
-    o, lse, (r32, l32, r64, l64, pav, vsum) = _run(tn, dtype, q, k, v, causal)
+def _check(tn, dtype, q, k, v, causal, scale=None):
+    o, lse, (r32, l32, r64, l64, pav, vsum) = _run(tn, dtype, q, k, v, causal, scale=scale)
     got = o.numpy().astype(np.float64)
     ref = _narrow(dtype, r32)
     tol = _bound(r32, r64, pav, got=got, kind=dtype, vsum=vsum) if dtype != "float32" else _bound(r32, r64)
@@ -140,13 +140,41 @@ def test_default_scale_and_explicit_scale_agree(tn):
     assert np.array_equal(a.numpy(), b.numpy()) and np.array_equal(la.numpy(), lb.numpy())
 
 
-def test_negative_scale_is_refused_by_name(tn):
-    """The prefill kernels take the row maximum of the unscaled scores, right
-    only for scale >= 0; a negative scale refuses instead of returning wrong
-    numbers."""
-    q = tn.tensor(np.ones((1, 1, 4, 64), np.float32), device="hip")
-    with pytest.raises(NotImplementedError, match="negative scale"):
-        tn._aten_dispatch(OP, q, q, q, 0.0, False, scale=-0.125)
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+def test_negative_scale_runs_on_the_plain_kernel(tn, dtype):
+    """The MFMA kernels take the row maximum of the unscaled scores, right
+    only for scale >= 0; a negative scale runs on the plain kernel, whose
+    maximum is over the scaled scores."""
+    q, k, v = _det((1, 4, 70, 64), 41), _det((1, 2, 90, 64), 42), _det((1, 2, 90, 64), 43)
+    _check(tn, dtype, q, k, v, True, scale=-0.125)
+    _check(tn, dtype, q, k, v, False, scale=-0.3)
+
+
+ANY_SHAPES = [
+    # head dims the MFMA kernels do not take: the plain kernel
+    (1, 4, 2, 40, 70, 32),
+    (2, 3, 1, 33, 50, 80),
+    (1, 6, 3, 17, 29, 72),
+    (1, 2, 2, 100, 300, 96),
+    (1, 2, 1, 20, 45, 256),
+    (1, 2, 2, 7, 9, 1),
+    (1, 3, 3, 70, 70, 200),
+]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", ANY_SHAPES)
+def test_other_head_dims_match_the_oracle(tn, shape, causal, dtype):
+    b, hq, hkv, l, s, d = shape
+    q, k, v = _det((b, hq, l, d), 4), _det((b, hkv, s, d), 5), _det((b, hkv, s, d), 6)
+    _check(tn, dtype, q, k, v, causal)
+
+
+def test_head_dim_past_256_is_refused_by_name(tn):
+    q = tn.tensor(np.ones((1, 1, 4, 264), np.float32), device="hip")
+    with pytest.raises(NotImplementedError, match="head_dim 264"):
+        tn._aten_dispatch(OP, q, q, q, 0.0, False)
 
 
 def test_gqa_is_indexed_not_tiled(tn):
@@ -287,7 +315,8 @@ def _check_masked(tn, dtype, q, k, v, mask, mask_dtype, causal=False, nan_rows=(
 @pytest.mark.parametrize("dtype,mask_dtype,D,causal", [
     ("bfloat16", "float32", 64, False), ("bfloat16", "bfloat16", 64, True), ("bfloat16", "float32", 128, True),
     ("float32", "float32", 64, True), ("float32", "float32", 128, False),
-    ("float16", "float16", 64, True), ("float16", "float32", 128, False)])
+    ("float16", "float16", 64, True), ("float16", "float32", 128, False),
+    ("float16", "float16", 80, False), ("bfloat16", "float32", 96, True), ("float32", "float32", 32, False)])
 def test_additive_mask_within_the_derived_bound(tn, dtype, mask_dtype, D, causal):
     rng = np.random.default_rng(D + int(causal))
     B, Hq, Hkv, L, S = 2, 4, 2, 70, 90

@@ -601,6 +601,127 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash16(
     if (lse && hh == 0) lse[row] = m == -INFINITY ? NAN : m * LN2 + logf(l);
 }
 
+// ---------------------------------------------------------------------------
+// Any head dimension up to ANY_DMAX other than the MFMA kernels' 64 and 128,
+// and a scale of either sign: a plain f32 kernel for every input dtype.
+// Workgroup = 256 threads over ANY_BQ = 32 queries of one (batch, head): thread
+// (row r = tid / 8, lane t = tid % 8) scores keys t, t + 8, t + 16, t + 24 of
+// each 32-key tile with a sequential f32 dot over d, and accumulates output
+// columns t, t + 8, ... of its row. K and V tiles are widened to f32 into
+// LDS; the row's eight threads share max and sum by shuffles and the row's
+// probabilities through LDS. Online softmax in log2 units over the scaled
+// scores (so the scale's sign does not matter); probabilities stay f32; the
+// output is narrowed RNE to the input dtype.
+// ---------------------------------------------------------------------------
+constexpr int ANY_DMAX = 256, ANY_BQ = 32, ANY_BK = 32;
+
+template <int ET>  // 0 f32, 1 bf16, 2 f16
+__device__ inline float any_load(const void* p, int64_t i) {
+    if constexpr (ET == 0) return reinterpret_cast<const float*>(p)[i];
+    else if constexpr (ET == 1) return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    else return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+template <int ET>
+__device__ inline void any_store(void* p, int64_t i, float v) {
+    if constexpr (ET == 0) reinterpret_cast<float*>(p)[i] = v;
+    else if constexpr (ET == 1) reinterpret_cast<uint16_t*>(p)[i] = bf16_from_f32(v);
+    else reinterpret_cast<uint16_t*>(p)[i] = f16_from_f32(v);
+}
+
+// MASK: 0 none; 1 f32; 2 the query's dtype; dense [B, Hq, L, S]
+template <int ET, int MASK>
+__global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, const void* __restrict__ Kg,
+                                                  const void* __restrict__ Vg, int Hq, int Hkv, int L, int S, int D,
+                                                  float sl2, int causal, void* __restrict__ Og,
+                                                  float* __restrict__ lse, const void* __restrict__ mask) {
+    __shared__ float sQ[ANY_BQ * ANY_DMAX];
+    __shared__ float sK[ANY_BK * (ANY_DMAX + 1)];  // rows padded by one word: the 8 keys a row reads at one d
+    __shared__ float sV[ANY_BK * ANY_DMAX];        // sit in 8 different banks
+    __shared__ float sP[ANY_BQ][ANY_BK];
+    const int tid = threadIdx.x, r = tid >> 3, t = tid & 7;
+    const int q0 = blockIdx.x * ANY_BQ, h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / (Hq / Hkv);
+    const int qi = q0 + r;
+    const int64_t bh = (int64_t)b * Hq + h;
+    const int64_t qbase = bh * L * D;
+    const int64_t kbase = ((int64_t)b * Hkv + kvh) * S * D;
+    const int KP = D + 1;
+    for (int e = tid; e < ANY_BQ * D; e += 256) {
+        const int rr = e / D, d = e - rr * D;
+        sQ[rr * D + d] = q0 + rr < L ? any_load<ET>(Qg, qbase + (int64_t)(q0 + rr) * D + d) : 0.0f;
+    }
+    constexpr int NC = ANY_DMAX / 8;  // output columns per thread, at most
+    float o[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) o[c] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    const int kend = causal ? min(S, q0 + ANY_BQ) : S;
+    for (int k0 = 0; k0 < kend; k0 += ANY_BK) {
+        __syncthreads();  // the previous tile's reads are done
+        for (int e = tid; e < ANY_BK * D; e += 256) {
+            const int j = e / D, d = e - j * D;
+            const bool in = k0 + j < S;
+            sK[j * KP + d] = in ? any_load<ET>(Kg, kbase + (int64_t)(k0 + j) * D + d) : 0.0f;
+            sV[j * D + d] = in ? any_load<ET>(Vg, kbase + (int64_t)(k0 + j) * D + d) : 0.0f;
+        }
+        __syncthreads();
+        float s[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int j = t + 8 * i, key = k0 + j;
+            float acc = 0.0f;
+            for (int d = 0; d < D; d++) acc = acc + sQ[r * D + d] * sK[j * KP + d];
+            float v = acc * sl2;
+            if constexpr (MASK == 1) {
+                if (qi < L && key < S) v = v + reinterpret_cast<const float*>(mask)[(bh * L + qi) * S + key] * LOG2E;
+            } else if constexpr (MASK == 2) {
+                if (qi < L && key < S) v = v + any_load<ET>(mask, (bh * L + qi) * S + key) * LOG2E;
+            }
+            if (key >= S || (causal && key > qi)) v = -INFINITY;
+            s[i] = v;
+            mx = fmaxf(mx, v);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 1));
+        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        mx = fmaxf(mx, __shfl_xor(mx, 4));
+        const float mn = fmaxf(m, mx);
+        const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+        const float mu = mn == -INFINITY ? 0.0f : mn;
+        float ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float p = exp2f(s[i] - mu);
+            sP[r][t + 8 * i] = p;
+            ps = ps + p;
+        }
+        ps = ps + __shfl_xor(ps, 1);
+        ps = ps + __shfl_xor(ps, 2);
+        ps = ps + __shfl_xor(ps, 4);
+        l = l * alpha + ps;
+        m = mn;
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int d = t + 8 * c;
+            if (d < D) {
+                float acc = o[c] * alpha;
+                for (int j = 0; j < ANY_BK; j++) acc = acc + sP[r][j] * sV[j * D + d];
+                o[c] = acc;
+            }
+        }
+    }
+    if (qi >= L) return;
+    const float inv = 1.0f / l;  // a row with no key: 0 * inf = NaN, as the reference's (aten.rs:10392-10420)
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int d = t + 8 * c;
+        if (d < D) any_store<ET>(Og, qbase + (int64_t)qi * D + d, o[c] * inv);
+    }
+    if (lse && t == 0) lse[bh * L + qi] = m == -INFINITY ? NAN : m * LN2 + logf(l);
+}
+
 constexpr int PF_BQ = 64, PF_BK = 64;
 
 
@@ -1824,7 +1945,7 @@ tn_status decode_sk_launch(hipStream_t st, const void* q, const void* k_cache, c
 tn_status refuse_head_dim(int64_t D) {
     char buf[256];
     std::snprintf(buf, sizeof buf,
-                  "%s: head_dim %lld is not implemented on the hip device (kernels exist for 64 and 128)", OP,
+                  "%s: head_dim %lld is not implemented on the hip device (kernels exist up to 256)", OP,
                   (long long)D);
     return fail(TN_ENOTIMPL, buf);
 }
@@ -1998,9 +2119,7 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
                                "as query");
     // 0 none, 1 f32, 2 bf16: the kernels' MASK parameter
     const int mk = !attn_mask ? 0 : mask_dtype == TN_F32 ? 1 : 2;
-    if (D != 64 && D != 128) return refuse_head_dim(D);
-    // the kernels take the row maximum before scaling, which needs scale >= 0
-    if (scale < 0.0) return fail(TN_ENOTIMPL, std::string(OP) + ": a negative scale is not implemented on the hip device");
+    if (D > ANY_DMAX) return refuse_head_dim(D);
     if (B * Hq * L == 0) return TN_OK;  // nothing to write (aten.rs:10242-10259 returns empty zeros)
     if (!q || !k || !v || !out) return fail(TN_EVALUE, std::string(OP) + ": null pointer");
     if (L > INT32_MAX || S > INT32_MAX || Hq > 65535 || B > 65535)
@@ -2010,6 +2129,29 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     hipStream_t st = (hipStream_t)stream;
     const int c = is_causal ? 1 : 0;
     const int64_t rows = B * Hq * L;
+    // the MFMA kernels take the row maximum of the unscaled scores (right for
+    // scale >= 0) and exist for head dims 64 and 128; anything else runs on
+    // the plain kernel
+    if ((D != 64 && D != 128) || sc < 0.0) {
+        const dim3 grid((unsigned)cdiv(L, ANY_BQ), (unsigned)Hq, (unsigned)B);
+        const int et = dtype == TN_F32 ? 0 : dtype == TN_BF16 ? 1 : 2;
+#define TN_ANY(ET, MK)                                                                                            \
+    hipLaunchKernelGGL((k_attn_any<ET, MK>), grid, dim3(256), 0, st, q, k, v, (int)Hq, (int)Hkv, (int)L, (int)S, \
+                       (int)D, sl2, c, out, lse, attn_mask)
+#define TN_ANY_MK(ET)                     \
+    do {                                  \
+        if (mk == 0) TN_ANY(ET, 0);       \
+        else if (mk == 1) TN_ANY(ET, 1);  \
+        else TN_ANY(ET, 2);               \
+    } while (0)
+        if (et == 0) TN_ANY_MK(0);
+        else if (et == 1) TN_ANY_MK(1);
+        else TN_ANY_MK(2);
+#undef TN_ANY_MK
+#undef TN_ANY
+        TN_LAUNCHED();
+        return TN_OK;
+    }
     if (dtype == TN_BF16 || dtype == TN_F16) {
         // the key/value buffer descriptors cover one head's S*D elements
         if (S * D * 2 > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": key length too large");
