@@ -229,8 +229,9 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
  * [B, Hkv, cap, D] with head stride cap*D, sequence b using keys 0..lens[b]-1.
  * Equals tn_sdpa_fwd with L = 1, non-causal, on the view k[:, :, :lens[b]]
  * (the reference passes attn_mask=None at L=1, sdpa_metal.rs:23-30).
- *   q [B, Hq, D], out [B, Hq, D] and the caches in `dtype` (TN_BF16, or
- *   TN_F32 for an f32 model); lens: device int32 [B], each in [1, cap];
+ *   q [B, Hq, D], out [B, Hq, D] and the caches in `dtype` (TN_BF16 or
+ *   TN_F16, or TN_F32 for an f32 model); lens: device int32 [B], each in
+ *   [1, cap];
  *   max_len: host upper bound of lens (sizes the split-KV grid);
  *   lse nullable f32 [B, Hq].
  * Split-KV with a combine pass; the partials live in the library workspace. */

@@ -192,22 +192,20 @@ def test_gqa_is_indexed_not_tiled(tn):
         assert np.array_equal(oh.numpy()[:, 0], full[:, h])
 
 
-def _decode_case(tn, B, Hq, Hkv, D, lens, cap, seed, max_len=None, scale=None):
-    """bf16 decode against the oracle per sequence; sequence b attends to keys
-    0 .. min(lens[b], max_len)-1 (a longer length is truncated at max_len)."""
+def _decode_case(tn, B, Hq, Hkv, D, lens, cap, seed, max_len=None, scale=None, dtype="bfloat16"):
+    """16-bit decode against the oracle per sequence; sequence b attends to
+    keys 0 .. min(lens[b], max_len)-1 (a longer length is truncated at max_len)."""
     rng = np.random.default_rng(seed)
     q = rng.standard_normal((B, Hq, D)).astype(np.float32)
     kc = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
     vc = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
-    qb = tn.tensor(q, dtype="bfloat16", device="hip")
-    kb = tn.tensor(kc, dtype="bfloat16", device="hip")
-    vb = tn.tensor(vc, dtype="bfloat16", device="hip")
+    qb, kb, vb = (_dev(tn, dtype, a) for a in (q, kc, vc))
     ln = tn.tensor(np.asarray(lens, np.int32), device="hip")
     max_len = max(lens) if max_len is None else max_len
     o, lse = tn.sdpa_decode(qb, kb, vb, ln, max_len, scale=scale)
     got = o.numpy().astype(np.float64)
     glse = lse.numpy().astype(np.float64)
-    qw, kw, vw = qb.numpy(), kb.numpy(), vb.numpy()
+    qw, kw, vw = (t.numpy().astype(np.float64) for t in (qb, kb, vb))
     worst = 0.0
     for b in range(B):
         L = min(lens[b], max_len)
@@ -218,8 +216,9 @@ def _decode_case(tn, B, Hq, Hkv, D, lens, cap, seed, max_len=None, scale=None):
         r32, l32 = O.sdpa(*args, scale=scale)
         r64, l64 = O.sdpa(*args, scale=scale, dtype=np.float64)
         pav, _ = O.sdpa(args[0], args[1], np.abs(args[2]), scale=scale, dtype=np.float64)
-        ref = O.bf16_to_f32(O.bf16_from_f32(r32)).astype(np.float64)
-        tol = _bound(r32, r64, pav, bf16=True, got=got[b:b + 1, :, None, :])
+        vsum = _vsum(args[2], Hq, 1, False) if dtype == "float16" else None
+        ref = _narrow(dtype, r32)
+        tol = _bound(r32, r64, pav, got=got[b:b + 1, :, None, :], kind=dtype, vsum=vsum)
         err = np.abs(got[b:b + 1, :, None, :] - ref)
         worst = max(worst, float(np.max(err / tol)))
         lt = _bound(l32, l64)
@@ -252,6 +251,19 @@ def test_decode_head_groups(tn, hq, hkv, d):
     """Query heads per kv head 8, 3, 1, 8 and 6 (groups of 8, 3, 1, 8 and 3 heads
     per wave)."""
     _decode_case(tn, 3, hq, hkv, d, [700, 33, 1500], 1536, 15 + hq)
+
+
+def test_decode_f16_caches(tn):
+    """float16 caches on both decode kernels: the stream-K one (ragged
+    lengths, head groups of 8 and 3, a negative scale) and the per-split one
+    (more than 1024 sequences), and BASELINE config 4's shape."""
+    _decode_case(tn, 3, 8, 2, 128, [1, 77, 300], 320, 51, dtype="float16")
+    _decode_case(tn, 2, 9, 3, 64, [129, 64], 200, 52, dtype="float16", scale=-0.2)
+    rng = np.random.default_rng(53)
+    lens = [int(x) for x in rng.integers(1, 20, size=1100)]
+    _decode_case(tn, 1100, 2, 1, 64, lens, 24, 54, dtype="float16")
+    lens = [int(x) for x in rng.integers(512, 4097, size=16)]
+    _decode_case(tn, 16, 32, 8, 128, lens, 4096, 55, dtype="float16")
 
 
 def test_decode_scale_of_either_sign(tn):

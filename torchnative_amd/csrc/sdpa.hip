@@ -76,6 +76,12 @@ struct El<false> {
     static __device__ inline uint32_t pack_p(float a, float b) { return pack2_bf16_hw(a, b); }
     static __device__ inline uint32_t pack_out(float a, float b) { return pack2_bf16(a, b); }
     static __device__ inline float widen(uint16_t h) { return bf16_to_f32(h); }
+    static __device__ inline f32x4 mfma16(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    // the low and high element of a packed pair, widened (exact)
+    static __device__ inline float lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+    static __device__ inline float hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 };
 template <>
 struct El<true> {
@@ -92,6 +98,11 @@ struct El<true> {
         return (uint32_t)f16_from_f32(a) | ((uint32_t)f16_from_f32(b) << 16);
     }
     static __device__ inline float widen(uint16_t h) { return f16_to_f32(h); }
+    static __device__ inline f32x4 mfma16(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ inline float lo(uint32_t w) { return f16_bits_hw((uint16_t)(w & 0xffffu)); }
+    static __device__ inline float hi(uint32_t w) { return f16_bits_hw((uint16_t)(w >> 16)); }
 };
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
@@ -972,7 +983,7 @@ constexpr int DEC_WAVE_KEYS = 64;
 constexpr int DEC_SPLIT = 4 * DEC_WAVE_KEYS;  // keys per workgroup
 static_assert(DEC_SPLIT == DECODE_SPLIT_KEYS, "the decode step sizes its partials with this");
 
-template <int D, int NR>
+template <int D, int NR, bool F16 = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void k_decode_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vc,
                    int Hq, int Hkv, int nrep, int cap, const int32_t* __restrict__ lens, int nsplit, float sl2,
@@ -1016,12 +1027,12 @@ void k_decode_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restrict__
         vv[i] = vchunk{};
         if (kk < nk) vv[i] = *reinterpret_cast<const vchunk*>(vp + (int64_t)(k0 + kk) * D + DL * lq);
     }
-    bf16x8 qf[D / 32];
+    typename El<F16>::v8 qf[D / 32];
 #pragma unroll
     for (int c = 0; c < D / 32; c++) {
         uint4 v = make_uint4(0, 0, 0, 0);
         if (lq < NR) v = *reinterpret_cast<const uint4*>(Qg + ((int64_t)b * Hq + hq0 + lq) * D + 32 * c + 8 * g);
-        qf[c] = __builtin_bit_cast(bf16x8, v);
+        qf[c] = __builtin_bit_cast(typename El<F16>::v8, v);
     }
 
     f32x4 s[4];
@@ -1030,7 +1041,7 @@ void k_decode_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restrict__
         s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < D / 32; c++)
-            s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[kt][c]), qf[c], s[kt], 0, 0, 0);
+            s[kt] = El<F16>::mfma16(__builtin_bit_cast(typename El<F16>::v8, kf[kt][c]), qf[c], s[kt]);
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -1069,8 +1080,8 @@ void k_decode_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restrict__
         __builtin_memcpy(ws, &vv[i], sizeof(ws));
 #pragma unroll
         for (int e = 0; e < DL / 2; e++) {
-            vf[2 * e] = __builtin_bit_cast(float, ws[e] << 16);
-            vf[2 * e + 1] = __builtin_bit_cast(float, ws[e] & 0xffff0000u);
+            vf[2 * e] = El<F16>::lo(ws[e]);
+            vf[2 * e + 1] = El<F16>::hi(ws[e]);
         }
 #pragma unroll
         for (int hh = 0; hh < NR; hh++) {
@@ -1146,7 +1157,7 @@ struct SkCfg {
     static constexpr int NB = (D == 128 && NR > 4) ? 3 : 4;  // 8 heads' accumulators take a slot's registers
 };
 
-template <int D, int NR>
+template <int D, int NR, bool F16 = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void k_decode_sk_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kc,
                       const uint16_t* __restrict__ Vc, int B, int Hq, int Hkv, int nrep, int cap,
@@ -1316,8 +1327,8 @@ void k_decode_sk_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restric
             s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int cc = 0; cc < D / 32; cc++)
-                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.k[kt][cc]),
-                                                                __builtin_bit_cast(bf16x8, f.q[cc]), s[kt], 0, 0, 0);
+                s[kt] = El<F16>::mfma16(__builtin_bit_cast(typename El<F16>::v8, f.k[kt][cc]),
+                                                                __builtin_bit_cast(typename El<F16>::v8, f.q[cc]), s[kt]);
         }
         float t[CH][4];
         float mx = -INFINITY;
@@ -1358,8 +1369,8 @@ void k_decode_sk_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restric
                 float vf[DL];
 #pragma unroll
                 for (int e = 0; e < DL / 2; e++) {
-                    vf[2 * e] = __builtin_bit_cast(float, ws[e] << 16);
-                    vf[2 * e + 1] = __builtin_bit_cast(float, ws[e] & 0xffff0000u);
+                    vf[2 * e] = El<F16>::lo(ws[e]);
+                    vf[2 * e + 1] = El<F16>::hi(ws[e]);
                 }
 #pragma unroll
                 for (int hh = 0; hh < NR; hh++) {
@@ -1502,7 +1513,9 @@ __global__ __launch_bounds__(D) void k_decode_sk_combine(const float* __restrict
         mm = bm;
     }
     const float mu = (mm == -INFINITY) ? 0.0f : mm;
-    if constexpr (sizeof(OT) == 2)
+    if constexpr (std::is_same<OT, _Float16>::value)
+        reinterpret_cast<uint16_t*>(out)[((int64_t)b * Hq + h) * D + d] = f16_from_f32(acc / tl);
+    else if constexpr (sizeof(OT) == 2)
         out[((int64_t)b * Hq + h) * D + d] = bf16_from_f32(acc / tl);
     else
         out[((int64_t)b * Hq + h) * D + d] = acc / tl;
@@ -1766,7 +1779,9 @@ __global__ __launch_bounds__(D) void k_decode_combine(const float* __restrict__ 
         tl = tl + ml.y * f;
         acc = acc + part_o[(base + s) * D + d] * f;
     }
-    if constexpr (sizeof(OT) == 2)
+    if constexpr (std::is_same<OT, _Float16>::value)
+        reinterpret_cast<uint16_t*>(out)[((int64_t)b * Hq + h) * D + d] = f16_from_f32(acc / tl);
+    else if constexpr (sizeof(OT) == 2)
         out[((int64_t)b * Hq + h) * D + d] = bf16_from_f32(acc / tl);
     else
         out[((int64_t)b * Hq + h) * D + d] = acc / tl;
@@ -1779,8 +1794,9 @@ const char* OP = "aten._scaled_dot_product_flash_attention_for_cpu.default";
 
 // Argument checks of the decode attention (shared with the decode step).
 tn_status decode_check(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, int64_t max_len) {
-    if (dtype != TN_BF16 && dtype != TN_F32)
-        return fail(TN_ENOTIMPL, "sdpa_decode: only float32 and bfloat16 KV caches are implemented on the hip device");
+    if (dtype != TN_BF16 && dtype != TN_F32 && dtype != TN_F16)
+        return fail(TN_ENOTIMPL,
+                    "sdpa_decode: only float32, bfloat16 and float16 KV caches are implemented on the hip device");
     if (B < 0 || Hq < 0 || Hkv <= 0 || cap <= 0 || D <= 0 || max_len < 1 || max_len > cap)
         return fail(TN_EINVAL, "sdpa_decode: need Hkv > 0, cap > 0 and 1 <= max_len <= cap");
     if (Hq % Hkv != 0) {
@@ -1852,9 +1868,16 @@ tn_status decode_launch(hipStream_t st, int dtype, const void* q, const void* k_
     auto kk = static_cast<const uint16_t*>(k_cache);
     auto vv = static_cast<const uint16_t*>(v_cache);
     dim3 grid((unsigned)nsplit, (unsigned)(Hkv * (nrep / nr)), (unsigned)B);
+    const bool h16 = dtype == TN_F16;
 #define TN_DEC(DD, NR)                                                                                            \
-    hipLaunchKernelGGL((k_decode_bf16<DD, NR>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, nrep,      \
-                       (int)cap, lens, nsplit, sl2, part_o, part_ml)
+    do {                                                                                                          \
+        if (h16)                                                                                                  \
+            hipLaunchKernelGGL((k_decode_bf16<DD, NR, true>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq,       \
+                               (int)Hkv, nrep, (int)cap, lens, nsplit, sl2, part_o, part_ml);                     \
+        else                                                                                                      \
+            hipLaunchKernelGGL((k_decode_bf16<DD, NR>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv,   \
+                               nrep, (int)cap, lens, nsplit, sl2, part_o, part_ml);                               \
+    } while (0)
 #define TN_DEC_D(DD)                       \
     switch (nr) {                          \
         case 8: TN_DEC(DD, 8); break;      \
@@ -1872,12 +1895,22 @@ tn_status decode_launch(hipStream_t st, int dtype, const void* q, const void* k_
 #undef TN_DEC
     TN_LAUNCHED();
     auto oo = static_cast<uint16_t*>(out);
-    if (D == 128)
-        hipLaunchKernelGGL((k_decode_combine<128, uint16_t>), dim3((unsigned)Hq, (unsigned)B), dim3(128), 0, st,
-                           part_o, part_ml, lens, (int)Hq, (int)cap, nsplit, oo, lse);
-    else
-        hipLaunchKernelGGL((k_decode_combine<64, uint16_t>), dim3((unsigned)Hq, (unsigned)B), dim3(64), 0, st,
-                           part_o, part_ml, lens, (int)Hq, (int)cap, nsplit, oo, lse);
+    auto oh = static_cast<_Float16*>(out);
+    if (D == 128) {
+        if (h16)
+            hipLaunchKernelGGL((k_decode_combine<128, _Float16>), dim3((unsigned)Hq, (unsigned)B), dim3(128), 0, st,
+                               part_o, part_ml, lens, (int)Hq, (int)cap, nsplit, oh, lse);
+        else
+            hipLaunchKernelGGL((k_decode_combine<128, uint16_t>), dim3((unsigned)Hq, (unsigned)B), dim3(128), 0, st,
+                               part_o, part_ml, lens, (int)Hq, (int)cap, nsplit, oo, lse);
+    } else {
+        if (h16)
+            hipLaunchKernelGGL((k_decode_combine<64, _Float16>), dim3((unsigned)Hq, (unsigned)B), dim3(64), 0, st,
+                               part_o, part_ml, lens, (int)Hq, (int)cap, nsplit, oh, lse);
+        else
+            hipLaunchKernelGGL((k_decode_combine<64, uint16_t>), dim3((unsigned)Hq, (unsigned)B), dim3(64), 0, st,
+                               part_o, part_ml, lens, (int)Hq, (int)cap, nsplit, oo, lse);
+    }
     TN_LAUNCHED();
     return TN_OK;
 }
@@ -1887,14 +1920,14 @@ namespace {
 // The stream-K bf16 decode (k_decode_sk_bf16 + k_decode_sk_combine) for
 // B <= SK_MAXB, its partials, unit prefix sums and the grid in the stream's
 // workspace.
-template <int D, int NR>
+template <int D, int NR, bool F16>
 tn_status decode_sk_run(hipStream_t st, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t B,
                         int64_t Hq, int64_t Hkv, int64_t cap, const int32_t* lens, int64_t max_len, float sl2,
                         uint16_t* out, float* lse) {
     const int nrep = (int)(Hq / Hkv);
     const int64_t G = Hkv * (nrep / NR);
     int wgs = 0;
-    TN_TRY(resident_workgroups(reinterpret_cast<const void*>(&k_decode_sk_bf16<D, NR>), 256, 0, &wgs));
+    TN_TRY(resident_workgroups(reinterpret_cast<const void*>(&k_decode_sk_bf16<D, NR, F16>), 256, 0, &wgs));
     const int64_t W = (int64_t)wgs * 4;
     const int64_t slots = B * G + W;
     const size_t po = (size_t)slots * NR * D * sizeof(float);
@@ -1905,18 +1938,21 @@ tn_status decode_sk_run(hipStream_t st, const uint16_t* q, const uint16_t* kc, c
     float* part_o = static_cast<float*>(ws);
     float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + po);
     int* pref = reinterpret_cast<int*>(static_cast<char*>(ws) + po + pm);
-    hipLaunchKernelGGL((k_decode_sk_bf16<D, NR>), dim3((unsigned)wgs), dim3(256), 0, st, q, kc, vc, (int)B, (int)Hq,
-                       (int)Hkv, nrep, (int)cap, lens, (int)max_len, sl2, part_o, part_ml, pref);
+    hipLaunchKernelGGL((k_decode_sk_bf16<D, NR, F16>), dim3((unsigned)wgs), dim3(256), 0, st, q, kc, vc, (int)B,
+                       (int)Hq, (int)Hkv, nrep, (int)cap, lens, (int)max_len, sl2, part_o, part_ml, pref);
     TN_LAUNCHED();
-    hipLaunchKernelGGL((k_decode_sk_combine<D, NR, uint16_t>), dim3((unsigned)Hq, (unsigned)B), dim3(D), 0, st,
-                       part_o, part_ml, pref, lens, (int)B, (int)Hq, (int)Hkv, nrep, (int)max_len, W, out, lse);
+    using OT = typename std::conditional<F16, _Float16, uint16_t>::type;
+    hipLaunchKernelGGL((k_decode_sk_combine<D, NR, OT>), dim3((unsigned)Hq, (unsigned)B), dim3(D), 0, st,
+                       part_o, part_ml, pref, lens, (int)B, (int)Hq, (int)Hkv, nrep, (int)max_len, W,
+                       reinterpret_cast<OT*>(out), lse);
     TN_LAUNCHED();
     return TN_OK;
 }
 
-tn_status decode_sk_launch(hipStream_t st, const void* q, const void* k_cache, const void* v_cache, int64_t B,
-                           int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens, int64_t max_len,
-                           double scale, void* out, float* lse) {
+tn_status decode_sk_launch(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
+                           int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens,
+                           int64_t max_len, double scale, void* out, float* lse) {
+    const bool h16 = dtype == TN_F16;
     const int nrep = (int)(Hq / Hkv);
     const int nr = nrep % 8 == 0 ? 8 : nrep % 4 == 0 ? 4 : nrep % 3 == 0 ? 3 : nrep % 2 == 0 ? 2 : 1;
     const double sc = std::isnan(scale) ? 1.0 / std::sqrt((double)D) : scale;
@@ -1925,7 +1961,9 @@ tn_status decode_sk_launch(hipStream_t st, const void* q, const void* k_cache, c
     auto kk = static_cast<const uint16_t*>(k_cache);
     auto vv = static_cast<const uint16_t*>(v_cache);
     auto oo = static_cast<uint16_t*>(out);
-#define TN_SK(DD, NR) return decode_sk_run<DD, NR>(st, qq, kk, vv, B, Hq, Hkv, cap, lens, max_len, sl2, oo, lse)
+#define TN_SK(DD, NR)                                                                                          \
+    return h16 ? decode_sk_run<DD, NR, true>(st, qq, kk, vv, B, Hq, Hkv, cap, lens, max_len, sl2, oo, lse)    \
+               : decode_sk_run<DD, NR, false>(st, qq, kk, vv, B, Hq, Hkv, cap, lens, max_len, sl2, oo, lse)
 #define TN_SK_D(DD)                    \
     switch (nr) {                      \
         case 8: TN_SK(DD, 8);          \
@@ -2279,12 +2317,13 @@ tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_c
         return fail(TN_EINVAL, "sdpa_decode: q, the caches and out must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     // the stream-K kernel counts 16-key units of all segments in an int
-    if (dtype == TN_BF16 && B <= SK_MAXB && B * Hq * cdiv(max_len, SK_UNIT) <= INT32_MAX)
-        return decode_sk_launch(st, q, k_cache, v_cache, B, Hq, Hkv, cap, D, lens, max_len, scale, out, lse);
+    const bool half = dtype == TN_BF16 || dtype == TN_F16;
+    if (half && B <= SK_MAXB && B * Hq * cdiv(max_len, SK_UNIT) <= INT32_MAX)
+        return decode_sk_launch(st, dtype, q, k_cache, v_cache, B, Hq, Hkv, cap, D, lens, max_len, scale, out, lse);
     // the split kernel below takes the row maximum before scaling
-    if (dtype == TN_BF16 && scale < 0.0)
+    if (half && scale < 0.0)
         return fail(TN_ENOTIMPL, "sdpa_decode: a negative scale is not implemented on the hip device for more than 1024 "
-                                 "bfloat16 sequences");
+                                 "16-bit sequences");
     const int64_t nsplit = cdiv(max_len, DEC_SPLIT);
     const size_t po = (size_t)B * Hq * nsplit * D * sizeof(float);
     const size_t pm = (size_t)B * Hq * nsplit * sizeof(float2);
