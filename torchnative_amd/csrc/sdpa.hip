@@ -307,11 +307,16 @@ __host__ __device__ inline int row_splits(int n, int target) { return n <= targe
 // of long and short items and the longest start first. ncls = 0: no row is
 // split and class c is query block nqb-1-c.
 constexpr int FLASH_MAX_CLS = 768;
+// A list of at most FLASH_INLINE classes travels inside the kernel arguments,
+// so a workgroup's class is one scalar load from the argument segment rather
+// than two dependent ones (the table pointer, then the entry).
+constexpr int FLASH_INLINE = 128;
 struct FlashWork {
     int target;            // tiles per item
     int bh;                // B * Hq
     int ncls;
-    const uint32_t* cls;   // device table [ncls]: qt | split << 16
+    const uint32_t* cls;   // device table [ncls] when ncls > FLASH_INLINE: qt | split << 16
+    uint32_t inl[FLASH_INLINE];  // the table itself when ncls <= FLASH_INLINE
 };
 
 // MASK: 0 none; 1 an f32 additive mask; 2 a bf16 one, dense [B, Hq, L, S]
@@ -353,7 +358,9 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash16(
     const int nqb = (L + F3_BQ - 1) / F3_BQ;
     const int cidx = (int)blockIdx.x / work.bh;
     const int bh = (int)blockIdx.x % work.bh;
-    const uint32_t cl = work.ncls ? work.cls[cidx] : (uint32_t)(nqb - 1 - cidx);
+    const uint32_t cl = work.ncls == 0              ? (uint32_t)(nqb - 1 - cidx)
+                        : work.ncls <= FLASH_INLINE ? work.inl[cidx]
+                                                    : work.cls[cidx];
     const int qt = (int)(cl & 0xffffu), split = (int)(cl >> 16);
     const int h = bh % Hq, b = bh / Hq;
     const int kvh = h / (Hq / Hkv);
@@ -2096,7 +2103,9 @@ tn_status flash_plan(hipStream_t st, int64_t B, int64_t Hq, int64_t L, int64_t S
     std::vector<uint32_t> table;
     p.nitems = flash_work(B, Hq, L, S, causal, slots, p.w, p.nsplit, table);
     p.w.cls = nullptr;
-    if (!table.empty()) {
+    if (!table.empty() && table.size() <= (size_t)FLASH_INLINE) {
+        std::copy(table.begin(), table.end(), p.w.inl);
+    } else if (!table.empty()) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         TN_HIP(hipStreamIsCapturing(st, &cs));
         if (cs != hipStreamCaptureStatusNone)
