@@ -387,3 +387,32 @@ def test_mask_dtype_rule(tn):
     mt = tn.tensor(np.zeros((1, 1, 4, 4), np.float32), dtype="bfloat16", device="hip")
     with pytest.raises(RuntimeError, match="Attention mask is the same data type as query"):
         tn._aten_dispatch(OP, qt, qt, qt, 0.0, False, attn_mask=mt)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_large_scores_on_the_mfma_kernels(tn, dtype, D, causal):
+    """Scores far outside the usual range (q and k scaled by 20 and 200): the
+    row maximum must be taken over finished MFMA results, or a partly
+    accumulated maximum makes exp2 overflow. Every tile count from one to many
+    stages and split rows (S up to 1100)."""
+    for S, amp in ((64, 200.0), (100, 200.0), (300, 20.0), (1100, 20.0)):
+        rng = np.random.default_rng(S + D)
+        q = rng.standard_normal((1, 2, S, D)) * amp
+        k = rng.standard_normal((1, 2, S, D)) * amp
+        v = rng.standard_normal((1, 2, S, D)) * 30.0
+        _check(tn, dtype, q, k, v, causal)
+
+
+def test_large_scores_on_the_f32_and_decode_kernels(tn):
+    rng = np.random.default_rng(61)
+    for D in (64, 128):
+        q = rng.standard_normal((1, 2, 300, D)) * 20.0
+        k = rng.standard_normal((1, 2, 300, D)) * 20.0
+        v = rng.standard_normal((1, 2, 300, D))
+        _check(tn, "float32", q, k, v, True)
+    # decode over bf16 and f16 caches: q and k scaled by 20 through the scale
+    for dtype in ("bfloat16", "float16"):
+        _decode_case(tn, 3, 8, 2, 128, [1, 77, 300], 320, 62, scale=400.0 / np.sqrt(128), dtype=dtype)
+        _decode_case(tn, 2, 9, 3, 64, [700, 64], 800, 63, scale=400.0 / 8, dtype=dtype)

@@ -462,6 +462,14 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash16(
                 const V8 ka = *reinterpret_cast<const V8*>(tK + row * D + swz(row, 2 * c + hh) * 8);
                 acc = E::mfma(ka, qf[c], acc);
             }
+            // The scores are read by VALU next, on interior tiles right after
+            // the branch around the edge masking; there the compiler's hazard
+            // pass (with MFMA results in VGPRs) emitted no wait states, and
+            // the row maximum read a partly accumulated result (wrong, and
+            // exp2 overflowed, for large scores). A VALU read of a 16-pass
+            // XDL result needs 18 wait states: they are spelled out here,
+            // tied to the accumulator so that no read is scheduled above them.
+            asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(acc));
 #pragma unroll
             for (int r = 0; r < 16; r++) sv[s2][r] = acc[r];
         }
@@ -555,6 +563,10 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash16(
         step(I0{}, st);
         if (st + 1 < nst) step(I1{}, st + 1);
     }
+    // the accumulators are read by VALU and LDS stores below, past the loop's
+    // exit branch: the XDL wait states, spelled out as for the scores
+#pragma unroll
+    for (int i = 0; i < D / 32; i++) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(o[i]));
 
     l = xor32_sum(l);
     // Tree merge of the key groups through LDS: in the round of width `half`,
