@@ -284,15 +284,17 @@ __device__ __attribute__((always_inline)) inline void merge_split_rows(float* pa
     if (threadIdx.x == 0) __hip_atomic_store(tickets + ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// key groups and keys per wave tile by head dim: both stage 32 KB of K and V
-// per ring stage (64 KB of LDS), so two 4-wave workgroups share a CU. (One
-// 8-wave workgroup per CU measured slower: its single barrier keeps the two
-// waves of each SIMD in the same phase, MFMA against MFMA and softmax
-// against softmax, where two workgroups drift apart and overlap.)
+// key groups and keys per wave tile: 32-key wave tiles at both head dims, so
+// a ring stage holds 64 keys (16 KB of K and V at D=64, 32 KB at D=128). At
+// D=64 this measured 1.5-2% faster on config 2 than 64-key tiles (64 KB of
+// ring) and leaves room for more workgroups per CU. One 8-wave workgroup per
+// CU measured no faster: its single barrier keeps the two waves of each SIMD
+// in the same phase, MFMA against MFMA and softmax against softmax, where
+// independent workgroups drift apart and overlap.
 template <int D>
 struct FlashCfg {
     static constexpr int KG = 2;
-    static constexpr int BKW = D == 64 ? 64 : 32;
+    static constexpr int BKW = 32;
 };
 
 // A row of n key tiles is cut into row_splits(n, target) items; item s covers
