@@ -193,3 +193,29 @@ def test_config3_prefill_gemm_bf16_in_bf16_out_at_full_size(tn):
     # rows computed in a separate, smaller call are the same bits
     part = tn._quantized_linear(tn.tensor(x_widened[300:305], device="hip"), q).numpy()
     assert part.tobytes() == y32[300:305].tobytes()
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_gemm_prepass_aligned_and_unaligned_x_agree_bitwise(tn, fmt):
+    """The GEMM's Q8_0 prepass has a 16-byte-load kernel for an aligned x and
+    a per-element one for any other x; both give the same codes and scales,
+    including a block of NaNs and a row of zeros, and match the oracle."""
+    from torchnative_amd import _lib
+
+    rng = np.random.default_rng(301)
+    m, n, k = 37, 70, 1024
+    x = (rng.standard_normal((m, k)) * 1.7).astype(np.float32)
+    x[3, 64:96] = np.nan
+    x[5] = 0.0
+    blob = O.synth_q4_0_weight(n, k, 0.01, 302) if fmt == "q4_0" else O.synth_q8_0_weight(n, k, 0.01, 302)
+    q = tn._quantized_from_blob(blob, (n, k), fmt, device="hip")
+    want = (O.q4_0_linear if fmt == "q4_0" else O.q8_0_linear)(x, blob, n, threads=8)
+    aligned = tn._quantized_linear(tn.tensor(x, device="hip"), q).numpy()
+    # the same rows one float past a 16-byte boundary
+    buf = tn.tensor(np.concatenate([np.zeros(1, np.float32), x.reshape(-1)]), device="hip")
+    y = tn.empty((m, n), "float32", "hip")
+    fn = getattr(_lib.lib(), f"tn_{fmt}_linear")
+    _lib.check(fn(None, buf.data_ptr() + 4, _lib.TN_F32, m, k, *q._planes(), n, None, y.data_ptr(), _lib.TN_F32))
+    unaligned = y.numpy()
+    assert aligned.tobytes() == unaligned.tobytes()
+    assert np.array_equal(aligned, want, equal_nan=True)

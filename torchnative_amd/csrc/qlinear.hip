@@ -67,7 +67,9 @@ __device__ inline float load_x<uint16_t>(const uint16_t* p) { return bf16_to_f32
 // amax/127 (IEEE division), id = 1/d or 0, q = (round-half-away(x*id)) as i8.
 // Returns q; *dx gets f32(f16(d)), the scale the dot product uses.
 __device__ inline int q8_0_lane(float v, float* dx) {
-    float a = fabsf(v);
+    // f32::max from 0 (k_quants.rs:676-705): a NaN lane counts as 0, so a
+    // block of NaNs has amax 0, id 0 and zero codes, as the reference's has
+    float a = fmaxf(0.0f, fabsf(v));
 #pragma unroll
     for (int off = 16; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
     float d = a / 127.0f;
@@ -587,6 +589,79 @@ __global__ __launch_bounds__(256) void k_q8_rows(const XT* __restrict__ x, int M
     }
 }
 
+// Eight consecutive activations as floats: 16 bytes of bf16 or 32 of f32
+// (p 16-byte aligned).
+template <typename XT>
+__device__ inline void load_x8(const XT* p, float (&v)[8]);
+template <>
+__device__ inline void load_x8<float>(const float* p, float (&v)[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+template <>
+__device__ inline void load_x8<uint16_t>(const uint16_t* p, float (&v)[8]) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = __builtin_bit_cast(float, w[i] << 16);
+        v[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
+    }
+}
+
+// The Q8_0 codes of one block held by four lanes, eight elements each: the
+// block's amax (order-free), d = amax/127, id = 1/d and the rounding are
+// q8_0_lane's, element for element, so the codes, the scale and the code sum
+// are identical; the sum comes back through `s`.
+__device__ inline void q8_0_quad(const float (&v)[8], int (&q)[8], float* dx, int* s) {
+    float a = 0.0f;  // f32::max from 0: NaNs are skipped (k_quants.rs:676-705)
+#pragma unroll
+    for (int e = 0; e < 8; e++) a = fmaxf(a, fabsf(v[e]));
+    a = fmaxf(a, __shfl_xor(a, 1, 4));
+    a = fmaxf(a, __shfl_xor(a, 2, 4));
+    const float d = a / 127.0f;
+    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    *dx = f16_to_f32(f16_from_f32(d));
+    int sum = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        q[e] = sat_i8(roundf(v[e] * id));
+        sum += q[e];
+    }
+    sum += __shfl_xor(sum, 1, 4);
+    sum += __shfl_xor(sum, 2, 4);
+    *s = sum;
+}
+
+// k_q8_rows for a 16-byte aligned x: four lanes per (row, block), one 16- or
+// 32-byte load each. Lane part p holds elements 8p .. 8p+7, whose K slots are
+// two runs of four (kslot_of_element), written as two 8-byte stores.
+template <typename XT>
+__global__ __launch_bounds__(256) void k_q8_rows_v(const XT* __restrict__ x, int M, int M_pad, int K, int nb,
+                                                   uint16_t* __restrict__ xc, float* __restrict__ dxT,
+                                                   float* __restrict__ corrT) {
+    const int64_t blk = (int64_t)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
+    const int part = threadIdx.x & 3;
+    if (blk >= (int64_t)M_pad * nb) return;  // the four lanes of a block leave together
+    const int row = (int)(blk / nb), b = (int)(blk - (int64_t)row * nb);
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (row < M) load_x8<XT>(x + (int64_t)row * K + b * QK + 8 * part, v);
+    int q[8], s;
+    float dx;
+    q8_0_quad(v, q, &dx, &s);
+    if (row >= M) dx = 0.0f;
+    auto code = [](int c) { return __builtin_bit_cast(uint32_t, (float)c) >> 16; };
+    const int slot0 = kslot_of_element(8 * part), slot1 = kslot_of_element(8 * part + 4);
+    *reinterpret_cast<uint2*>(xc + blk * QK + slot0) =
+        make_uint2(code(q[0]) | (code(q[1]) << 16), code(q[2]) | (code(q[3]) << 16));
+    *reinterpret_cast<uint2*>(xc + blk * QK + slot1) =
+        make_uint2(code(q[4]) | (code(q[5]) << 16), code(q[6]) | (code(q[7]) << 16));
+    if (part == 0) {
+        dxT[(int64_t)b * M_pad + row] = dx;
+        corrT[(int64_t)b * M_pad + row] = (float)(-136 * s);
+    }
+}
+
 // bytes 0,1 (or 2,3) of x -> the bf16 pair (128 + byte0, 128 + byte1): the
 // high byte of each half comes from the constant 0x43
 __device__ inline uint32_t codes_pair01(uint32_t x) { return __builtin_amdgcn_perm(0x43434343u, x, 0x04010400u); }
@@ -793,6 +868,28 @@ __global__ __launch_bounds__(256) void k_q8_rows_i8(const XT* __restrict__ x, in
     }
     xc[blk * QK + lane] = (int8_t)q;
     if (lane == 0) dxT[(int64_t)b * M_pad + row] = dx;
+}
+
+// k_q8_rows_i8 for a 16-byte aligned x: four lanes per (row, block), eight
+// int8 codes each in natural order (one 8-byte store).
+template <typename XT>
+__global__ __launch_bounds__(256) void k_q8_rows_i8_v(const XT* __restrict__ x, int M, int M_pad, int K, int nb,
+                                                      int8_t* __restrict__ xc, float* __restrict__ dxT) {
+    const int64_t blk = (int64_t)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
+    const int part = threadIdx.x & 3;
+    if (blk >= (int64_t)M_pad * nb) return;
+    const int row = (int)(blk / nb), b = (int)(blk - (int64_t)row * nb);
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (row < M) load_x8<XT>(x + (int64_t)row * K + b * QK + 8 * part, v);
+    int q[8], s;
+    float dx;
+    q8_0_quad(v, q, &dx, &s);
+    if (row >= M) dx = 0.0f;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; e++) w[e >> 2] |= ((uint32_t)q[e] & 0xffu) << (8 * (e & 3));
+    *reinterpret_cast<uint2*>(xc + blk * QK + 8 * part) = make_uint2(w[0], w[1]);
+    if (part == 0) dxT[(int64_t)b * M_pad + row] = dx;
 }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -1021,7 +1118,9 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
     const int64_t M_pad = cdiv(m, GM_BM) * GM_BM;
     if (M_pad > INT32_MAX || n > INT32_MAX) return fail(TN_EVALUE, "torch._C._quantized_linear: shape too large");
     const int64_t blocks = M_pad * nb;
-    const unsigned pgrid = (unsigned)cdiv(blocks, 8);
+    const unsigned pgrid = (unsigned)cdiv(blocks, 8);   // 32 lanes per block
+    const unsigned vgrid = (unsigned)cdiv(blocks, 64);  // 4 lanes per block
+    const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0;
     const dim3 grid((unsigned)cdiv(n, GM_BN), (unsigned)(M_pad / GM_BM));
     const size_t dx_bytes = (size_t)M_pad * nb * 4;
     void* ws = nullptr;
@@ -1031,8 +1130,12 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
         if (s != TN_OK) return s;
         int8_t* xc = static_cast<int8_t*>(ws);
         float* dxT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes);
-        hipLaunchKernelGGL((k_q8_rows_i8<XT>), dim3(pgrid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
-                           dxT);
+        if (aligned)
+            hipLaunchKernelGGL((k_q8_rows_i8_v<XT>), dim3(vgrid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb,
+                               xc, dxT);
+        else
+            hipLaunchKernelGGL((k_q8_rows_i8<XT>), dim3(pgrid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb,
+                               xc, dxT);
         TN_LAUNCHED();
         hipLaunchKernelGGL(k_gemm_q8, grid, dim3(GM_THREADS), 0, st, xc, dxT, (int)m, (int)M_pad, nb, qs, d, (int)n,
                            bias, y, y_bf16);
@@ -1044,8 +1147,12 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
         uint16_t* xc = static_cast<uint16_t*>(ws);
         float* dxT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes);
         float* corrT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes + dx_bytes);
-        hipLaunchKernelGGL((k_q8_rows<XT>), dim3(pgrid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
-                           dxT, corrT);
+        if (aligned)
+            hipLaunchKernelGGL((k_q8_rows_v<XT>), dim3(vgrid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
+                               dxT, corrT);
+        else
+            hipLaunchKernelGGL((k_q8_rows<XT>), dim3(pgrid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
+                               dxT, corrT);
         TN_LAUNCHED();
         hipLaunchKernelGGL(k_gemm, grid, dim3(GM_THREADS), 0, st, xc, dxT, corrT, (int)m, (int)M_pad, nb, qs, d,
                            (int)n, bias, y, y_bf16);
