@@ -234,7 +234,10 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
  *   [1, cap];
  *   max_len: host upper bound of lens (sizes the split-KV grid);
  *   lse nullable f32 [B, Hq].
- * Split-KV with a combine pass; the partials live in the library workspace. */
+ * Head dims 64 and 128: split-KV with a combine pass, the partials in the
+ * library workspace; any other head dim up to 256 runs on the plain kernel
+ * (one workgroup per (sequence, head)). A sequence of length 0 gives NaN out
+ * and -inf lse. */
 tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_cache,
                          const void* v_cache, int64_t B, int64_t Hq, int64_t Hkv, int64_t cap,
                          int64_t D, const int32_t* lens, int64_t max_len, double scale,

@@ -266,6 +266,16 @@ def test_decode_f16_caches(tn):
     _decode_case(tn, 16, 32, 8, 128, lens, 4096, 55, dtype="float16")
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+def test_decode_other_head_dims(tn, dtype):
+    """Head dims the MFMA decode kernels do not take run on the plain kernel,
+    with ragged lengths, an empty sequence and truncation at max_len."""
+    _decode_case(tn, 3, 8, 2, 96, [1, 77, 300], 320, 71, dtype=dtype)
+    _decode_case(tn, 3, 4, 4, 32, [0, 5, 40], 48, 72, dtype=dtype)
+    _decode_case(tn, 2, 6, 3, 80, [100, 50], 128, 73, max_len=64, dtype=dtype)
+    _decode_case(tn, 2, 2, 1, 256, [33, 200], 200, 74, scale=-0.1, dtype=dtype)
+
+
 def test_decode_scale_of_either_sign(tn):
     _decode_case(tn, 2, 8, 2, 128, [300, 41], 320, 21, scale=0.3)
     _decode_case(tn, 2, 8, 2, 128, [300, 41], 320, 22, scale=-0.2)

@@ -662,11 +662,14 @@ __device__ inline void any_store(void* p, int64_t i, float v) {
 }
 
 // MASK: 0 none; 1 f32; 2 the query's dtype; dense [B, Hq, L, S]
+// lens (decode): nullable device int32 [B]; sequence b then attends keys
+// 0 .. min(lens[b], max_len) - 1 of its S = cap rows.
 template <int ET, int MASK>
 __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, const void* __restrict__ Kg,
                                                   const void* __restrict__ Vg, int Hq, int Hkv, int L, int S, int D,
                                                   float sl2, int causal, void* __restrict__ Og,
-                                                  float* __restrict__ lse, const void* __restrict__ mask) {
+                                                  float* __restrict__ lse, const void* __restrict__ mask,
+                                                  const int32_t* __restrict__ lens, int max_len) {
     __shared__ float sQ[ANY_BQ * ANY_DMAX];
     __shared__ float sK[ANY_BK * (ANY_DMAX + 1)];  // rows padded by one word: the 8 keys a row reads at one d
     __shared__ float sV[ANY_BK * ANY_DMAX];        // sit in 8 different banks
@@ -688,7 +691,9 @@ __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, c
 #pragma unroll
     for (int c = 0; c < NC; c++) o[c] = 0.0f;
     float m = -INFINITY, l = 0.0f;
-    const int kend = causal ? min(S, q0 + ANY_BQ) : S;
+    // keys this workgroup's rows may see: [0, kvalid)
+    const int kvalid = lens ? max(0, min(min(lens[b], max_len), S)) : S;
+    const int kend = causal ? min(kvalid, q0 + ANY_BQ) : kvalid;
     for (int k0 = 0; k0 < kend; k0 += ANY_BK) {
         __syncthreads();  // the previous tile's reads are done
         for (int e = tid; e < ANY_BK * D; e += 256) {
@@ -711,7 +716,7 @@ __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, c
             } else if constexpr (MASK == 2) {
                 if (qi < L && key < S) v = v + any_load<ET>(mask, (bh * L + qi) * S + key) * LOG2E;
             }
-            if (key >= S || (causal && key > qi)) v = -INFINITY;
+            if (key >= kvalid || (causal && key > qi)) v = -INFINITY;
             s[i] = v;
             mx = fmaxf(mx, v);
         }
@@ -751,7 +756,9 @@ __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, c
         const int d = t + 8 * c;
         if (d < D) any_store<ET>(Og, qbase + (int64_t)qi * D + d, o[c] * inv);
     }
-    if (lse && t == 0) lse[bh * L + qi] = m == -INFINITY ? NAN : m * LN2 + logf(l);
+    // a row with no key: NaN, as the reference's (aten.rs:10392-10420); a decode
+    // sequence of length 0: -inf, as the split decode kernels give
+    if (lse && t == 0) lse[bh * L + qi] = m == -INFINITY ? (lens ? -INFINITY : NAN) : m * LN2 + logf(l);
 }
 
 constexpr int PF_BQ = 64, PF_BK = 64;
@@ -1828,10 +1835,10 @@ tn_status decode_check(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t ca
                       (long long)Hq, (long long)Hkv);
         return fail(TN_ENOTIMPL, buf);
     }
-    if (D != 64 && D != 128) {
+    if (D > ANY_DMAX) {
         char buf[256];
         std::snprintf(buf, sizeof buf,
-                      "sdpa_decode: head_dim %lld is not implemented on the hip device (kernels exist for 64 and 128)",
+                      "sdpa_decode: head_dim %lld is not implemented on the hip device (kernels exist up to 256)",
                       (long long)D);
         return fail(TN_ENOTIMPL, buf);
     }
@@ -2198,7 +2205,7 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         const int et = dtype == TN_F32 ? 0 : dtype == TN_BF16 ? 1 : 2;
 #define TN_ANY(ET, MK)                                                                                            \
     hipLaunchKernelGGL((k_attn_any<ET, MK>), grid, dim3(256), 0, st, q, k, v, (int)Hq, (int)Hkv, (int)L, (int)S, \
-                       (int)D, sl2, c, out, lse, attn_mask)
+                       (int)D, sl2, c, out, lse, attn_mask, nullptr, 0)
 #define TN_ANY_MK(ET)                     \
     do {                                  \
         if (mk == 0) TN_ANY(ET, 0);       \
@@ -2339,6 +2346,24 @@ tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_c
     if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) % 16 != 0)
         return fail(TN_EINVAL, "sdpa_decode: q, the caches and out must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
+    if (D != 64 && D != 128) {
+        // the plain kernel: one query row per (sequence, head), the cache's cap
+        // rows as its keys, each sequence's length from lens
+        const double sc = std::isnan(scale) ? 1.0 / std::sqrt((double)D) : scale;
+        const float sl2 = (float)sc * LOG2E;
+        const dim3 grid(1u, (unsigned)Hq, (unsigned)B);
+        if (dtype == TN_F32)
+            hipLaunchKernelGGL((k_attn_any<0, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
+                               (int)cap, (int)D, sl2, 0, out, lse, nullptr, lens, (int)max_len);
+        else if (dtype == TN_BF16)
+            hipLaunchKernelGGL((k_attn_any<1, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
+                               (int)cap, (int)D, sl2, 0, out, lse, nullptr, lens, (int)max_len);
+        else
+            hipLaunchKernelGGL((k_attn_any<2, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
+                               (int)cap, (int)D, sl2, 0, out, lse, nullptr, lens, (int)max_len);
+        TN_LAUNCHED();
+        return TN_OK;
+    }
     // the stream-K kernel counts 16-key units of all segments in an int
     const bool half = dtype == TN_BF16 || dtype == TN_F16;
     if (half && B <= SK_MAXB && B * Hq * cdiv(max_len, SK_UNIT) <= INT32_MAX)
