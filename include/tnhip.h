@@ -198,8 +198,10 @@ tn_status tn_q4_k_linear(void* stream, const void* x, int x_dtype, int64_t m, in
  * `aten._scaled_dot_product_flash_attention_for_cpu(q, k, v, dropout_p=0.,
  * is_causal=False, *, attn_mask=None, scale=None) -> (out, logsumexp)`
  * (aten.rs:10092-10440), device half.
- *   q [B,Hq,L,D], k/v [B,Hkv,S,D] in `dtype` (TN_F32, TN_BF16 or TN_F16),
- *   dense; TN_F64 is refused by name.
+ *   q [B,Hq,L,D], k/v [B,Hkv,S,D] in `dtype` (TN_F32, TN_BF16, TN_F16 or
+ *   TN_F64), dense. An f64 query computes in f64 (plain kernel) and writes
+ *   lse as f64 (`lse` then points at doubles); an f32 mask on it is refused
+ *   by name (aten.rs:10160-10170).
  *   GQA: query head h reads key/value head h / (Hq/Hkv), indexed, not
  *   materialised (aten.rs:17106-17126); Hq % Hkv != 0 is refused by name.
  *   is_causal: upper-left aligned, row t attends keys 0..=t (aten.rs:10038-10041).

@@ -94,7 +94,9 @@ def test_sdpa_refusals_name_the_reason(L):
     assert call(D=272) == _lib.TN_ENOTIMPL and "head_dim 272" in _lib.last_error()
     assert call(Hkv=4) == _lib.TN_ENOTIMPL and "do not divide" in _lib.last_error()
     assert call(S=0) == _lib.TN_ENOTIMPL and "zero key length" in _lib.last_error()
-    assert call(dtype=_lib.TN_F64) == _lib.TN_ENOTIMPL and "Double" in _lib.last_error()
+    assert call(dtype=99) == _lib.TN_EINVAL and "Expected data type" in _lib.last_error()
+    assert call(dtype=_lib.TN_F64, mask=1, mask_dtype=_lib.TN_F32) == _lib.TN_ENOTIMPL
+    assert "float32 attn_mask on a float64" in _lib.last_error()
     # the mask is the query's dtype or float32 (aten.rs:10142-10150)
     assert call(mask=1, mask_dtype=_lib.TN_F16) == _lib.TN_EINVAL
     assert "Attention mask is the same data type as query" in _lib.last_error()

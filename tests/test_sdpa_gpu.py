@@ -426,3 +426,61 @@ def test_large_scores_on_the_f32_and_decode_kernels(tn):
     for dtype in ("bfloat16", "float16"):
         _decode_case(tn, 3, 8, 2, 128, [1, 77, 300], 320, 62, scale=400.0 / np.sqrt(128), dtype=dtype)
         _decode_case(tn, 2, 9, 3, 64, [700, 64], 800, 63, scale=400.0 / 8, dtype=dtype)
+
+
+def _f64_bound(q, k, v, scale=None):
+    """|gpu - oracle| for two f64 evaluations of the same attention: each is
+    within 2 gamma_D * max_j sum_d |q_d k_jd| * |scale| * max|V| (score
+    rounding, which moves each probability by at most that relative amount)
+    plus 4 gamma_(S+4) * max|V| (the sums) of the exact value; the bound is
+    twice that. The lse gets the score term without max|V| plus 4 gamma_(S+4)."""
+    B, Hq, L, D = q.shape
+    S = k.shape[2]
+    g = lambda n: n * 2.0 ** -53 / (1 - n * 2.0 ** -53)
+    kk = np.repeat(np.abs(k), Hq // k.shape[1], axis=1)
+    amax = float(np.max(np.abs(q) @ np.swapaxes(kk, -1, -2)))
+    sc = abs(scale) if scale is not None else 1.0 / np.sqrt(D)
+    vmax = float(np.max(np.abs(v)))
+    score = 2 * g(D) * amax * sc
+    return 2 * (score * vmax + 4 * g(S + 4) * vmax), 2 * (score + 4 * g(S + 4))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(1, 9, 3, 26, 26, 64), (2, 8, 2, 65, 130, 128), (1, 3, 1, 100, 37, 80),
+                                   (1, 2, 2, 40, 600, 64)])
+def test_float64_computes_in_float64(tn, shape, causal):
+    """f64 attention runs in f64: within the f64 rounding bound of the
+    oracle's f64 result (an f32 evaluation misses it by orders of magnitude)."""
+    b, hq, hkv, l, s, d = shape
+    q, k, v = _det((b, hq, l, d), 7), _det((b, hkv, s, d), 8), _det((b, hkv, s, d), 9)
+    qt, kt, vt = (tn.tensor(a, dtype="float64", device="hip") for a in (q, k, v))
+    o, lse = tn._aten_dispatch(OP, qt, kt, vt, 0.0, causal)
+    r64, l64 = O.sdpa(q, k, v, is_causal=causal, threads=16, dtype=np.float64)
+    r32, _ = O.sdpa(q, k, v, is_causal=causal, threads=16)
+    tol, ltol = _f64_bound(q, k, v)
+    got = o.numpy()
+    assert o.dtype == "float64" and lse.dtype == "float64"
+    assert float(np.max(np.abs(got - r64))) <= tol
+    assert float(np.max(np.abs(lse.numpy() - l64))) <= ltol
+    assert float(np.max(np.abs(r32 - r64))) > tol  # the bound separates f64 from f32 arithmetic
+
+
+def test_float64_mask_rule_and_masked_rows(tn):
+    rng = np.random.default_rng(81)
+    q, k, v = rng.standard_normal((1, 2, 20, 64)), rng.standard_normal((1, 2, 30, 64)), rng.standard_normal((1, 2, 30, 64))
+    mask = rng.standard_normal((1, 2, 20, 30))
+    mask[0, :, 4, :] = -np.inf
+    qt, kt, vt = (tn.tensor(a, dtype="float64", device="hip") for a in (q, k, v))
+    m32 = tn.tensor(mask.astype(np.float32), device="hip")
+    with pytest.raises(NotImplementedError, match="float32 attn_mask on a float64"):
+        tn._aten_dispatch(OP, qt, kt, vt, 0.0, False, attn_mask=m32)
+    m64 = tn.tensor(mask, dtype="float64", device="hip")
+    o, lse = tn._aten_dispatch(OP, qt, kt, vt, 0.0, False, attn_mask=m64)
+    with np.errstate(invalid="ignore"):
+        r64, l64 = O.sdpa(q, k, v, mask=mask, threads=16, dtype=np.float64)
+    got = o.numpy()
+    assert np.all(np.isnan(got[0, :, 4])) and np.all(np.isnan(lse.numpy()[0, :, 4]))
+    keep = np.ones(20, bool)
+    keep[4] = False
+    tol, _ = _f64_bound(q, k, v)
+    assert float(np.max(np.abs(got[0, :, keep] - r64[0, :, keep]))) <= tol + 2 ** -40 * float(np.max(np.abs(mask[np.isfinite(mask)])))

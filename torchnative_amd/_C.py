@@ -296,7 +296,7 @@ def _scaled_dot_product_flash_attention(query: Tensor, key: Tensor, value: Tenso
                                f"[{B}, {Hq}, {L}, {S}]") from None
         attn_mask = Tensor.from_numpy(np.ascontiguousarray(full), dtype=attn_mask.dtype, device="hip")
     out = Tensor((B, Hq, L, D), query.dtype, "hip")
-    lse = Tensor((B, Hq, L), "float32", "hip")
+    lse = Tensor((B, Hq, L), "float64" if query.dtype == "float64" else "float32", "hip")
     sc = float("nan") if scale is None else float(scale)
     check(lib().tn_sdpa_fwd(current_stream(), _dt(query.dtype), query.data_ptr(), key.data_ptr(), value.data_ptr(),
                             B, Hq, Hkv, L, S, D, attn_mask.data_ptr() if attn_mask is not None else None,

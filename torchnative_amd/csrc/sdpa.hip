@@ -645,35 +645,48 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash16(
 // scores (so the scale's sign does not matter); probabilities stay f32; the
 // output is narrowed RNE to the input dtype.
 // ---------------------------------------------------------------------------
-constexpr int ANY_DMAX = 256, ANY_BQ = 32, ANY_BK = 32;
+constexpr int ANY_DMAX = 256, ANY_BQ = 32;
 
-template <int ET>  // 0 f32, 1 bf16, 2 f16
-__device__ inline float any_load(const void* p, int64_t i) {
+// element type ET: 0 f32, 1 bf16, 2 f16, 3 f64; arithmetic in f64 for f64
+// inputs (the reference computes f64 attention in f64), f32 otherwise
+template <int ET>
+using AnyT = typename std::conditional<ET == 3, double, float>::type;
+
+template <int ET>
+__device__ inline AnyT<ET> any_load(const void* p, int64_t i) {
     if constexpr (ET == 0) return reinterpret_cast<const float*>(p)[i];
     else if constexpr (ET == 1) return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
-    else return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    else if constexpr (ET == 2) return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    else return reinterpret_cast<const double*>(p)[i];
 }
 
 template <int ET>
-__device__ inline void any_store(void* p, int64_t i, float v) {
+__device__ inline void any_store(void* p, int64_t i, AnyT<ET> v) {
     if constexpr (ET == 0) reinterpret_cast<float*>(p)[i] = v;
     else if constexpr (ET == 1) reinterpret_cast<uint16_t*>(p)[i] = bf16_from_f32(v);
-    else reinterpret_cast<uint16_t*>(p)[i] = f16_from_f32(v);
+    else if constexpr (ET == 2) reinterpret_cast<uint16_t*>(p)[i] = f16_from_f32(v);
+    else reinterpret_cast<double*>(p)[i] = v;
 }
 
-// MASK: 0 none; 1 f32; 2 the query's dtype; dense [B, Hq, L, S]
 // lens (decode): nullable device int32 [B]; sequence b then attends keys
-// 0 .. min(lens[b], max_len) - 1 of its S = cap rows.
+// 0 .. min(lens[b], max_len) - 1 of its S = cap rows. lse is f32, or f64 for
+// f64 inputs. Key tiles are 32 keys (16 for f64, which doubles the LDS).
+// MASK: 0 none; 1 f32; 2 the query's dtype; dense [B, Hq, L, S]
 template <int ET, int MASK>
 __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, const void* __restrict__ Kg,
                                                   const void* __restrict__ Vg, int Hq, int Hkv, int L, int S, int D,
-                                                  float sl2, int causal, void* __restrict__ Og,
-                                                  float* __restrict__ lse, const void* __restrict__ mask,
+                                                  double scale, int causal, void* __restrict__ Og,
+                                                  void* __restrict__ lse, const void* __restrict__ mask,
                                                   const int32_t* __restrict__ lens, int max_len) {
-    __shared__ float sQ[ANY_BQ * ANY_DMAX];
-    __shared__ float sK[ANY_BK * (ANY_DMAX + 1)];  // rows padded by one word: the 8 keys a row reads at one d
-    __shared__ float sV[ANY_BK * ANY_DMAX];        // sit in 8 different banks
-    __shared__ float sP[ANY_BQ][ANY_BK];
+    using T = AnyT<ET>;
+    constexpr int BK = ET == 3 ? 16 : 32;  // keys per tile
+    constexpr int KPT = BK / 8;            // keys per thread per tile
+    __shared__ T sQ[ANY_BQ * ANY_DMAX];
+    __shared__ T sK[BK * (ANY_DMAX + 1)];  // rows padded by one element: the 8 keys a row reads at one d
+    __shared__ T sV[BK * ANY_DMAX];        // sit in different banks
+    __shared__ T sP[ANY_BQ][BK];
+    const T sl2 = (T)scale * (T)1.4426950408889634;  // scores to log2 units
+    const T log2e = (T)1.4426950408889634;
     const int tid = threadIdx.x, r = tid >> 3, t = tid & 7;
     const int q0 = blockIdx.x * ANY_BQ, h = blockIdx.y, b = blockIdx.z;
     const int kvh = h / (Hq / Hkv);
@@ -684,52 +697,52 @@ __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, c
     const int KP = D + 1;
     for (int e = tid; e < ANY_BQ * D; e += 256) {
         const int rr = e / D, d = e - rr * D;
-        sQ[rr * D + d] = q0 + rr < L ? any_load<ET>(Qg, qbase + (int64_t)(q0 + rr) * D + d) : 0.0f;
+        sQ[rr * D + d] = q0 + rr < L ? any_load<ET>(Qg, qbase + (int64_t)(q0 + rr) * D + d) : (T)0;
     }
     constexpr int NC = ANY_DMAX / 8;  // output columns per thread, at most
-    float o[NC];
+    T o[NC];
 #pragma unroll
-    for (int c = 0; c < NC; c++) o[c] = 0.0f;
-    float m = -INFINITY, l = 0.0f;
+    for (int c = 0; c < NC; c++) o[c] = 0;
+    T m = -INFINITY, l = 0;
     // keys this workgroup's rows may see: [0, kvalid)
     const int kvalid = lens ? max(0, min(min(lens[b], max_len), S)) : S;
     const int kend = causal ? min(kvalid, q0 + ANY_BQ) : kvalid;
-    for (int k0 = 0; k0 < kend; k0 += ANY_BK) {
+    for (int k0 = 0; k0 < kend; k0 += BK) {
         __syncthreads();  // the previous tile's reads are done
-        for (int e = tid; e < ANY_BK * D; e += 256) {
+        for (int e = tid; e < BK * D; e += 256) {
             const int j = e / D, d = e - j * D;
             const bool in = k0 + j < S;
-            sK[j * KP + d] = in ? any_load<ET>(Kg, kbase + (int64_t)(k0 + j) * D + d) : 0.0f;
-            sV[j * D + d] = in ? any_load<ET>(Vg, kbase + (int64_t)(k0 + j) * D + d) : 0.0f;
+            sK[j * KP + d] = in ? any_load<ET>(Kg, kbase + (int64_t)(k0 + j) * D + d) : (T)0;
+            sV[j * D + d] = in ? any_load<ET>(Vg, kbase + (int64_t)(k0 + j) * D + d) : (T)0;
         }
         __syncthreads();
-        float s[4];
-        float mx = -INFINITY;
+        T sc[KPT];
+        T mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < KPT; i++) {
             const int j = t + 8 * i, key = k0 + j;
-            float acc = 0.0f;
+            T acc = 0;
             for (int d = 0; d < D; d++) acc = acc + sQ[r * D + d] * sK[j * KP + d];
-            float v = acc * sl2;
+            T v = acc * sl2;
             if constexpr (MASK == 1) {
-                if (qi < L && key < S) v = v + reinterpret_cast<const float*>(mask)[(bh * L + qi) * S + key] * LOG2E;
+                if (qi < L && key < S) v = v + (T)reinterpret_cast<const float*>(mask)[(bh * L + qi) * S + key] * log2e;
             } else if constexpr (MASK == 2) {
-                if (qi < L && key < S) v = v + any_load<ET>(mask, (bh * L + qi) * S + key) * LOG2E;
+                if (qi < L && key < S) v = v + any_load<ET>(mask, (bh * L + qi) * S + key) * log2e;
             }
             if (key >= kvalid || (causal && key > qi)) v = -INFINITY;
-            s[i] = v;
-            mx = fmaxf(mx, v);
+            sc[i] = v;
+            mx = fmax(mx, v);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 1));
-        mx = fmaxf(mx, __shfl_xor(mx, 2));
-        mx = fmaxf(mx, __shfl_xor(mx, 4));
-        const float mn = fmaxf(m, mx);
-        const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
-        const float mu = mn == -INFINITY ? 0.0f : mn;
-        float ps = 0.0f;
+        mx = fmax(mx, __shfl_xor(mx, 1));
+        mx = fmax(mx, __shfl_xor(mx, 2));
+        mx = fmax(mx, __shfl_xor(mx, 4));
+        const T mn = fmax(m, mx);
+        const T alpha = mn == -INFINITY ? (T)1 : exp2(m - mn);
+        const T mu = mn == -INFINITY ? (T)0 : mn;
+        T ps = 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float p = exp2f(s[i] - mu);
+        for (int i = 0; i < KPT; i++) {
+            const T p = exp2(sc[i] - mu);
             sP[r][t + 8 * i] = p;
             ps = ps + p;
         }
@@ -743,14 +756,14 @@ __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, c
         for (int c = 0; c < NC; c++) {
             const int d = t + 8 * c;
             if (d < D) {
-                float acc = o[c] * alpha;
-                for (int j = 0; j < ANY_BK; j++) acc = acc + sP[r][j] * sV[j * D + d];
+                T acc = o[c] * alpha;
+                for (int j = 0; j < BK; j++) acc = acc + sP[r][j] * sV[j * D + d];
                 o[c] = acc;
             }
         }
     }
     if (qi >= L) return;
-    const float inv = 1.0f / l;  // a row with no key: 0 * inf = NaN, as the reference's (aten.rs:10392-10420)
+    const T inv = (T)1 / l;  // a row with no key: 0 * inf = NaN, as the reference's (aten.rs:10392-10420)
 #pragma unroll
     for (int c = 0; c < NC; c++) {
         const int d = t + 8 * c;
@@ -758,7 +771,11 @@ __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, c
     }
     // a row with no key: NaN, as the reference's (aten.rs:10392-10420); a decode
     // sequence of length 0: -inf, as the split decode kernels give
-    if (lse && t == 0) lse[bh * L + qi] = m == -INFINITY ? (lens ? -INFINITY : NAN) : m * LN2 + logf(l);
+    if (lse && t == 0) {
+        const T lv = m == -INFINITY ? (lens ? (T)-INFINITY : (T)NAN) : m * (T)0.69314718055994531 + log(l);
+        if constexpr (ET == 3) reinterpret_cast<double*>(lse)[bh * L + qi] = lv;
+        else reinterpret_cast<float*>(lse)[bh * L + qi] = lv;
+    }
 }
 
 constexpr int PF_BQ = 64, PF_BK = 64;
@@ -2156,12 +2173,9 @@ extern "C" {
 tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, const void* v, int64_t B, int64_t Hq,
                       int64_t Hkv, int64_t L, int64_t S, int64_t D, const void* attn_mask, int mask_dtype,
                       int is_causal, double scale, void* out, float* lse) {
-    if (dtype != TN_F32 && dtype != TN_BF16 && dtype != TN_F16) {
-        const char* name = dtype == TN_F64 ? "Double" : "an unknown type";
-        return fail(dtype == TN_F64 ? TN_ENOTIMPL : TN_EINVAL,
-                    std::string("scaled_dot_product_attention_flash_attention: ") + name +
-                        " is not implemented on the hip device (float32, bfloat16 and float16 are)");
-    }
+    if (dtype != TN_F32 && dtype != TN_BF16 && dtype != TN_F16 && dtype != TN_F64)
+        return fail(TN_EINVAL, "scaled_dot_product_attention_flash_attention: Expected data type in FP32, FP64, BF16, "
+                               "FP16");
     if (B < 0 || Hq < 0 || L < 0 || S < 0 || D < 0 || Hkv < 0)
         return fail(TN_EINVAL, std::string(OP) + ": negative dimension");
     if (D == 0 || S == 0) {
@@ -2185,7 +2199,11 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     if (attn_mask && mask_dtype != dtype && mask_dtype != TN_F32)
         return fail(TN_EINVAL, "scaled_dot_product_attention_flash_attention: Attention mask is the same data type "
                                "as query");
-    // 0 none, 1 f32, 2 bf16: the kernels' MASK parameter
+    // an f64 query with an f32 mask is refused by name (aten.rs:10160-10170)
+    if (attn_mask && dtype == TN_F64 && mask_dtype == TN_F32)
+        return fail(TN_ENOTIMPL, "aten._scaled_dot_product_flash_attention_for_cpu: a float32 attn_mask on a float64 "
+                                 "query is refused. Pass the mask as float64.");
+    // 0 none, 1 f32, 2 the query's dtype: the kernels' MASK parameter
     const int mk = !attn_mask ? 0 : mask_dtype == TN_F32 ? 1 : 2;
     if (D > ANY_DMAX) return refuse_head_dim(D);
     if (B * Hq * L == 0) return TN_OK;  // nothing to write (aten.rs:10242-10259 returns empty zeros)
@@ -2200,12 +2218,12 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     // the MFMA kernels take the row maximum of the unscaled scores (right for
     // scale >= 0) and exist for head dims 64 and 128; anything else runs on
     // the plain kernel
-    if ((D != 64 && D != 128) || sc < 0.0) {
+    if ((D != 64 && D != 128) || sc < 0.0 || dtype == TN_F64) {
         const dim3 grid((unsigned)cdiv(L, ANY_BQ), (unsigned)Hq, (unsigned)B);
-        const int et = dtype == TN_F32 ? 0 : dtype == TN_BF16 ? 1 : 2;
+        const int et = dtype == TN_F32 ? 0 : dtype == TN_BF16 ? 1 : dtype == TN_F16 ? 2 : 3;
 #define TN_ANY(ET, MK)                                                                                            \
     hipLaunchKernelGGL((k_attn_any<ET, MK>), grid, dim3(256), 0, st, q, k, v, (int)Hq, (int)Hkv, (int)L, (int)S, \
-                       (int)D, sl2, c, out, lse, attn_mask, nullptr, 0)
+                       (int)D, sc, c, out, lse, attn_mask, nullptr, 0)
 #define TN_ANY_MK(ET)                     \
     do {                                  \
         if (mk == 0) TN_ANY(ET, 0);       \
@@ -2214,7 +2232,8 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     } while (0)
         if (et == 0) TN_ANY_MK(0);
         else if (et == 1) TN_ANY_MK(1);
-        else TN_ANY_MK(2);
+        else if (et == 2) TN_ANY_MK(2);
+        else TN_ANY_MK(3);
 #undef TN_ANY_MK
 #undef TN_ANY
         TN_LAUNCHED();
@@ -2350,17 +2369,16 @@ tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_c
         // the plain kernel: one query row per (sequence, head), the cache's cap
         // rows as its keys, each sequence's length from lens
         const double sc = std::isnan(scale) ? 1.0 / std::sqrt((double)D) : scale;
-        const float sl2 = (float)sc * LOG2E;
         const dim3 grid(1u, (unsigned)Hq, (unsigned)B);
         if (dtype == TN_F32)
             hipLaunchKernelGGL((k_attn_any<0, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
-                               (int)cap, (int)D, sl2, 0, out, lse, nullptr, lens, (int)max_len);
+                               (int)cap, (int)D, sc, 0, out, lse, nullptr, lens, (int)max_len);
         else if (dtype == TN_BF16)
             hipLaunchKernelGGL((k_attn_any<1, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
-                               (int)cap, (int)D, sl2, 0, out, lse, nullptr, lens, (int)max_len);
+                               (int)cap, (int)D, sc, 0, out, lse, nullptr, lens, (int)max_len);
         else
             hipLaunchKernelGGL((k_attn_any<2, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
-                               (int)cap, (int)D, sl2, 0, out, lse, nullptr, lens, (int)max_len);
+                               (int)cap, (int)D, sc, 0, out, lse, nullptr, lens, (int)max_len);
         TN_LAUNCHED();
         return TN_OK;
     }
