@@ -122,7 +122,7 @@ def bench_sdpa(tn, L, dtype, steps, warmup, B=1, Hq=9, Hkv=3, S=2048, D=64, seed
     lib = L.lib()
 
     def step():
-        st = lib.tn_sdpa_fwd(None, code, q.data_ptr(), k.data_ptr(), v.data_ptr(), B, Hq, Hkv, S, S, D, None, 0, 1,
+        st = lib.tn_sdpa_fwd(None, code, q.data_ptr(), k.data_ptr(), v.data_ptr(), B, Hq, Hkv, S, S, D, None, 0, None, 1,
                              float("nan"), out.data_ptr(), lse.data_ptr())
         if st:
             L.check(st)

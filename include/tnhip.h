@@ -44,13 +44,15 @@ typedef int tn_status;
 #define TN_EHIP 3     /* RuntimeError from the HIP runtime */
 #define TN_EVALUE 4   /* ValueError (bad blob size, bad argument value) */
 
-/* Element types (torch.float32, torch.bfloat16, torch.float16, torch.float64). */
+/* Element types (torch.float32, torch.bfloat16, torch.float16, torch.float64,
+ * and torch.bool for an attention mask: one byte, nonzero = true). */
 #define TN_F32 0
 #define TN_BF16 1
 #define TN_F16 2
 #define TN_F64 3
+#define TN_BOOL 4
 
-#define TN_ABI_VERSION 1
+#define TN_ABI_VERSION 2
 
 /* ---- errors, probe, counters (err.rs; device.rs:1671-1708 _cuda_counters /
  *      _cuda_probe; vulkan.rs:2138-2268 _vulkan_probe/_ops/_counters) ---- */
@@ -88,6 +90,15 @@ tn_status tn_memset(void* dst, int value, size_t bytes, void* stream);
 tn_status tn_stream_create(void** stream);
 tn_status tn_stream_destroy(void* stream);
 tn_status tn_stream_synchronize(void* stream);
+/* Graph capture of any sequence of calls on a created stream (the HIP-graph
+ * counterpart of the reference's capture.rs:1-35): calls between begin and
+ * end are recorded, not run; end returns an instantiated graph for
+ * tn_graph_launch / tn_graph_destroy. A call that would allocate (a first
+ * call of a shape, or one larger than any before it on this stream) is
+ * refused while capturing; make it once before. Work buffers a graph
+ * captured stay allocated until tn_stream_destroy. */
+tn_status tn_stream_begin_capture(void* stream);
+tn_status tn_stream_end_capture(void* stream, void** graph);
 tn_status tn_device_synchronize(void);
 tn_status tn_event_create(void** event);
 tn_status tn_event_destroy(void* event);
@@ -205,11 +216,18 @@ tn_status tn_q4_k_linear(void* stream, const void* x, int x_dtype, int64_t m, in
  *   GQA: query head h reads key/value head h / (Hq/Hkv), indexed, not
  *   materialised (aten.rs:17106-17126); Hq % Hkv != 0 is refused by name.
  *   is_causal: upper-left aligned, row t attends keys 0..=t (aten.rs:10038-10041).
- *   attn_mask: nullable, [B,Hq,L,S] dense additive, in `mask_dtype` (the query
- *   dtype or TN_F32, aten.rs:10142-10148; others are refused with the
- *   reference's wording), added after scaling (aten.rs:10383-10389). A row
- *   whose every key is masked gives NaN in out and lse, as the reference's
- *   row-max shift does (aten.rs:10392-10420).
+ *   attn_mask: nullable, additive, in `mask_dtype` (the query dtype or TN_F32,
+ *   aten.rs:10142-10148; others are refused with the reference's wording),
+ *   added after scaling (aten.rs:10383-10389). TN_BOOL takes a bool mask as
+ *   F.sdpa's CIA body turns it into an additive one before this op,
+ *   where(mask, 0, -inf) in the query's dtype (bootstrap.py:12918-12925,
+ *   :13065-13066), read in place with no conversion pass. A row whose every
+ *   key is masked gives NaN in out and lse, as the reference's row-max shift
+ *   does (aten.rs:10392-10420).
+ *   mask_strides: nullable host int64[4], the mask's element strides over
+ *   (B, Hq, L, S); a zero stride broadcasts that dim, so a [L, S] or
+ *   [B, 1, L, S] mask is read where it lies, as the reference broadcasts
+ *   the mask onto the scores (aten.rs:10293-10303). NULL: dense [B,Hq,L,S].
  *   scale: NaN selects 1/sqrt(D) (aten.rs:10216).
  *   out: [B,Hq,L,D] in `dtype` (row-major, aten.rs:10436-10437);
  *   lse: nullable f32 [B,Hq,L], logsumexp over the masked, scaled scores.
@@ -222,7 +240,8 @@ tn_status tn_q4_k_linear(void* stream, const void* x, int x_dtype, int64_t m, in
  * probabilities); a head dim past 256 is refused by name. */
 tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, const void* v,
                       int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t S, int64_t D,
-                      const void* attn_mask, int mask_dtype, int is_causal, double scale,
+                      const void* attn_mask, int mask_dtype, const int64_t* mask_strides,
+                      int is_causal, double scale,
                       void* out, float* lse);
 
 /* Decode attention: one query token per sequence over a contiguous

@@ -122,3 +122,60 @@ class Decoder:
             h = (h + linear(act, L["down"], c.hidden, dt).astype(dt)).astype(dt)
         x = rmsnorm(h, self.norm, c.eps, dt)
         return linear(x, self.lm_blob, c.vocab, dt).astype(dt)
+
+
+def linear_rows(x, blob, n, dtype=np.float32, threads=8):
+    """`linear` for every row of x [T, K] at once: row-independent, so equal
+    to T one-row calls (the reference's batched == one-row property,
+    tests/numerics/test_qgemm.py:64-87). float32 runs the C oracle on all
+    rows; float64 forms the same quantised product from the dequantised
+    codes in float64 (each code times its scale is exact there; only the
+    K-term sum rounds)."""
+    x32 = np.ascontiguousarray(x, np.float32)
+    if dtype == np.float32:
+        return O.q4_0_linear(x32, blob, n, threads=threads)
+    T, k = x32.shape
+    xd = O.q8_0_dequantize(O.q8_0_quantize(x32), T * k).reshape(T, k).astype(np.float64)
+    wd = O.q4_0_dequantize(blob, n * k).reshape(n, k).astype(np.float64)
+    return xd @ wd.T
+
+
+def teacher_forced_logits(dec: "Decoder", tokens, want, threads=8) -> dict:
+    """Logits of `dec`'s model at the positions in `want` when `tokens` are
+    fed one per position from 0: the same values as step() called on each
+    token in turn (every op is row-wise except the attention, which sees keys
+    0..t for row t, i.e. upper-left causal over the sequence), computed a
+    whole sequence at a time. Returns {position: logits in dec.dtype}."""
+    c, dt = dec.cfg, dec.dtype
+    Hq, Hkv, D, I = c.n_heads, c.n_kv_heads, c.head_dim, c.inter
+    toks = np.asarray(tokens, np.int64)
+    T = toks.size
+    pos = np.arange(T)
+    h = dec.embed[toks].astype(dt)
+    ang = pos[:, None].astype(dt) * np.asarray(dec.freqs, dt)[None, :]
+    cos, sin = np.cos(ang).astype(dt), np.sin(ang).astype(dt)
+
+    def rope_rows(x):  # x [T, heads, D]
+        half = D // 2
+        x1, x2 = x[..., :half], x[..., half:]
+        cc, ss = cos[:, None, :], sin[:, None, :]
+        return np.concatenate([x1 * cc + (-x2) * ss, x2 * cc + x1 * ss], axis=-1).astype(dt)
+
+    for L in dec.layers:
+        x = rmsnorm(h, L["ln1"], c.eps, dt)
+        qkv = linear_rows(x, L["qkv"], (Hq + 2 * Hkv) * D, dt, threads).astype(dt)
+        q = rope_rows(qkv[:, :Hq * D].reshape(T, Hq, D))
+        k = rope_rows(qkv[:, Hq * D:(Hq + Hkv) * D].reshape(T, Hkv, D))
+        v = qkv[:, (Hq + Hkv) * D:].reshape(T, Hkv, D)
+        a, _ = O.sdpa(q.transpose(1, 0, 2)[None], k.transpose(1, 0, 2)[None], v.transpose(1, 0, 2)[None],
+                      is_causal=True, threads=threads, dtype=dt)
+        a = a[0].transpose(1, 0, 2).reshape(T, Hq * D)
+        h = (h + linear_rows(a, L["o"], c.hidden, dt, threads).astype(dt)).astype(dt)
+        x = rmsnorm(h, L["ln2"], c.eps, dt)
+        gu = linear_rows(x, L["gate_up"], 2 * I, dt, threads).astype(dt)
+        act = silu_mul(gu[:, :I], gu[:, I:], dt)
+        h = (h + linear_rows(act, L["down"], c.hidden, dt, threads).astype(dt)).astype(dt)
+    sel = np.asarray(sorted(set(int(p) for p in want)), np.int64)
+    x = rmsnorm(h[sel], dec.norm, c.eps, dt)
+    logits = linear_rows(x, dec.lm_blob, c.vocab, dt, threads).astype(dt)
+    return {int(p): logits[i] for i, p in enumerate(sel)}

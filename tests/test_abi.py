@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol(L):
 
 
 def test_abi_version_and_op_list(L):
-    assert L.tn_abi_version() == 1
+    assert L.tn_abi_version() == 2
     ops = L.tn_ops().decode()
     assert "torch._C._quantized_linear(q4_0)" in ops
     assert "torch._C._quantized_linear(q8_0)" in ops
@@ -89,7 +89,7 @@ def test_sdpa_refusals_name_the_reason(L):
     def call(dtype=_lib.TN_BF16, mask=None, mask_dtype=0, **kw):
         a = {**args, **kw}
         return L.tn_sdpa_fwd(None, dtype, None, None, None, a["B"], a["Hq"], a["Hkv"], a["L"], a["S"], a["D"],
-                             mask, mask_dtype, 1, float("nan"), None, None)
+                             mask, mask_dtype, None, 1, float("nan"), None, None)
 
     assert call(D=272) == _lib.TN_ENOTIMPL and "head_dim 272" in _lib.last_error()
     assert call(Hkv=4) == _lib.TN_ENOTIMPL and "do not divide" in _lib.last_error()

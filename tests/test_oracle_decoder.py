@@ -105,3 +105,36 @@ def test_model_weights_are_deterministic(n):
     assert all(np.array_equal(a[k], b[k]) for k in a)
     c = OD.layer_weights(SMALL, n, 10)
     assert not np.array_equal(a["qkv"], c["qkv"])
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_a_whole_sequence_at_once_equals_step_by_step(dtype):
+    """The batched teacher-forced run (used to check the full-size model)
+    gives step()'s logits: row-wise ops are row-wise and the attention of row
+    t sees keys 0..t. float32: within a few ulp-sized steps of the logits'
+    scale (the batched C attention sums in the same order, and the q4 linear
+    is row-independent bit for bit); float64 likewise."""
+    cfg = OD.LlamaConfig(n_layers=2, hidden=128, n_heads=6, n_kv_heads=2, head_dim=64, inter=256, vocab=512)
+    toks = [3, 500, 17, 17, 0, 256, 99, 1, 2, 77, 300, 411]
+    dec = OD.Decoder(cfg, 5, 16, dtype)
+    want = {p: dec.step(t, p) for p, t in enumerate(toks)}
+    got = OD.teacher_forced_logits(OD.Decoder(cfg, 5, 16, dtype), toks, range(len(toks)))
+    for p in range(len(toks)):
+        scale = float(np.max(np.abs(want[p])))
+        rel = 1e-5 if dtype == np.float32 else 1e-12
+        assert float(np.max(np.abs(got[p] - want[p]))) <= rel * scale
+
+
+def test_the_float64_linear_rows_is_the_exact_quantised_product():
+    """linear_rows in float64 against the exact dyadic value of the same
+    quantised product (exact_linear_q4_0) within its rounding bound."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((5, 96)).astype(np.float32)
+    w = (rng.standard_normal((40, 96)) * 0.02).astype(np.float32)
+    blob = O.q4_0_quantize(w)
+    got = OD.linear_rows(x, blob, 40, np.float64)
+    value, abs_sum, ref_err = O.exact_linear_q4_0(O.q8_0_quantize(x), blob, 5, 40, 96)
+    assert np.all(np.abs(got - value) <= ref_err + 96 * 2.0 ** -53 * abs_sum)
+    # and the float32 rows are the C oracle's one-row calls, bit for bit
+    f32 = OD.linear_rows(x, blob, 40, np.float32, threads=3)
+    assert all(np.array_equal(f32[i], O.q4_0_linear(x[i:i + 1], blob, 40)[0]) for i in range(5))

@@ -244,7 +244,8 @@ def _quantized_linear(input: Tensor, weight: QTensor, bias: Tensor | None = None
 
 
 def _dt(name):
-    code = {"float32": _lib.TN_F32, "bfloat16": _lib.TN_BF16, "float16": _lib.TN_F16, "float64": _lib.TN_F64}.get(name)
+    code = {"float32": _lib.TN_F32, "bfloat16": _lib.TN_BF16, "float16": _lib.TN_F16, "float64": _lib.TN_F64,
+            "bool": _lib.TN_BOOL}.get(name)
     if code is None:
         raise NotImplementedError(f"dtype {name} has no C ABI code")
     return code
@@ -255,7 +256,7 @@ def _dt(name):
 
 def _scaled_dot_product_flash_attention(query: Tensor, key: Tensor, value: Tensor, dropout_p: float = 0.0,
                                         is_causal: bool = False, *, attn_mask: Tensor | None = None,
-                                        scale: float | None = None):
+                                        scale: float | None = None, _check_only: bool = False):
     """The device half of aten._scaled_dot_product_flash_attention_for_cpu
     (aten.rs:10092-10440). Returns (out, logsumexp); out is row-major
     [B,Hq,L,D] in the query dtype, logsumexp float32 [B,Hq,L]."""
@@ -286,21 +287,37 @@ def _scaled_dot_product_flash_attention(query: Tensor, key: Tensor, value: Tenso
         if t.shape[0] != B or t.shape[2] != S or t.shape[3] != D or t.shape[1] != Hkv:
             raise RuntimeError(f"{op}: query {list(query.shape)} and {name} {list(t.shape)} do not describe one "
                                "attention -- batch, key length and head dimension all have to agree")
-    if attn_mask is not None and tuple(attn_mask.shape) != (B, Hq, L, S):
-        # the kernels read a dense [B, Hq, L, S] mask: a broadcastable one is
-        # materialised first, as the reference's own path does (aten.rs:10293-10303)
-        try:
-            full = np.broadcast_to(attn_mask.bits(), (B, Hq, L, S))
-        except ValueError:
-            raise RuntimeError(f"{op}: attn_mask of shape {list(attn_mask.shape)} cannot be broadcast to "
-                               f"[{B}, {Hq}, {L}, {S}]") from None
-        attn_mask = Tensor.from_numpy(np.ascontiguousarray(full), dtype=attn_mask.dtype, device="hip")
+    if _check_only:
+        return None
+    return _sdpa_call(query, key, value, is_causal, attn_mask, scale)
+
+
+def _mask_strides(op, mask: Tensor, B, Hq, L, S):
+    """Element strides of `mask` (dense in its own shape) broadcast onto
+    [B, Hq, L, S]: numpy's rule, a missing or size-1 dim repeats (stride 0).
+    The reference broadcasts the mask onto the scores the same way
+    (aten.rs:10293-10303); here the kernels read it where it lies."""
+    shape = tuple(mask.shape)
+    if len(shape) > 4 or any(s not in (1, t) for s, t in zip(shape[::-1], (S, L, Hq, B))):
+        raise RuntimeError(f"{op}: attn_mask of shape {list(shape)} cannot be broadcast to [{B}, {Hq}, {L}, {S}]")
+    full = (1,) * (4 - len(shape)) + shape
+    strides, acc = [0] * 4, 1
+    for i in range(3, -1, -1):
+        strides[i] = 0 if full[i] == 1 else acc
+        acc *= full[i]
+    return (ctypes.c_int64 * 4)(*strides)
+
+
+def _sdpa_call(query, key, value, is_causal, attn_mask, scale):
+    B, Hq, L, D = query.shape
+    Hkv, S = key.shape[1], key.shape[2]
+    strides = _mask_strides(SDPA_OP, attn_mask, B, Hq, L, S) if attn_mask is not None else None
     out = Tensor((B, Hq, L, D), query.dtype, "hip")
     lse = Tensor((B, Hq, L), "float64" if query.dtype == "float64" else "float32", "hip")
     sc = float("nan") if scale is None else float(scale)
     check(lib().tn_sdpa_fwd(current_stream(), _dt(query.dtype), query.data_ptr(), key.data_ptr(), value.data_ptr(),
                             B, Hq, Hkv, L, S, D, attn_mask.data_ptr() if attn_mask is not None else None,
-                            _dt(attn_mask.dtype) if attn_mask is not None else 0, int(bool(is_causal)), sc,
+                            _dt(attn_mask.dtype) if attn_mask is not None else 0, strides, int(bool(is_causal)), sc,
                             out.data_ptr(), lse.data_ptr()))
     return out, lse
 
@@ -308,13 +325,24 @@ def _scaled_dot_product_flash_attention(query: Tensor, key: Tensor, value: Tenso
 def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None,
                                  enable_gqa=False):
     """`F.scaled_dot_product_attention` as the reference's CIA body reaches the
-    flash op (bootstrap.py:13036-13080): returns the output only."""
+    flash op (bootstrap.py:13036-13080): returns the output only. A bool mask
+    is taken as the additive where(mask, 0, -inf) in the query's dtype that
+    the CIA body builds before the flash call (bootstrap.py:12918-12925,
+    :13065-13066); the kernels read the bool bytes in place (TN_BOOL), so no
+    converted copy is made."""
     if query.dim() == 4 and key.dim() == 4 and query.shape[1] != key.shape[1] and not enable_gqa:
         raise RuntimeError("scaled_dot_product_attention: query and key head counts differ; pass enable_gqa=True")
     if attn_mask is not None and is_causal:
         raise RuntimeError("_scaled_dot_product_attention: Explicit attn_mask should not be set when is_causal=True")
-    out, _ = _scaled_dot_product_flash_attention(query, key, value, dropout_p, is_causal, attn_mask=attn_mask,
-                                                 scale=scale)
+    if attn_mask is None or attn_mask.dtype != "bool":
+        out, _ = _scaled_dot_product_flash_attention(query, key, value, dropout_p, is_causal, attn_mask=attn_mask,
+                                                     scale=scale)
+        return out
+    # the flash op's own checks, with the mask as the query-dtype tensor it stands for
+    _scaled_dot_product_flash_attention(query, key, value, dropout_p, is_causal, attn_mask=None, scale=scale,
+                                        _check_only=True)
+    _require_hip(SDPA_OP, attn_mask)
+    out, _ = _sdpa_call(query, key, value, is_causal, attn_mask, scale)
     return out
 
 

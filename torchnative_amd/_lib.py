@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtnhip.so")
 
 TN_OK, TN_EINVAL, TN_ENOTIMPL, TN_EHIP, TN_EVALUE = 0, 1, 2, 3, 4
-TN_F32, TN_BF16, TN_F16, TN_F64 = 0, 1, 2, 3
+TN_F32, TN_BF16, TN_F16, TN_F64, TN_BOOL = 0, 1, 2, 3, 4
 TN_PRO_NONE, TN_PRO_RMSNORM, TN_PRO_SILU = 0, 1, 2
 
 # every symbol include/tnhip.h declares, with (restype, argtypes)
@@ -76,6 +76,8 @@ SIGNATURES = {
     "tn_stream_create": (_I, [ctypes.POINTER(_P)]),
     "tn_stream_destroy": (_I, [_P]),
     "tn_stream_synchronize": (_I, [_P]),
+    "tn_stream_begin_capture": (_I, [_P]),
+    "tn_stream_end_capture": (_I, [_P, ctypes.POINTER(_P)]),
     "tn_device_synchronize": (_I, []),
     "tn_event_create": (_I, [ctypes.POINTER(_P)]),
     "tn_event_destroy": (_I, [_P]),
@@ -98,7 +100,7 @@ SIGNATURES = {
     "tn_q4_k_dequantize": (_I, [_P, _P, _I64, _I64, _P]),
     "tn_q4_k_linear": (_I, [_P, _P, _I, _I64, _I64, _P, _I64, _P, _P, _I]),
     "tn_q4_0_linear_decode": (_I, [_P, _P, _I64, _I, _P, _D, _P, _P, _I64, _P, _P]),
-    "tn_sdpa_fwd": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I, _I, _D, _P, _P]),
+    "tn_sdpa_fwd": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I, _P, _I, _D, _P, _P]),
     "tn_sdpa_decode": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _D, _P, _P]),
     "tn_embedding": (_I, [_P, _P, _I64, _P, _I64, _I64, _P]),
     "tn_rmsnorm": (_I, [_P, _P, _I64, _I64, _P, _D, _P]),

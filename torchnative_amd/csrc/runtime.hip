@@ -9,6 +9,8 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
+#include <algorithm>
 
 #include "tn_common.h"
 
@@ -36,14 +38,33 @@ Counters& counters() {
 }
 
 namespace {
+// A stream's scratch. Buffers are never freed while the stream lives: a
+// graph captured from it keeps the addresses it saw, so a buffer outgrown by
+// a later, larger call is retired (kept) rather than freed, and all of them
+// go with tn_stream_destroy. Growth at least doubles, so the retired ones
+// total less than the live one.
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
     uint32_t* tickets = nullptr;  // zeroed counters, returned to zero by their users
     size_t ntickets = 0;
+    std::vector<void*> retired;
+    size_t retired_bytes = 0;
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+// Growth allocates, which a stream under graph capture must not do (and a
+// graph could not replay): refused by name.
+tn_status refuse_if_capturing(hipStream_t stream, const char* what) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    TN_HIP(hipStreamIsCapturing(stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(TN_EINVAL, std::string("tnhip: this call needs more ") + what +
+                                   " than the stream holds, and a stream under graph capture cannot allocate; make "
+                                   "the same call (or a larger one) once before capturing");
+    return TN_OK;
+}
 }  // namespace
 
 tn_status workspace(hipStream_t stream, size_t bytes, void** out) {
@@ -52,17 +73,16 @@ tn_status workspace(hipStream_t stream, size_t bytes, void** out) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace& w = g_ws[{dev, stream}];
     if (w.bytes < bytes) {
-        size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+        TN_TRY(refuse_if_capturing(stream, "workspace"));
+        size_t want = std::max(bytes, std::max((size_t)1 << 20, 2 * w.bytes));
         want = (want + 4095) & ~(size_t)4095;
+        void* p = nullptr;
+        TN_HIP(hipMalloc(&p, want));
         if (w.ptr) {
-            // the old buffer may still be read by work queued on this stream
-            TN_HIP(hipStreamSynchronize(stream));
-            TN_HIP(hipFree(w.ptr));
-            counters().workspace_bytes.fetch_sub(w.bytes);
-            w.ptr = nullptr;
-            w.bytes = 0;
+            w.retired.push_back(w.ptr);
+            w.retired_bytes += w.bytes;
         }
-        TN_HIP(hipMalloc(&w.ptr, want));
+        w.ptr = p;
         w.bytes = want;
         counters().workspace_bytes.fetch_add(want);
     }
@@ -76,22 +96,18 @@ tn_status tickets(hipStream_t stream, size_t n, uint32_t** out) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace& w = g_ws[{dev, stream}];
     if (w.ntickets < n) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        TN_HIP(hipStreamIsCapturing(stream, &cs));
-        if (cs != hipStreamCaptureStatusNone)
-            return fail(TN_EINVAL, "tnhip: the first call that needs the stream's ticket counters cannot be captured "
-                                   "(they are cleared when allocated); make one call before capturing");
-        size_t want = n < 4096 ? 4096 : (n + 4095) & ~(size_t)4095;
-        if (w.tickets) {
-            TN_HIP(hipStreamSynchronize(stream));
-            TN_HIP(hipFree(w.tickets));
-            counters().workspace_bytes.fetch_sub(w.ntickets * 4);
-            w.tickets = nullptr;
-            w.ntickets = 0;
-        }
-        TN_HIP(hipMalloc(reinterpret_cast<void**>(&w.tickets), want * 4));
+        TN_TRY(refuse_if_capturing(stream, "ticket counters"));
+        size_t want = std::max(n, std::max((size_t)4096, 2 * w.ntickets));
+        want = (want + 4095) & ~(size_t)4095;
+        uint32_t* p = nullptr;
+        TN_HIP(hipMalloc(reinterpret_cast<void**>(&p), want * 4));
         // zeroed once, ahead of the first kernel on this stream that takes a ticket
-        TN_HIP(hipMemsetAsync(w.tickets, 0, want * 4, stream));
+        TN_HIP(hipMemsetAsync(p, 0, want * 4, stream));
+        if (w.tickets) {
+            w.retired.push_back(w.tickets);
+            w.retired_bytes += w.ntickets * 4;
+        }
+        w.tickets = p;
         w.ntickets = want;
         counters().workspace_bytes.fetch_add(want * 4);
     }
@@ -288,11 +304,36 @@ tn_status tn_stream_destroy(void* stream) {
                     TN_HIP(hipFree(it->second.tickets));
                     counters().workspace_bytes.fetch_sub(it->second.ntickets * 4);
                 }
+                for (void* r : it->second.retired) TN_HIP(hipFree(r));
+                counters().workspace_bytes.fetch_sub(it->second.retired_bytes);
                 g_ws.erase(it);
             }
         }
         TN_HIP(hipStreamDestroy((hipStream_t)stream));
     }
+    return TN_OK;
+}
+
+tn_status tn_stream_begin_capture(void* stream) {
+    if (!stream) return fail(TN_EVALUE, "tn_stream_begin_capture: the default stream cannot be captured");
+    TN_HIP(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    return TN_OK;
+}
+
+tn_status tn_stream_end_capture(void* stream, void** graph) {
+    if (!graph) return fail(TN_EVALUE, "tn_stream_end_capture: null output");
+    *graph = nullptr;
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture((hipStream_t)stream, &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return hip_fail(e, "hipStreamEndCapture");
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ei != hipSuccess) return hip_fail(ei, "hipGraphInstantiate");
+    *graph = exec;
     return TN_OK;
 }
 

@@ -126,6 +126,56 @@ __device__ inline void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
+// An attention mask as the kernels read it, broadcast by strides: element
+// (b, h, i, j) sits at p[b*sb + h*sh + i*sl + j*sk] (element strides; a zero
+// stride repeats that dim, as aten.rs:10293-10303 broadcasts the mask onto
+// the scores). The kernels' MASK parameter names its format:
+//   1 f32 additive; 2 additive in the 16-bit (or f64) query format;
+//   3 bool (one byte, nonzero = attend), read as where(mask, 0, -inf), which
+//     is the additive mask F.sdpa builds from a bool one
+//     (bootstrap.py:12918-12925, :13065-13066).
+struct MaskRef {
+    const void* p;
+    int64_t sb, sh, sl, sk;
+};
+
+// The additive value of mask element `off` in natural units.
+template <int MASK, bool F16>
+__device__ inline float mask_val(const void* p, int64_t off) {
+    if constexpr (MASK == 1) return reinterpret_cast<const float*>(p)[off];
+    else if constexpr (MASK == 3) return reinterpret_cast<const uint8_t*>(p)[off] ? 0.0f : -INFINITY;
+    else if constexpr (F16) return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[off]);
+    else return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[off]);
+}
+
+// Four consecutive keys key .. key+3 of one mask row (row = the row's element
+// offset); keys at or past S read as 0. One 16-, 8- or 4-byte load when the
+// key dim is dense and the quad is aligned, else four element loads.
+template <int MASK, bool F16>
+__device__ inline f32x4 mask_quad(const MaskRef& m, int64_t row, int key, int S) {
+    constexpr int ES = MASK == 1 ? 4 : MASK == 3 ? 1 : 2;  // element bytes
+    const int64_t off = row + (int64_t)key * m.sk;
+    const char* a = reinterpret_cast<const char*>(m.p) + off * ES;
+    if (m.sk == 1 && key + 3 < S && (reinterpret_cast<uintptr_t>(a) & (4 * ES - 1)) == 0) {
+        if constexpr (MASK == 1) {
+            const float4 v = *reinterpret_cast<const float4*>(a);
+            return (f32x4){v.x, v.y, v.z, v.w};
+        } else if constexpr (MASK == 3) {
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(a);
+            return (f32x4){(v & 0xffu) ? 0.0f : -INFINITY, (v & 0xff00u) ? 0.0f : -INFINITY,
+                           (v & 0xff0000u) ? 0.0f : -INFINITY, (v & 0xff000000u) ? 0.0f : -INFINITY};
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(a);
+            auto w = [](uint32_t h) { return F16 ? f16_to_f32((uint16_t)h) : bf16_to_f32((uint16_t)h); };
+            return (f32x4){w(v.x & 0xffffu), w(v.x >> 16), w(v.y & 0xffffu), w(v.y >> 16)};
+        }
+    }
+    f32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) r[i] = key + i < S ? mask_val<MASK, F16>(m.p, off + (int64_t)i * m.sk) : 0.0f;
+    return r;
+}
+
 
 
 // 16 bytes per lane from a raw buffer straight into LDS (buffer_load_dwordx4
@@ -321,14 +371,15 @@ struct FlashWork {
     uint32_t inl[FLASH_INLINE];  // the table itself when ncls <= FLASH_INLINE
 };
 
-// MASK: 0 none; 1 an f32 additive mask; 2 a bf16 one, dense [B, Hq, L, S]
-// (aten.rs:10383-10389: added to the scaled scores before the row maximum)
+// MASK: 0 none; 1 an f32 additive mask; 2 one in the input format; 3 a bool
+// one (MaskRef), added to the scaled scores before the row maximum
+// (aten.rs:10383-10389)
 template <int D, int MASK = 0, bool F16 = false>
 __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash16(
     const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kg, const uint16_t* __restrict__ Vg, int Hq,
     int Hkv, int L, int S, float sl2, int causal, const FlashWork work, int nsplit, uint16_t* __restrict__ Og,
     float* __restrict__ lse, float* __restrict__ part_o, float2* __restrict__ part_ml, uint32_t* __restrict__ tickets,
-    const void* __restrict__ mask) {
+    const MaskRef mask) {
     constexpr int KG = FlashCfg<D>::KG;        // key groups
     constexpr int BKW = FlashCfg<D>::BKW;      // keys per wave tile
     constexpr int NH = BKW / 32;               // 32-key halves per wave tile
@@ -490,18 +541,12 @@ __global__ __launch_bounds__(128 * FlashCfg<D>::KG) void k_flash16(
                 // scores to log2 units with the mask added: raw*scale*log2e + mask*log2e;
                 // from here on the scale is 1
                 if (qi < L) {
-                    const int64_t mrow = ((int64_t)bh * L + qi) * S;
+                    const int64_t mrow = (int64_t)b * mask.sb + (int64_t)h * mask.sh + (int64_t)qi * mask.sl;
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int key = k0 + 32 * s2 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                        float mv = 0.0f;
-                        if (key < S) {
-                            if constexpr (MASK == 1)
-                                mv = reinterpret_cast<const float*>(mask)[mrow + key];
-                            else
-                                mv = E::widen(reinterpret_cast<const uint16_t*>(mask)[mrow + key]);
-                        }
-                        v[r] = v[r] * sl2 + mv * LOG2E;
+                    for (int rq = 0; rq < 4; rq++) {
+                        const f32x4 mv = mask_quad<MASK, F16>(mask, mrow, k0 + 32 * s2 + 8 * rq + 4 * hh, S);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) v[4 * rq + e] = v[4 * rq + e] * sl2 + mv[e] * LOG2E;
                     }
                 }
             }
@@ -671,12 +716,12 @@ __device__ inline void any_store(void* p, int64_t i, AnyT<ET> v) {
 // lens (decode): nullable device int32 [B]; sequence b then attends keys
 // 0 .. min(lens[b], max_len) - 1 of its S = cap rows. lse is f32, or f64 for
 // f64 inputs. Key tiles are 32 keys (16 for f64, which doubles the LDS).
-// MASK: 0 none; 1 f32; 2 the query's dtype; dense [B, Hq, L, S]
+// MASK: 0 none; 1 f32; 2 the query's dtype; 3 bool (MaskRef)
 template <int ET, int MASK>
 __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, const void* __restrict__ Kg,
                                                   const void* __restrict__ Vg, int Hq, int Hkv, int L, int S, int D,
                                                   double scale, int causal, void* __restrict__ Og,
-                                                  void* __restrict__ lse, const void* __restrict__ mask,
+                                                  void* __restrict__ lse, const MaskRef mask,
                                                   const int32_t* __restrict__ lens, int max_len) {
     using T = AnyT<ET>;
     constexpr int BK = ET == 3 ? 16 : 32;  // keys per tile
@@ -724,10 +769,16 @@ __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, c
             T acc = 0;
             for (int d = 0; d < D; d++) acc = acc + sQ[r * D + d] * sK[j * KP + d];
             T v = acc * sl2;
-            if constexpr (MASK == 1) {
-                if (qi < L && key < S) v = v + (T)reinterpret_cast<const float*>(mask)[(bh * L + qi) * S + key] * log2e;
-            } else if constexpr (MASK == 2) {
-                if (qi < L && key < S) v = v + any_load<ET>(mask, (bh * L + qi) * S + key) * log2e;
+            if constexpr (MASK != 0) {
+                if (qi < L && key < S) {
+                    const int64_t off = (int64_t)b * mask.sb + (int64_t)h * mask.sh + (int64_t)qi * mask.sl +
+                                        (int64_t)key * mask.sk;
+                    T mv;
+                    if constexpr (MASK == 1) mv = (T)reinterpret_cast<const float*>(mask.p)[off];
+                    else if constexpr (MASK == 3) mv = reinterpret_cast<const uint8_t*>(mask.p)[off] ? (T)0 : (T)-INFINITY;
+                    else mv = any_load<ET>(mask.p, off);
+                    v = v + mv * log2e;
+                }
             }
             if (key >= kvalid || (causal && key > qi)) v = -INFINITY;
             sc[i] = v;
@@ -790,14 +841,15 @@ constexpr int PF_BQ = 64, PF_BK = 64;
 // hit 64 distinct banks.
 // ---------------------------------------------------------------------------
 
-// MASK: 1 adds a dense f32 [B, Hq, L, S] mask to the scaled scores (aten.rs:10383-10389)
+// MASK: 1 adds an f32 mask, 3 a bool one (MaskRef), to the scaled scores
+// (aten.rs:10383-10389)
 template <int D, int BK, int MASK = 0>
 __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, const float* __restrict__ Kg,
                                               const float* __restrict__ Vg, int Hq, int Hkv, int L, int S,
                                               float sl2, int causal, int tiles_per, int nsplit,
                                               float* __restrict__ Og, float* __restrict__ lse,
                                               float* __restrict__ part_o, float2* __restrict__ part_ml,
-                                              const float* __restrict__ mask) {
+                                              const MaskRef mask) {
     constexpr int BQ = PF_BQ;
     constexpr int RS = D + 4;
     constexpr int CH = (BK * D / 4) / 256;  // float4 chunks of K (and of V) per thread
@@ -875,15 +927,13 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
         if constexpr (MASK != 0) {
             // scores to log2 units with the mask added; from here on the scale is 1
             if (qi < L) {
-                const int64_t mrow = (((int64_t)b * Hq + h) * L + qi) * S;
+                const int64_t mrow = (int64_t)b * mask.sb + (int64_t)h * mask.sh + (int64_t)qi * mask.sl;
 #pragma unroll
-                for (int kt = 0; kt < BK / 16; kt++)
+                for (int kt = 0; kt < BK / 16; kt++) {
+                    const f32x4 mv = mask_quad<MASK, false>(mask, mrow, k0 + 16 * kt + 4 * g, S);
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int key = k0 + 16 * kt + 4 * g + r;
-                        const float mv = key < S ? mask[mrow + key] : 0.0f;
-                        s[kt][r] = s[kt][r] * sl2 + mv * LOG2E;
-                    }
+                    for (int r = 0; r < 4; r++) s[kt][r] = s[kt][r] * sl2 + mv[r] * LOG2E;
+                }
             }
         }
         const float scl = MASK ? 1.0f : sl2;  // scores' factor to log2 units
@@ -2172,7 +2222,7 @@ extern "C" {
 
 tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, const void* v, int64_t B, int64_t Hq,
                       int64_t Hkv, int64_t L, int64_t S, int64_t D, const void* attn_mask, int mask_dtype,
-                      int is_causal, double scale, void* out, float* lse) {
+                      const int64_t* mask_strides, int is_causal, double scale, void* out, float* lse) {
     if (dtype != TN_F32 && dtype != TN_BF16 && dtype != TN_F16 && dtype != TN_F64)
         return fail(TN_EINVAL, "scaled_dot_product_attention_flash_attention: Expected data type in FP32, FP64, BF16, "
                                "FP16");
@@ -2195,16 +2245,28 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
                       OP, (long long)Hq, (long long)Hkv);
         return fail(TN_ENOTIMPL, buf);
     }
-    // the mask is the query's dtype or float32 (aten.rs:10142-10150)
-    if (attn_mask && mask_dtype != dtype && mask_dtype != TN_F32)
+    // the mask is the query's dtype or float32 (aten.rs:10142-10150), or a
+    // bool one, read as F.sdpa's where(mask, 0, -inf) in the query's dtype
+    if (attn_mask && mask_dtype != dtype && mask_dtype != TN_F32 && mask_dtype != TN_BOOL)
         return fail(TN_EINVAL, "scaled_dot_product_attention_flash_attention: Attention mask is the same data type "
                                "as query");
     // an f64 query with an f32 mask is refused by name (aten.rs:10160-10170)
     if (attn_mask && dtype == TN_F64 && mask_dtype == TN_F32)
         return fail(TN_ENOTIMPL, "aten._scaled_dot_product_flash_attention_for_cpu: a float32 attn_mask on a float64 "
                                  "query is refused. Pass the mask as float64.");
-    // 0 none, 1 f32, 2 the query's dtype: the kernels' MASK parameter
-    const int mk = !attn_mask ? 0 : mask_dtype == TN_F32 ? 1 : 2;
+    // 0 none, 1 f32, 2 the query's dtype, 3 bool: the kernels' MASK parameter
+    const int mk = !attn_mask ? 0 : mask_dtype == TN_F32 ? 1 : mask_dtype == TN_BOOL ? 3 : 2;
+    // element strides over (B, Hq, L, S); null: dense [B, Hq, L, S]
+    MaskRef mref{attn_mask, Hq * L * S, L * S, S, 1};
+    if (attn_mask && mask_strides) {
+        for (int i = 0; i < 4; i++)
+            if (mask_strides[i] < 0)
+                return fail(TN_EVALUE, std::string(OP) + ": attn_mask strides must be non-negative");
+        mref.sb = mask_strides[0];
+        mref.sh = mask_strides[1];
+        mref.sl = mask_strides[2];
+        mref.sk = mask_strides[3];
+    }
     if (D > ANY_DMAX) return refuse_head_dim(D);
     if (B * Hq * L == 0) return TN_OK;  // nothing to write (aten.rs:10242-10259 returns empty zeros)
     if (!q || !k || !v || !out) return fail(TN_EVALUE, std::string(OP) + ": null pointer");
@@ -2223,11 +2285,12 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         const int et = dtype == TN_F32 ? 0 : dtype == TN_BF16 ? 1 : dtype == TN_F16 ? 2 : 3;
 #define TN_ANY(ET, MK)                                                                                            \
     hipLaunchKernelGGL((k_attn_any<ET, MK>), grid, dim3(256), 0, st, q, k, v, (int)Hq, (int)Hkv, (int)L, (int)S, \
-                       (int)D, sc, c, out, lse, attn_mask, nullptr, 0)
+                       (int)D, sc, c, out, lse, mref, nullptr, 0)
 #define TN_ANY_MK(ET)                     \
     do {                                  \
         if (mk == 0) TN_ANY(ET, 0);       \
         else if (mk == 1) TN_ANY(ET, 1);  \
+        else if (mk == 3) TN_ANY(ET, 3);  \
         else TN_ANY(ET, 2);               \
     } while (0)
         if (et == 0) TN_ANY_MK(0);
@@ -2280,11 +2343,12 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
 #define TN_FLASH(DD, MK, H)                                                                                      \
     hipLaunchKernelGGL((k_flash16<DD, MK, H>), dim3((unsigned)nitems), dim3(128 * FlashCfg<DD>::KG), 0, st, qq, kk, \
                        vv, (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, work, nsplit, oo, lse, part_o, part_ml, tick,   \
-                       attn_mask)
+                       mref)
 #define TN_FLASH_MK(DD, H)              \
     do {                                \
         if (mk == 0) TN_FLASH(DD, 0, H); \
         else if (mk == 1) TN_FLASH(DD, 1, H); \
+        else if (mk == 3) TN_FLASH(DD, 3, H); \
         else TN_FLASH(DD, 2, H);        \
     } while (0)
         const bool h16 = dtype == TN_F16;
@@ -2321,22 +2385,20 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         auto kk = static_cast<const float*>(k);
         auto vv = static_cast<const float*>(v);
         auto oo = static_cast<float*>(out);
-        auto mm = static_cast<const float*>(attn_mask);  // an f32 query takes an f32 mask only
+        // an f32 query takes an f32 mask (mk 1) or a bool one (mk 3)
+#define TN_FA(DD, BKK, MK)                                                                                       \
+    hipLaunchKernelGGL((k_fa_f32<DD, BKK, MK>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,   \
+                       (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml, mref)
         if (D == 64) {
-            if (mk)
-                hipLaunchKernelGGL((k_fa_f32<64, 64, 1>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv,
-                                   (int)L, (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml, mm);
-            else
-                hipLaunchKernelGGL((k_fa_f32<64, 64>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
-                                   (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml, nullptr);
+            if (mk == 1) TN_FA(64, 64, 1);
+            else if (mk == 3) TN_FA(64, 64, 3);
+            else TN_FA(64, 64, 0);
         } else {
-            if (mk)
-                hipLaunchKernelGGL((k_fa_f32<128, 32, 1>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv,
-                                   (int)L, (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml, mm);
-            else
-                hipLaunchKernelGGL((k_fa_f32<128, 32>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,
-                                   (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml, nullptr);
+            if (mk == 1) TN_FA(128, 32, 1);
+            else if (mk == 3) TN_FA(128, 32, 3);
+            else TN_FA(128, 32, 0);
         }
+#undef TN_FA
         TN_LAUNCHED();
         if (nsplit > 1) {
             const int64_t row_lo = first_split_row(L, S, c, PF_BQ, bk, tiles_per);
@@ -2372,13 +2434,13 @@ tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_c
         const dim3 grid(1u, (unsigned)Hq, (unsigned)B);
         if (dtype == TN_F32)
             hipLaunchKernelGGL((k_attn_any<0, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
-                               (int)cap, (int)D, sc, 0, out, lse, nullptr, lens, (int)max_len);
+                               (int)cap, (int)D, sc, 0, out, lse, MaskRef{}, lens, (int)max_len);
         else if (dtype == TN_BF16)
             hipLaunchKernelGGL((k_attn_any<1, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
-                               (int)cap, (int)D, sc, 0, out, lse, nullptr, lens, (int)max_len);
+                               (int)cap, (int)D, sc, 0, out, lse, MaskRef{}, lens, (int)max_len);
         else
             hipLaunchKernelGGL((k_attn_any<2, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
-                               (int)cap, (int)D, sc, 0, out, lse, nullptr, lens, (int)max_len);
+                               (int)cap, (int)D, sc, 0, out, lse, MaskRef{}, lens, (int)max_len);
         TN_LAUNCHED();
         return TN_OK;
     }

@@ -27,6 +27,7 @@ DTYPES = {
     "int32": (np.int32, 4, None),
     "int64": (np.int64, 8, None),
     "uint8": (np.uint8, 1, None),
+    "bool": (np.bool_, 1, _lib.TN_BOOL),
 }
 float32, bfloat16, float16, float64 = "float32", "bfloat16", "float16", "float64"
 int32, int64, uint8 = "int32", "int64", "uint8"
@@ -171,7 +172,8 @@ class Tensor:
         if dtype is None:
             dtype = {np.dtype(np.float32): "float32", np.dtype(np.float64): "float64",
                      np.dtype(np.float16): "float16", np.dtype(np.int32): "int32",
-                     np.dtype(np.int64): "int64", np.dtype(np.uint8): "uint8"}.get(arr.dtype)
+                     np.dtype(np.int64): "int64", np.dtype(np.uint8): "uint8",
+                     np.dtype(np.bool_): "bool"}.get(arr.dtype)
             if dtype is None:
                 raise NotImplementedError(f"torchnative_amd: numpy dtype {arr.dtype} has no tensor dtype")
         if dtype == "bfloat16":
