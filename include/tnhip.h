@@ -264,6 +264,23 @@ tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_c
                          int64_t D, const int32_t* lens, int64_t max_len, double scale,
                          void* out, float* lse);
 
+/* tn_sdpa_decode for callers that cannot allocate device memory: code under
+ * HIP graph capture, serving loops and harnesses that forbid hipMalloc. It
+ * has no counterpart in the reference. Same arguments, same kernels and the
+ * same result bit for bit as tn_sdpa_decode; its work buffer (split
+ * partials and the stream-K prefix sums) is a fixed device array of
+ * TN_DECODE_SCRATCH_BYTES per GPU, in the library's own device memory, held
+ * until the process ends. It calls no hipMalloc or hipFree. A call whose
+ * work buffer would exceed the array refuses with TN_EVALUE naming both
+ * sizes (e.g. config 4's B=16, 32/8 heads, head dim 128 needs about 4.5 MB).
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (on different streams) race, so serialise them. */
+#define TN_DECODE_SCRATCH_BYTES (8u << 20)
+tn_status tn_sdpa_decode_noalloc(void* stream, int dtype, const void* q, const void* k_cache,
+                                 const void* v_cache, int64_t B, int64_t Hq, int64_t Hkv, int64_t cap,
+                                 int64_t D, const int32_t* lens, int64_t max_len, double scale,
+                                 void* out, float* lse);
+
 /* ---- decode-step ops ----
  * The per-token aten ops around the linear and the attention in a Llama-style
  * decoder step, f32, as the reference runs them for an f32 model

@@ -102,6 +102,7 @@ SIGNATURES = {
     "tn_q4_0_linear_decode": (_I, [_P, _P, _I64, _I, _P, _D, _P, _P, _I64, _P, _P]),
     "tn_sdpa_fwd": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I, _P, _I, _D, _P, _P]),
     "tn_sdpa_decode": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _D, _P, _P]),
+    "tn_sdpa_decode_noalloc": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _D, _P, _P]),
     "tn_embedding": (_I, [_P, _P, _I64, _P, _I64, _I64, _P]),
     "tn_rmsnorm": (_I, [_P, _P, _I64, _I64, _P, _D, _P]),
     "tn_rope": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),

@@ -1887,6 +1887,45 @@ const char* OP = "aten._scaled_dot_product_flash_attention_for_cpu.default";
 
 }  // namespace
 
+// Where a decode attention call gets its work buffer (partials, prefix sums):
+// the stream's workspace, or the fixed device array of the no-alloc entry.
+using ScratchFn = tn_status (*)(hipStream_t, size_t, void**);
+
+// The no-alloc entry's work buffer: one array per GPU, in the code object's
+// device memory, held until the process ends. Host code never passes the
+// symbol itself (in host code it is a stand-in, not a device address): its
+// device address comes from hipGetSymbolAddress, once per device, with that
+// device current, and is kept per device.
+constexpr size_t DECODE_SCRATCH_BYTES = TN_DECODE_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[DECODE_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, void*> g_scratch_addr;
+
+tn_status static_scratch(hipStream_t, size_t bytes, void** out) {
+    if (bytes > DECODE_SCRATCH_BYTES) {
+        char buf[256];
+        std::snprintf(buf, sizeof buf,
+                      "tn_sdpa_decode_noalloc: this call needs %zu bytes of work buffer, more than the %zu bytes of "
+                      "the fixed device array; use tn_sdpa_decode",
+                      bytes, DECODE_SCRATCH_BYTES);
+        return fail(TN_EVALUE, buf);
+    }
+    int dev = 0;
+    TN_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto it = g_scratch_addr.find(dev);
+    if (it == g_scratch_addr.end()) {
+        void* p = nullptr;
+        TN_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        it = g_scratch_addr.emplace(dev, p).first;
+    }
+    *out = it->second;
+    return TN_OK;
+}
+}  // namespace
+
 // Argument checks of the decode attention (shared with the decode step).
 tn_status decode_check(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, int64_t max_len) {
     if (dtype != TN_BF16 && dtype != TN_F32 && dtype != TN_F16)
@@ -2018,7 +2057,7 @@ namespace {
 template <int D, int NR, bool F16>
 tn_status decode_sk_run(hipStream_t st, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t B,
                         int64_t Hq, int64_t Hkv, int64_t cap, const int32_t* lens, int64_t max_len, float sl2,
-                        uint16_t* out, float* lse) {
+                        uint16_t* out, float* lse, ScratchFn get) {
     const int nrep = (int)(Hq / Hkv);
     const int64_t G = Hkv * (nrep / NR);
     int wgs = 0;
@@ -2029,7 +2068,7 @@ tn_status decode_sk_run(hipStream_t st, const uint16_t* q, const uint16_t* kc, c
     const size_t pm = (size_t)slots * NR * sizeof(float2);
     const size_t pp = (size_t)(B + 1) * sizeof(int);
     void* ws = nullptr;
-    TN_TRY(workspace(st, po + pm + pp, &ws));
+    TN_TRY(get(st, po + pm + pp, &ws));
     float* part_o = static_cast<float*>(ws);
     float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + po);
     int* pref = reinterpret_cast<int*>(static_cast<char*>(ws) + po + pm);
@@ -2046,7 +2085,7 @@ tn_status decode_sk_run(hipStream_t st, const uint16_t* q, const uint16_t* kc, c
 
 tn_status decode_sk_launch(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
                            int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens,
-                           int64_t max_len, double scale, void* out, float* lse) {
+                           int64_t max_len, double scale, void* out, float* lse, ScratchFn get) {
     const bool h16 = dtype == TN_F16;
     const int nrep = (int)(Hq / Hkv);
     const int nr = nrep % 8 == 0 ? 8 : nrep % 4 == 0 ? 4 : nrep % 3 == 0 ? 3 : nrep % 2 == 0 ? 2 : 1;
@@ -2057,8 +2096,8 @@ tn_status decode_sk_launch(hipStream_t st, int dtype, const void* q, const void*
     auto vv = static_cast<const uint16_t*>(v_cache);
     auto oo = static_cast<uint16_t*>(out);
 #define TN_SK(DD, NR)                                                                                          \
-    return h16 ? decode_sk_run<DD, NR, true>(st, qq, kk, vv, B, Hq, Hkv, cap, lens, max_len, sl2, oo, lse)    \
-               : decode_sk_run<DD, NR, false>(st, qq, kk, vv, B, Hq, Hkv, cap, lens, max_len, sl2, oo, lse)
+    return h16 ? decode_sk_run<DD, NR, true>(st, qq, kk, vv, B, Hq, Hkv, cap, lens, max_len, sl2, oo, lse, get) \
+               : decode_sk_run<DD, NR, false>(st, qq, kk, vv, B, Hq, Hkv, cap, lens, max_len, sl2, oo, lse, get)
 #define TN_SK_D(DD)                    \
     switch (nr) {                      \
         case 8: TN_SK(DD, 8);          \
@@ -2417,9 +2456,14 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     return TN_OK;
 }
 
-tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_cache, const void* v_cache, int64_t B,
-                         int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens, int64_t max_len,
-                         double scale, void* out, float* lse) {
+}  // extern "C"
+
+namespace {
+
+// tn_sdpa_decode and its no-alloc twin: the same kernels, the work buffer from `get`.
+tn_status decode_entry(void* stream, int dtype, const void* q, const void* k_cache, const void* v_cache, int64_t B,
+                       int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens, int64_t max_len,
+                       double scale, void* out, float* lse, ScratchFn get) {
     tn_status s = decode_check(dtype, B, Hq, Hkv, cap, D, max_len);
     if (s != TN_OK || B == 0 || Hq == 0) return s;
     if (!q || !k_cache || !v_cache || !out || !lens) return fail(TN_EVALUE, "sdpa_decode: null pointer");
@@ -2447,7 +2491,8 @@ tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_c
     // the stream-K kernel counts 16-key units of all segments in an int
     const bool half = dtype == TN_BF16 || dtype == TN_F16;
     if (half && B <= SK_MAXB && B * Hq * cdiv(max_len, SK_UNIT) <= INT32_MAX)
-        return decode_sk_launch(st, dtype, q, k_cache, v_cache, B, Hq, Hkv, cap, D, lens, max_len, scale, out, lse);
+        return decode_sk_launch(st, dtype, q, k_cache, v_cache, B, Hq, Hkv, cap, D, lens, max_len, scale, out, lse,
+                                get);
     // the split kernel below takes the row maximum before scaling
     if (half && scale < 0.0)
         return fail(TN_ENOTIMPL, "sdpa_decode: a negative scale is not implemented on the hip device for more than 1024 "
@@ -2455,11 +2500,34 @@ tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_c
     const int64_t nsplit = cdiv(max_len, DEC_SPLIT);
     const size_t po = (size_t)B * Hq * nsplit * D * sizeof(float);
     const size_t pm = (size_t)B * Hq * nsplit * sizeof(float2);
+    // the single-pass f32 kernel takes no partials
+    const bool one_pass = dtype == TN_F32 && max_len <= DEC1_MAX_KEYS;
     void* ws = nullptr;
-    s = workspace(st, po + pm, &ws);
-    if (s != TN_OK) return s;
+    if (!one_pass) {
+        s = get(st, po + pm, &ws);
+        if (s != TN_OK) return s;
+    }
+    float2* part_ml = ws ? reinterpret_cast<float2*>(static_cast<char*>(ws) + po) : nullptr;
     return decode_launch(st, dtype, q, k_cache, v_cache, B, Hq, Hkv, cap, D, lens, max_len, scale, out, lse,
-                         static_cast<float*>(ws), reinterpret_cast<float2*>(static_cast<char*>(ws) + po));
+                         static_cast<float*>(ws), part_ml);
+}
+
+}  // namespace
+
+extern "C" {
+
+tn_status tn_sdpa_decode(void* stream, int dtype, const void* q, const void* k_cache, const void* v_cache, int64_t B,
+                         int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens, int64_t max_len,
+                         double scale, void* out, float* lse) {
+    return decode_entry(stream, dtype, q, k_cache, v_cache, B, Hq, Hkv, cap, D, lens, max_len, scale, out, lse,
+                        workspace);
+}
+
+tn_status tn_sdpa_decode_noalloc(void* stream, int dtype, const void* q, const void* k_cache, const void* v_cache,
+                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens,
+                                 int64_t max_len, double scale, void* out, float* lse) {
+    return decode_entry(stream, dtype, q, k_cache, v_cache, B, Hq, Hkv, cap, D, lens, max_len, scale, out, lse,
+                        static_scratch);
 }
 
 }  // extern "C"
