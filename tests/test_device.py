@@ -1,9 +1,9 @@
-"""The `hip` device member (torchnative/python/torchnative/device/__init__.py
-:118-165, :307-361, :479-503): availability is measured by tn_probe, an
-unavailable device carries a named reason, `require()` raises naming it, and
-on the GPU the member is available with the probe's detail and its counters
-move with the work -- the checks tests/devices/cuda/test_cuda.py makes of the
-CUDA member."""
+"""The hip device's availability: measured by running tn_probe, a negative
+answer carries one of the reason codes, `ensure()` raises with that code, a
+missing library reads as `not_built` (never a fallback), and on the GPU the
+device is usable with the probe's properties and its counters move with the
+work -- the checks the reference's tests/devices/cuda/test_cuda.py makes of
+its CUDA member."""
 
 import numpy as np
 import pytest
@@ -12,42 +12,41 @@ from torchnative_amd import _lib
 from torchnative_amd import device as D
 
 
-def test_availability_records_follow_the_rules():
-    with pytest.raises(ValueError, match="kind"):
-        D.Availability("hip", True, "x", "guessed")
-    with pytest.raises(ValueError, match="must not carry"):
-        D.Availability("hip", True, "x", "measured", reason="no_driver")
-    with pytest.raises(ValueError, match="without a named reason"):
-        D.Availability("hip", False, "x", "measured")
-    a = D.Availability("hip", False, "x", "declared", reason="not_built", detail={"k": 1})
-    assert a.as_dict() == {"device": "hip", "available": False, "reason": "not_built", "source": "x",
-                           "kind": "declared", "detail": {"k": 1}}
+def test_a_probe_result_carries_a_reason_exactly_when_unusable():
+    with pytest.raises(ValueError, match="exactly one"):
+        D.ProbeResult(True, "no_driver")
+    with pytest.raises(ValueError, match="exactly one"):
+        D.ProbeResult(False)
+    with pytest.raises(ValueError, match="unknown reason code"):
+        D.ProbeResult(False, "tired")
+    assert D.ProbeResult(False, "no_device", {"error": "x"}).props == {"error": "x"}
 
 
-def test_the_answer_is_measured_and_names_its_reason():
-    a = D.hip.availability()
-    assert a.kind == "measured" and a.source.startswith("tn_probe")
-    if not a.available:
-        assert a.reason in D.REASONS
-        with pytest.raises(D.DeviceUnavailable, match=f"reason: {a.reason}"):
-            D.hip.require()
-    rep = D.report()
-    assert set(rep) == {"hip"} and rep["hip"]["eager"] is True and D.members() == (D.hip,)
+def test_the_answer_comes_from_the_probe_and_names_its_reason():
+    r = D.probe()
+    st = D.hip.status()
+    assert st["usable"] == r.usable and st["eager"] is True and set(D.report()) == {"hip"}
+    if not r.usable:
+        assert r.reason in D.REASONS
+        with pytest.raises(D.DeviceUnavailable) as e:
+            D.hip.ensure()
+        assert e.value.reason == r.reason and r.reason in str(e.value)
+        assert not D.hip.is_available()
 
 
 def test_a_missing_library_is_not_built_not_a_fallback(monkeypatch):
     monkeypatch.setattr(_lib, "LIB_PATH", "/nonexistent/libtnhip.so")
     monkeypatch.setattr(_lib, "_lib", None)
-    a = D.hip.availability()
-    assert not a.available and a.reason == "not_built" and "no host fallback" in a.detail["error"]
+    r = D.probe()
+    assert not r.usable and r.reason == "not_built" and "no host fallback" in r.props["error"]
 
 
 @pytest.mark.gpu
-def test_on_the_gpu_the_member_is_available_and_counts_its_work():
+def test_on_the_gpu_the_device_is_usable_and_counts_its_work():
     import torchnative_amd as tn
 
-    a = D.hip.require().availability()
-    assert a.available and a.reason is None and a.detail["arch"].startswith("gfx950")
+    r = D.hip.ensure()
+    assert r.usable and r.reason is None and r.props["arch"].startswith("gfx950") and D.hip.is_available()
     assert "torch._C._quantized_linear(q4_k)" in ",".join(D.hip.ops())
     tn._C._hip_counters_reset()
     before = D.hip.counters()

@@ -1,107 +1,105 @@
-"""The `hip` member of the device namespace.
+"""Is the hip device usable in this process, and if not, why not.
 
-Mirrors torchnative/python/torchnative/device/__init__.py: the availability
-record (`Availability`, :118-165) with its rules (an available device carries
-no reason; an unavailable one carries a *name*, never prose alone; `kind`
-says whether the answer was measured or declared), the eager device with
-`available` / `require()` / `report()` (:307-361), the CUDA member that
-passes its probe's reason through unchanged (:479-503), and `members()` /
-`report()` (:789-803). The answer comes from `tn_probe` (include/tnhip.h),
-which runs the HIP runtime, so it is always "measured".
+The answer comes from running the library's own probe (`tn_probe`,
+include/tnhip.h), which asks the HIP runtime for the current device and
+checks that it is a gfx950; nothing is inferred from the environment. A
+negative answer always carries one of four reason codes, so callers and
+tests can branch on the code rather than parse prose:
 
-Reasons:
   not_built   libtnhip.so has not been built (there is no host fallback);
   no_driver   the HIP runtime cannot enumerate devices;
   no_device   the runtime sees no GPU;
   wrong_arch  the current GPU is not a gfx950 (the library is built for it only).
+
+The reference's device namespace (torchnative/python/torchnative/device)
+would take this as one more member: INTEGRATION.md shows the small class it
+would register, which forwards its availability question to `probe()`.
 """
 
 from __future__ import annotations
 
 import re
+from dataclasses import dataclass, field
 
 from . import _lib
 
-__all__ = ["Availability", "DeviceUnavailable", "HipDevice", "hip", "members", "report"]
+__all__ = ["ProbeResult", "DeviceUnavailable", "probe", "hip", "report", "REASONS"]
 
 REASONS = ("not_built", "no_driver", "no_device", "wrong_arch")
 
 
 class DeviceUnavailable(RuntimeError):
-    """This device is not usable in this process; the message names why."""
+    """The hip device cannot be used here; `.reason` holds the code."""
+
+    def __init__(self, reason: str, message: str):
+        super().__init__(message)
+        self.reason = reason
 
 
-class Availability:
-    """One availability answer and what produced it."""
+@dataclass(frozen=True)
+class ProbeResult:
+    """One run of the probe. `props` holds what tn_probe reported about the
+    device (name, arch, CUs, HBM bytes, clock, device count) when usable,
+    or the error text under "error" when not."""
 
-    __slots__ = ("device", "available", "reason", "source", "kind", "detail")
+    usable: bool
+    reason: str | None = None
+    props: dict = field(default_factory=dict)
 
-    def __init__(self, device, available, source, kind, reason=None, detail=None):
-        if kind not in ("measured", "declared"):
-            raise ValueError(f"kind must be 'measured' or 'declared', got {kind!r}")
-        if available and reason is not None:
-            raise ValueError("an available device must not carry a refusal reason")
-        if not available and not reason:
-            raise ValueError(f"{device}: unavailable without a named reason")
-        self.device, self.available, self.reason = device, bool(available), reason
-        self.source, self.kind, self.detail = source, kind, dict(detail or {})
-
-    def as_dict(self):
-        return {"device": self.device, "available": self.available, "reason": self.reason, "source": self.source,
-                "kind": self.kind, "detail": self.detail}
-
-    def __repr__(self):
-        state = "available" if self.available else f"unavailable ({self.reason})"
-        return f"<Availability {self.device}: {state} via {self.source} [{self.kind}]>"
+    def __post_init__(self):
+        if self.usable == (self.reason is not None):
+            raise ValueError("a usable probe has no reason code and an unusable one has exactly one")
+        if self.reason is not None and self.reason not in REASONS + ("unclassified",):
+            raise ValueError(f"unknown reason code {self.reason!r}")
 
 
-class HipDevice:
-    """The MI355X (gfx950) behind libtnhip: an eager tensor destination."""
+def probe() -> ProbeResult:
+    """Run tn_probe now and classify the outcome."""
+    try:
+        _lib.lib()
+    except _lib.HipLibraryMissing as e:
+        return ProbeResult(False, "not_built", {"error": str(e)})
+    from ._C import _hip_probe
 
-    __slots__ = ()
-    type = "hip"
-    eager = True
-    source = "tn_probe (libtnhip)"
+    try:
+        return ProbeResult(True, None, _hip_probe())
+    except NotImplementedError as e:
+        text = str(e)
+        code = re.match(r"tnhip: (\w+):", text)
+        reason = code.group(1) if code and code.group(1) in REASONS else "unclassified"
+        return ProbeResult(False, reason, {"error": text})
 
-    def availability(self) -> Availability:
-        try:
-            L = _lib.lib()
-        except _lib.HipLibraryMissing as e:
-            return Availability("hip", False, self.source, "measured", reason="not_built", detail={"error": str(e)})
-        from ._C import _hip_probe
 
-        try:
-            probe = _hip_probe()
-        except NotImplementedError as e:
-            msg = str(e)
-            m = re.search(r"tnhip: (\w+):", msg)
-            reason = m.group(1) if m and m.group(1) in REASONS else "unclassified"
-            return Availability("hip", False, self.source, "measured", reason=reason, detail={"error": msg})
-        del L
-        return Availability("hip", True, self.source, "measured", detail=probe)
+class _Hip:
+    """`torchnative_amd.device.hip`: the MI355X behind libtnhip, an eager
+    device (every op runs when called; nothing is traced)."""
 
-    @property
-    def available(self) -> bool:
-        return self.availability().available
+    name = "hip"
 
-    def require(self) -> "HipDevice":
-        """Return self, or raise DeviceUnavailable naming the reason."""
-        a = self.availability()
-        if not a.available:
-            raise DeviceUnavailable(f"torchnative_amd.device.hip is not available in this process -- reason: "
-                                    f"{a.reason} (probe: {a.source})")
-        return self
+    def is_available(self) -> bool:
+        return probe().usable
 
-    def report(self) -> dict:
-        return {"type": self.type, "eager": self.eager, **self.availability().as_dict()}
+    def ensure(self) -> ProbeResult:
+        """The probe result if the device is usable, else DeviceUnavailable
+        carrying the reason code."""
+        r = probe()
+        if not r.usable:
+            raise DeviceUnavailable(r.reason, f"hip device unusable ({r.reason}): {r.props.get('error', '')}")
+        return r
 
-    # what the reference's `_cuda_counters` / `_vulkan_ops` expose for residency tests
+    def status(self) -> dict:
+        r = probe()
+        return {"device": self.name, "usable": r.usable, "reason": r.reason, "eager": True, **r.props}
+
     def counters(self) -> dict:
+        """Launches, uploads, host readbacks, refusals and workspace bytes
+        since the last reset (tn_counters)."""
         from ._C import _hip_counters
 
         return _hip_counters()
 
     def ops(self) -> list:
+        """The op names this backend executes (tn_ops); anything else is refused."""
         from ._C import _hip_ops
 
         return _hip_ops()
@@ -112,16 +110,12 @@ class HipDevice:
         synchronize()
 
     def __repr__(self):
-        return "torchnative_amd.device.hip (eager)"
+        return "<torchnative_amd.device.hip>"
 
 
-hip = HipDevice()
-
-
-def members():
-    """Every device this package provides, in a stable order."""
-    return (hip,)
+hip = _Hip()
 
 
 def report() -> dict:
-    return {d.type: d.report() for d in members()}
+    """The status of every device this package provides, by name."""
+    return {hip.name: hip.status()}

@@ -1,21 +1,25 @@
-"""GGUF checkpoints for the hip device: the container and the loaders that put
-a file's tensors on the device.
+"""GGUF checkpoints for the hip device.
 
-Mirrors torchnative/python/torchnative/gguf: `GGUFFile` (reader.py:306-492),
-the GGML type table and its refusals (reader.py:111-166), `load_tensor`
-(__init__.py:135-170) and `quantized_linear` (__init__.py:173-201). As in the
-reference, block tensors are never decoded or re-encoded on the way in: the
-file's GGML blocks go byte for byte to `_quantized_from_blob`, which on this
-backend splits them into the device's code and scale planes
-(tn_q4_0_from_blob / tn_q8_0_from_blob / tn_q4_k_from_blob), so `_quantized_blob` of a loaded
-weight returns the file's bytes.
+What the reference does with a GGUF file (torchnative/python/torchnative/gguf,
+`load_tensor` at __init__.py:135-170 and `quantized_linear` at :173-201) is:
+read the container, hand dense tensors over in their own dtype, and hand
+block tensors over as their GGML blocks, never decoded on the way in. This
+module does the same for the hip device: a block tensor's bytes go to
+`_quantized_from_blob`, which splits them into the device's code and scale
+planes (tn_q4_0_from_blob, tn_q8_0_from_blob, tn_q4_k_from_blob), so
+`_quantized_blob` of a loaded weight gives back the file's bytes.
 
-The container is read with `mmap` and `struct` only. Layout (GGUF v2/v3,
-little-endian): magic "GGUF", u32 version, u64 tensor count, u64 key/value
-count; key/value pairs (string key, u32 value type, value); tensor descriptors
-(string name, u32 n_dims, u64 ne[n_dims] fastest-varying first, u32 GGML type,
-u64 data offset); padding to `general.alignment` (default 32); tensor data.
-Strings are a u64 byte length and the bytes.
+The container, as the GGUF specification lays it out (v2 and v3, little
+endian): a 24-byte header (b"GGUF", u32 version, u64 tensor count, u64
+metadata count); the metadata pairs (string key, u32 value type, value); the
+tensor descriptors (string name, u32 dimension count, u64 extents fastest
+first, u32 GGML type, u64 offset into the data section); zero padding to
+`general.alignment` (32 when absent); the data section. A string is a u64
+byte count and the bytes; an array is a u32 element type, a u64 count and
+the elements.
+
+The file is memory-mapped; `scan` walks it once, checking every read against
+the file's size, and everything after that is a slice of the map.
 """
 
 from __future__ import annotations
@@ -23,125 +27,131 @@ from __future__ import annotations
 import mmap
 import os
 import struct
+from dataclasses import dataclass
+from typing import NamedTuple, Optional
 
 import numpy as np
 
-__all__ = ["GGUFFile", "GGUFTensorInfo", "GGML_TYPES", "GGUFFormatError", "UnsupportedGGUF", "type_name",
-           "refusal", "load_tensor", "quantized_linear"]
-
-_MAGIC = b"GGUF"
-_DEFAULT_ALIGNMENT = 32
-_MAX_DIMS = 4
+__all__ = ["GGUFFile", "GGUFTensorInfo", "TensorEntry", "GGMLType", "GGML_TYPES", "GGUFFormatError",
+           "UnsupportedGGUF", "type_name", "refusal", "load_tensor", "quantized_linear"]
 
 
 class GGUFFormatError(ValueError):
-    """The bytes are not a well-formed GGUF file."""
+    """The bytes break the GGUF layout."""
 
 
 class UnsupportedGGUF(NotImplementedError):
-    """A well-formed GGUF construct that is refused, with the reason."""
+    """Valid GGUF that this backend does not load; the message says why."""
 
 
-# Why a type is not loaded. The first four follow the reference's four refusal
-# kinds (reader.py:83-108); the last is this backend's own: a block format the
-# reference holds whose kernels the hip device does not have.
-_WHY = {
-    "activation": ("is an activation-side block format (the right-hand operand llama.cpp builds inside "
-                   "vec_dot), never a stored weight; `_quantize` refuses it as a weight for the same reason."),
-    "no_candle": ("has no candle GgmlDType, so the reference has no storage or kernel for it; re-quantise the "
-                  "model to q8_0 or q4_0 for this backend."),
-    "not_wired": "is a plain numeric type no checkpoint uses for weights; it is not wired and not guessed at.",
-    "removed": "is a repacked layout ggml dropped from the file format; a file carrying it is not read.",
-    "not_on_hip": ("is a block format the reference holds, but the hip device implements only q4_0, q8_0 and "
-                   "q4_k blocks; re-quantise to one of them."),
-}
+class GGMLType(NamedTuple):
+    """One row of the GGML type table. `load` is "dense" (read as `what`, a
+    dtype), "blocks" (kept as the quantised format `what`) or "no" (refused;
+    `what` keys the reason)."""
 
-# GGML type id -> (name, elements per block, bytes per block, kind, dtype / format / refusal key).
-# Ids, block sizes and byte sizes are the file format's (ggml.c type_traits).
-GGML_TYPES = {
-    0: ("F32", 1, 4, "dense", "float32"),
-    1: ("F16", 1, 2, "dense", "float16"),
-    30: ("BF16", 1, 2, "dense", "bfloat16"),
-    2: ("Q4_0", 32, 18, "block", "q4_0"),
-    8: ("Q8_0", 32, 34, "block", "q8_0"),
-    3: ("Q4_1", 32, 20, "refused", "not_on_hip"),
-    6: ("Q5_0", 32, 22, "refused", "not_on_hip"),
-    7: ("Q5_1", 32, 24, "refused", "not_on_hip"),
-    10: ("Q2_K", 256, 84, "refused", "not_on_hip"),
-    11: ("Q3_K", 256, 110, "refused", "not_on_hip"),
-    12: ("Q4_K", 256, 144, "block", "q4_k"),
-    13: ("Q5_K", 256, 176, "refused", "not_on_hip"),
-    14: ("Q6_K", 256, 210, "refused", "not_on_hip"),
-    9: ("Q8_1", 32, 36, "refused", "activation"),
-    15: ("Q8_K", 256, 292, "refused", "activation"),
-    16: ("IQ2_XXS", 256, 66, "refused", "no_candle"),
-    17: ("IQ2_XS", 256, 74, "refused", "no_candle"),
-    18: ("IQ3_XXS", 256, 98, "refused", "no_candle"),
-    19: ("IQ1_S", 256, 50, "refused", "no_candle"),
-    20: ("IQ4_NL", 32, 18, "refused", "no_candle"),
-    21: ("IQ3_S", 256, 110, "refused", "no_candle"),
-    22: ("IQ2_S", 256, 82, "refused", "no_candle"),
-    23: ("IQ4_XS", 256, 136, "refused", "no_candle"),
-    29: ("IQ1_M", 256, 56, "refused", "no_candle"),
-    34: ("TQ1_0", 256, 54, "refused", "no_candle"),
-    35: ("TQ2_0", 256, 66, "refused", "no_candle"),
-    39: ("MXFP4", 32, 17, "refused", "no_candle"),
-    24: ("I8", 1, 1, "refused", "not_wired"),
-    25: ("I16", 1, 2, "refused", "not_wired"),
-    26: ("I32", 1, 4, "refused", "not_wired"),
-    27: ("I64", 1, 8, "refused", "not_wired"),
-    28: ("F64", 1, 8, "refused", "not_wired"),
-    31: ("Q4_0_4_4", None, None, "refused", "removed"),
-    32: ("Q4_0_4_8", None, None, "refused", "removed"),
-    33: ("Q4_0_8_8", None, None, "refused", "removed"),
-    36: ("IQ4_NL_4_4", None, None, "refused", "removed"),
-    37: ("IQ4_NL_4_8", None, None, "refused", "removed"),
-    38: ("IQ4_NL_8_8", None, None, "refused", "removed"),
+    id: int
+    name: str
+    block: Optional[int]  # elements per block
+    size: Optional[int]  # bytes per block
+    load: str
+    what: str
+
+
+# The GGML type ids with their elements and bytes per block are the file
+# format's own (ggml's type traits); a reader has to agree with them exactly.
+GGML_TYPES = {t.id: t for t in (GGMLType(*row) for row in (
+    (0, "F32", 1, 4, "dense", "float32"),
+    (1, "F16", 1, 2, "dense", "float16"),
+    (2, "Q4_0", 32, 18, "blocks", "q4_0"),
+    (3, "Q4_1", 32, 20, "no", "other_blocks"),
+    (6, "Q5_0", 32, 22, "no", "other_blocks"),
+    (7, "Q5_1", 32, 24, "no", "other_blocks"),
+    (8, "Q8_0", 32, 34, "blocks", "q8_0"),
+    (9, "Q8_1", 32, 36, "no", "rhs_only"),
+    (10, "Q2_K", 256, 84, "no", "other_blocks"),
+    (11, "Q3_K", 256, 110, "no", "other_blocks"),
+    (12, "Q4_K", 256, 144, "blocks", "q4_k"),
+    (13, "Q5_K", 256, 176, "no", "other_blocks"),
+    (14, "Q6_K", 256, 210, "no", "other_blocks"),
+    (15, "Q8_K", 256, 292, "no", "rhs_only"),
+    (16, "IQ2_XXS", 256, 66, "no", "iq"),
+    (17, "IQ2_XS", 256, 74, "no", "iq"),
+    (18, "IQ3_XXS", 256, 98, "no", "iq"),
+    (19, "IQ1_S", 256, 50, "no", "iq"),
+    (20, "IQ4_NL", 32, 18, "no", "iq"),
+    (21, "IQ3_S", 256, 110, "no", "iq"),
+    (22, "IQ2_S", 256, 82, "no", "iq"),
+    (23, "IQ4_XS", 256, 136, "no", "iq"),
+    (24, "I8", 1, 1, "no", "integer"),
+    (25, "I16", 1, 2, "no", "integer"),
+    (26, "I32", 1, 4, "no", "integer"),
+    (27, "I64", 1, 8, "no", "integer"),
+    (28, "F64", 1, 8, "no", "integer"),
+    (29, "IQ1_M", 256, 56, "no", "iq"),
+    (30, "BF16", 1, 2, "dense", "bfloat16"),
+    (31, "Q4_0_4_4", None, None, "no", "retired"),
+    (32, "Q4_0_4_8", None, None, "no", "retired"),
+    (33, "Q4_0_8_8", None, None, "no", "retired"),
+    (34, "TQ1_0", 256, 54, "no", "iq"),
+    (35, "TQ2_0", 256, 66, "no", "iq"),
+    (36, "IQ4_NL_4_4", None, None, "no", "retired"),
+    (37, "IQ4_NL_4_8", None, None, "no", "retired"),
+    (38, "IQ4_NL_8_8", None, None, "no", "retired"),
+    (39, "MXFP4", 32, 17, "no", "iq"),
+))}
+
+# Why a type is not loaded on this backend.
+_WHY_NOT = {
+    "other_blocks": "is a block format with no hip kernel here; the hip device runs q4_0, q8_0 and q4_k "
+                    "blocks, so re-quantise the model to one of those",
+    "rhs_only": "only ever exists as the quantised activation inside a block dot product, so no weight is "
+                "stored in it",
+    "iq": "has no storage type in the reference's candle either; re-quantise the model to q4_0, q8_0 or q4_k",
+    "integer": "is a plain numeric element type that checkpoints do not use for weights; it is not loaded",
+    "retired": "is an interleaved layout that ggml no longer writes; its files have to be re-converted",
 }
 
 
 def type_name(ggml_type: int) -> str:
     t = GGML_TYPES.get(ggml_type)
-    return t[0] if t else f"<unknown GGML type id {ggml_type}>"
+    return t.name if t else f"unknown#{ggml_type}"
 
 
 def refusal(ggml_type: int, tensor_name: str | None = None):
-    """The UnsupportedGGUF for a type that is not loaded here, else None."""
-    where = f" (tensor {tensor_name!r})" if tensor_name else ""
+    """The UnsupportedGGUF a tensor of this type would raise, or None if it loads."""
+    subject = f"tensor {tensor_name!r}" if tensor_name is not None else "a tensor"
     t = GGML_TYPES.get(ggml_type)
     if t is None:
-        return UnsupportedGGUF(f"GGML type id {ggml_type}{where} is unknown to this reader; it is refused rather "
-                               "than read as some other type.")
-    if t[3] == "refused":
-        return UnsupportedGGUF(f"GGML type {t[0]}{where} {_WHY[t[4]]}")
+        return UnsupportedGGUF(f"{subject} has GGML type id {ggml_type}, which is not in this reader's table; "
+                               "nothing is guessed about its layout")
+    if t.load == "no":
+        return UnsupportedGGUF(f"{subject} is {t.name}, which {_WHY_NOT[t.what]}")
     return None
 
 
-# GGUF metadata value types: id -> struct code (8 = string, 9 = array)
-_SCALAR = {0: "B", 1: "b", 2: "H", 3: "h", 4: "I", 5: "i", 6: "f", 7: "?", 10: "Q", 11: "q", 12: "d"}
-_STRING, _ARRAY = 8, 9
+@dataclass(frozen=True)
+class TensorEntry:
+    """One tensor descriptor. `ne` is GGUF's order (fastest first); `shape`
+    is torch's (reversed), so a linear weight with ne = [in, out] has shape
+    (out, in). `offset` is absolute in the file. `nbytes` is None when the
+    type's size is not known (the tensor is listed but never read)."""
 
+    name: str
+    ggml_type: int
+    ne: tuple
+    offset: int
+    nbytes: Optional[int]
 
-class ArrayValue(list):
-    """A GGUF array value; `element_type` keeps the GGUF element type id."""
+    @property
+    def shape(self) -> tuple:
+        return tuple(reversed(self.ne))
 
-    def __init__(self, element_type, items):
-        super().__init__(items)
-        self.element_type = element_type
-
-
-class GGUFTensorInfo:
-    """One tensor descriptor. `shape` is in torch order (GGUF's `ne`
-    reversed), so a linear weight stored as ne = [in, out] is (out, in).
-    `offset` is absolute in the file; `nbytes` is None for a type of unknown
-    size (listed, never read)."""
-
-    __slots__ = ("name", "ggml_type", "ne", "shape", "offset", "nbytes", "n_elements")
-
-    def __init__(self, name, ggml_type, ne, offset, nbytes, n_elements):
-        self.name, self.ggml_type, self.ne = name, ggml_type, tuple(ne)
-        self.shape = tuple(reversed(self.ne))
-        self.offset, self.nbytes, self.n_elements = offset, nbytes, n_elements
+    @property
+    def n_elements(self) -> int:
+        n = 1
+        for d in self.ne:
+            n *= d
+        return n
 
     @property
     def type_name(self) -> str:
@@ -149,95 +159,180 @@ class GGUFTensorInfo:
 
     @property
     def kind(self) -> str:
+        """"dense", "block" or "refused"."""
         t = GGML_TYPES.get(self.ggml_type)
-        return t[3] if t else "refused"
+        return {"dense": "dense", "blocks": "block"}.get(t.load, "refused") if t else "refused"
 
     @property
     def format(self):
-        """The `_quantized_formats()` name of a block type loaded here, else None."""
+        """The quantised format a block tensor loads as (`_quantized_formats()`), else None."""
         t = GGML_TYPES.get(self.ggml_type)
-        return t[4] if t and t[3] == "block" else None
-
-    def __repr__(self):
-        return (f"GGUFTensorInfo({self.name!r}, {self.type_name}, shape={self.shape}, offset={self.offset}, "
-                f"nbytes={self.nbytes})")
+        return t.what if t is not None and t.load == "blocks" else None
 
 
-class _Parser:
-    """Sequential little-endian reads over the mapped file, each bounds-checked."""
+GGUFTensorInfo = TensorEntry  # the descriptor's name on the reference side
 
-    def __init__(self, buf, size, path):
-        self.buf, self.size, self.path, self.pos = buf, size, path, 0
+_VT_STRING, _VT_ARRAY = 8, 9
+# metadata scalar value types: GGUF id -> numpy dtype (little endian)
+_VT_SCALAR = {0: "<u1", 1: "<i1", 2: "<u2", 3: "<i2", 4: "<u4", 5: "<i4", 6: "<f4", 7: "?", 10: "<u8", 11: "<i8",
+              12: "<f8"}
+_HEADER = struct.Struct("<4sIQQ")
+_U32, _U64 = struct.Struct("<I"), struct.Struct("<Q")
 
-    def need(self, n, what):
-        if n < 0 or self.pos + n > self.size:
-            raise GGUFFormatError(f"{self.path}: truncated -- {what} needs {n} bytes at offset {self.pos} of a "
-                                  f"{self.size}-byte file")
-        p = self.pos
-        self.pos += n
-        return p
 
-    def unpack(self, code, what):
-        size = struct.calcsize("<" + code)
-        return struct.unpack_from("<" + code, self.buf, self.need(size, what))[0]
+def scan(buf, size: int, path: str) -> dict:
+    """Walk the container once. Returns version, metadata (key -> value),
+    metadata_types (key -> type id, or (9, element type id) for arrays),
+    alignment, data_offset and the tensor entries in file order."""
+    pos = 0
 
-    def string(self, what):
-        n = self.unpack("Q", f"the length of {what}")
-        p = self.need(n, what)
-        # surrogateescape: bytes that are not UTF-8 survive a round trip
-        return bytes(self.buf[p:p + n]).decode("utf-8", "surrogateescape")
+    def take(n: int, what: str) -> int:
+        nonlocal pos
+        if pos + n > size:
+            raise GGUFFormatError(f"{path}: the file ends inside {what} (it needs bytes {pos}..{pos + n} of a "
+                                  f"{size}-byte file)")
+        start, pos = pos, pos + n
+        return start
 
-    def value(self, vtype, what, nested=False):
-        if vtype in _SCALAR:
-            return self.unpack(_SCALAR[vtype], what)
-        if vtype == _STRING:
-            return self.string(what)
-        if vtype != _ARRAY:
-            raise GGUFFormatError(f"{self.path}: {what} has unknown GGUF value type {vtype}")
-        if nested:
-            raise UnsupportedGGUF(f"{self.path}: {what} is an array of arrays, which this reader does not read")
-        etype = self.unpack("I", f"the element type of {what}")
-        count = self.unpack("Q", f"the element count of {what}")
-        if count > self.size - self.pos:  # every element takes at least one byte
-            raise GGUFFormatError(f"{self.path}: {what} claims {count} elements with {self.size - self.pos} "
-                                  "bytes left")
-        if etype in _SCALAR:
-            code = _SCALAR[etype]
-            p = self.need(struct.calcsize("<" + code) * count, what)
-            return ArrayValue(etype, list(struct.unpack_from(f"<{count}{code}", self.buf, p)))
-        return ArrayValue(etype, [self.value(etype, f"{what}[{i}]", nested=True) for i in range(count)])
+    def u32(what):
+        return _U32.unpack_from(buf, take(4, what))[0]
+
+    def u64(what):
+        return _U64.unpack_from(buf, take(8, what))[0]
+
+    def text(what):
+        n = u64(f"the byte count of {what}")
+        start = take(n, what)
+        # surrogateescape keeps bytes that are not UTF-8 (some vocabularies hold them)
+        return bytes(buf[start:start + n]).decode("utf-8", "surrogateescape")
+
+    def scalar(vt, what):
+        dt = np.dtype(_VT_SCALAR[vt])
+        v = np.frombuffer(buf, dtype=dt, count=1, offset=take(dt.itemsize, what))[0]
+        return bool(v) if vt == 7 else v.item()
+
+    def value(vt, what):
+        if vt in _VT_SCALAR:
+            return scalar(vt, what), vt
+        if vt == _VT_STRING:
+            return text(what), vt
+        if vt != _VT_ARRAY:
+            raise GGUFFormatError(f"{path}: {what} has value type {vt}, which GGUF does not define")
+        et = u32(f"the element type of {what}")
+        n = u64(f"the length of {what}")
+        if et in _VT_SCALAR:
+            dt = np.dtype(_VT_SCALAR[et])
+            start = take(n * dt.itemsize, f"the {n} elements of {what}")
+            items = np.frombuffer(buf, dtype=dt, count=n, offset=start).tolist()
+            return items, (_VT_ARRAY, et)
+        if et == _VT_STRING:
+            if n * 8 > size - pos:  # each string has at least its 8-byte count
+                raise GGUFFormatError(f"{path}: {what} says it holds {n} strings; the {size - pos} bytes left "
+                                      "cannot")
+            return [text(f"{what}[{i}]") for i in range(n)], (_VT_ARRAY, et)
+        if et == _VT_ARRAY:
+            raise UnsupportedGGUF(f"{path}: {what} is an array of arrays; this reader stops at one level")
+        raise GGUFFormatError(f"{path}: {what} has element type {et}, which GGUF does not define")
+
+    if size < _HEADER.size:
+        raise GGUFFormatError(f"{path}: {size} bytes -- shorter than the {_HEADER.size}-byte GGUF header")
+    magic, version, n_tensors, n_kv = _HEADER.unpack_from(buf, take(_HEADER.size, "the header"))
+    if magic != b"GGUF":
+        raise GGUFFormatError(f"{path}: begins with {magic!r} where a GGUF file begins with b'GGUF'")
+    if version not in (2, 3):
+        swapped = struct.unpack("<I", struct.pack(">I", version))[0]
+        if swapped in (1, 2, 3):
+            raise UnsupportedGGUF(f"{path}: a big-endian GGUF file (version field {version:#010x}); this reader "
+                                  "reads little-endian files")
+        if version == 1:
+            raise UnsupportedGGUF(f"{path}: GGUF v1 stores 32-bit counts; convert the model again with a current "
+                                  "llama.cpp to get v3")
+        raise UnsupportedGGUF(f"{path}: GGUF v{version}; this reader knows v2 and v3")
+    # every metadata pair and every descriptor starts with an 8-byte string length
+    if (n_tensors + n_kv) * 8 > size:
+        raise GGUFFormatError(f"{path}: a header announcing {n_kv} metadata pairs and {n_tensors} tensors does "
+                              f"not fit in {size} bytes")
+
+    metadata, types = {}, {}
+    for i in range(n_kv):
+        key = text(f"metadata key {i}")
+        if key in metadata:
+            raise GGUFFormatError(f"{path}: duplicate metadata key {key!r}")
+        metadata[key], types[key] = value(u32(f"the value type of {key!r}"), f"metadata {key!r}")
+    align = metadata.get("general.alignment", 32)
+    if isinstance(align, bool) or not isinstance(align, int) or align < 1 or (align & (align - 1)):
+        raise GGUFFormatError(f"{path}: general.alignment must be a power of two, got {align!r}")
+
+    raw_entries = []
+    for i in range(n_tensors):
+        name = text(f"the name of tensor {i}")
+        nd = u32(f"the rank of {name!r}")
+        if nd < 1 or nd > 4:
+            raise GGUFFormatError(f"{path}: tensor {name!r} is {nd}-dimensional; GGUF tensors have 1 to 4 "
+                                  "dimensions")
+        ne = tuple(u64(f"extent {d} of {name!r}") for d in range(nd))
+        raw_entries.append((name, ne, u32(f"the GGML type of {name!r}"), u64(f"the data offset of {name!r}")))
+    data_offset = -(-pos // align) * align
+
+    entries, seen = [], set()
+    for name, ne, gtype, rel in raw_entries:
+        if name in seen:
+            raise GGUFFormatError(f"{path}: duplicate tensor name {name!r}")
+        seen.add(name)
+        if rel % align:
+            raise GGUFFormatError(f"{path}: tensor {name!r} starts {rel} bytes into the data section, which breaks "
+                                  f"its {align}-byte alignment")
+        t = GGML_TYPES.get(gtype)
+        nbytes = None
+        if t is not None and t.block is not None:
+            if ne[0] % t.block:
+                raise GGUFFormatError(f"{path}: tensor {name!r} is {t.name} with rows of {ne[0]} elements, which "
+                                      f"{t.block}-element blocks do not divide")
+            count = 1
+            for d in ne:
+                count *= d
+            nbytes = count // t.block * t.size
+            if data_offset + rel + nbytes > size:
+                raise GGUFFormatError(f"{path}: tensor {name!r} needs bytes up to {data_offset + rel + nbytes}, but "
+                                      f"the file stops at {size} (cut short?)")
+        entries.append(TensorEntry(name, gtype, ne, data_offset + rel, nbytes))
+    return {"version": version, "metadata": metadata, "metadata_types": types, "alignment": align,
+            "data_offset": data_offset, "entries": entries}
 
 
 class GGUFFile:
-    """A GGUF file, memory-mapped read-only.
+    """A GGUF file mapped read-only, usable as a context manager:
 
         with GGUFFile(path) as f:
             f.metadata["general.architecture"]
-            f.tensors["blk.0.attn_q.weight"]   # GGUFTensorInfo
-            f.raw("blk.0.attn_q.weight")       # the stored bytes
+            f.tensors["blk.0.attn_q.weight"].shape
+            f.tensor_bytes("blk.0.attn_q.weight")   # a view of the stored bytes
     """
 
     def __init__(self, path):
         self.path = os.fspath(path)
-        self._fh = open(self.path, "rb")
-        self._mm = None
+        with open(self.path, "rb") as fh:
+            size = os.fstat(fh.fileno()).st_size
+            if size == 0:
+                raise GGUFFormatError(f"{self.path}: 0 bytes -- a GGUF file starts with a 24-byte header")
+            self._map = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+        self.size = size
         try:
-            self.size = os.fstat(self._fh.fileno()).st_size
-            if self.size == 0:
-                raise GGUFFormatError(f"{self.path}: empty file, not GGUF")
-            self._mm = mmap.mmap(self._fh.fileno(), 0, access=mmap.ACCESS_READ)
-            self._read_header()
+            found = scan(self._map, size, self.path)
         except BaseException:
             self.close()
             raise
+        self.version = found["version"]
+        self.metadata = found["metadata"]
+        self.metadata_types = found["metadata_types"]
+        self.alignment = found["alignment"]
+        self.data_offset = found["data_offset"]
+        self.tensors = {e.name: e for e in found["entries"]}
 
     def close(self):
-        if self._mm is not None:
-            self._mm.close()
-            self._mm = None
-        if self._fh is not None:
-            self._fh.close()
-            self._fh = None
+        m, self._map = getattr(self, "_map", None), None
+        if m is not None:
+            m.close()
 
     def __enter__(self):
         return self
@@ -245,152 +340,81 @@ class GGUFFile:
     def __exit__(self, *exc):
         self.close()
 
-    def _read_header(self):
-        p = _Parser(self._mm, self.size, self.path)
-        p0 = p.need(4, "the magic")
-        magic = bytes(self._mm[p0:p0 + 4])
-        if magic != _MAGIC:
-            raise GGUFFormatError(f"{self.path}: not a GGUF file (magic {magic!r}, expected {_MAGIC!r})")
-        version = p.unpack("I", "the version")
-        if version not in (2, 3):
-            if struct.unpack(">I", struct.pack("<I", version))[0] in (1, 2, 3):
-                raise UnsupportedGGUF(f"{self.path}: big-endian GGUF (the version field reads {version:#x}); only "
-                                      "little-endian files are read")
-            if version == 1:
-                raise UnsupportedGGUF(f"{self.path}: GGUF version 1 (32-bit counts) is not read; re-convert the "
-                                      "model with a current llama.cpp")
-            raise UnsupportedGGUF(f"{self.path}: GGUF version {version} is not read (2 and 3 are)")
-        self.version = version
-        n_tensors = p.unpack("Q", "the tensor count")
-        n_kv = p.unpack("Q", "the metadata count")
-        if 8 * max(n_tensors, n_kv) > self.size:  # every entry starts with an 8-byte length
-            raise GGUFFormatError(f"{self.path}: the header claims {n_kv} metadata entries and {n_tensors} "
-                                  f"tensors, more than {self.size} bytes can hold")
-        self.metadata, self.metadata_types = {}, {}
-        for i in range(n_kv):
-            key = p.string(f"metadata key #{i}")
-            vtype = p.unpack("I", f"the value type of {key!r}")
-            if key in self.metadata:
-                raise GGUFFormatError(f"{self.path}: metadata key {key!r} appears twice")
-            self.metadata[key] = p.value(vtype, f"metadata {key!r}")
-            self.metadata_types[key] = vtype
-        align = self.metadata.get("general.alignment", _DEFAULT_ALIGNMENT)
-        if type(align) is not int or align <= 0 or align & (align - 1):
-            raise GGUFFormatError(f"{self.path}: general.alignment = {align!r} is not a positive power of two")
-        self.alignment = align
+    def info(self, name) -> TensorEntry:
+        try:
+            return self.tensors[name]
+        except KeyError:
+            raise KeyError(f"{name!r}: no such tensor in {self.path}") from None
 
-        descs = []
-        for i in range(n_tensors):
-            name = p.string(f"tensor name #{i}")
-            nd = p.unpack("I", f"the dimension count of {name!r}")
-            if not 1 <= nd <= _MAX_DIMS:
-                raise GGUFFormatError(f"{self.path}: tensor {name!r} has {nd} dimensions (1 to {_MAX_DIMS} allowed)")
-            ne = [p.unpack("Q", f"dimension {d} of {name!r}") for d in range(nd)]
-            gtype = p.unpack("I", f"the type of {name!r}")
-            rel = p.unpack("Q", f"the data offset of {name!r}")
-            descs.append((name, ne, gtype, rel))
-        self.data_offset = (p.pos + align - 1) // align * align
-
-        self.tensors = {}
-        for name, ne, gtype, rel in descs:
-            if name in self.tensors:
-                raise GGUFFormatError(f"{self.path}: tensor {name!r} appears twice")
-            if rel % align:
-                raise GGUFFormatError(f"{self.path}: tensor {name!r} starts at data offset {rel}, not a multiple "
-                                      f"of the alignment {align}")
-            count = 1
-            for d in ne:
-                count *= d
-            t = GGML_TYPES.get(gtype)
-            nbytes = None
-            if t is not None and t[1] is not None:
-                if ne[0] % t[1]:
-                    raise GGUFFormatError(f"{self.path}: tensor {name!r} is {t[0]} with ne[0] = {ne[0]}, not a "
-                                          f"multiple of its block size {t[1]}")
-                nbytes = count // t[1] * t[2]
-                end = self.data_offset + rel + nbytes
-                if end > self.size:
-                    raise GGUFFormatError(f"{self.path}: tensor {name!r} ends at byte {end}, past the end of the "
-                                          f"{self.size}-byte file (truncated)")
-            self.tensors[name] = GGUFTensorInfo(name, gtype, ne, self.data_offset + rel, nbytes, count)
-
-    def info(self, name) -> GGUFTensorInfo:
-        if name not in self.tensors:
-            raise KeyError(f"{self.path} has no tensor named {name!r}")
-        return self.tensors[name]
-
-    def raw(self, name, refuse=True) -> bytes:
-        """The tensor's stored bytes. `refuse=False` returns the bytes of a
-        type that is not loaded (size permitting), for tooling that copies
-        tensors through untouched."""
-        info = self.info(name)
-        why = refusal(info.ggml_type, name)
-        if refuse and why is not None:
+    def tensor_bytes(self, name, *, allow_unloaded: bool = False) -> memoryview:
+        """The stored bytes of tensor `name` (a view of the map). A type this
+        backend does not load raises its refusal unless `allow_unloaded`, for
+        tools that copy such tensors through untouched."""
+        e = self.info(name)
+        why = refusal(e.ggml_type, name)
+        if why is not None and not allow_unloaded:
             raise why
-        if info.nbytes is None:
-            raise why or UnsupportedGGUF(f"tensor {name!r}: {info.type_name} has no known byte size")
-        return self._mm[info.offset:info.offset + info.nbytes]
+        if e.nbytes is None:
+            raise why
+        return memoryview(self._map)[e.offset:e.offset + e.nbytes]
 
     def __repr__(self):
-        return (f"GGUFFile({self.path!r}, version={getattr(self, 'version', '?')}, "
-                f"tensors={len(getattr(self, 'tensors', {}))}, metadata={len(getattr(self, 'metadata', {}))})")
+        return f"<GGUFFile {self.path} v{getattr(self, 'version', '?')}: {len(getattr(self, 'tensors', {}))} tensors>"
 
 
-def _unpermute_rows(rows: np.ndarray, n_head: int, shape) -> np.ndarray:
-    """Undo llama.cpp's q/k row interleave (convert_hf_to_gguf's `permute`):
-    within each head the file holds rows (d, p) in order d-major for pair
-    index p in {0, 1}; HF's rotate-half layout wants p-major. `rows` is
-    [n_rows, row_bytes] (whole rows: a row of blocks never mixes rows, so the
-    blocks move as they are)."""
+def _rows_to_rotate_half(rows: np.ndarray, n_head: int, shape) -> np.ndarray:
+    """llama.cpp's converter stores each head's q/k rows interleaved (row 2d + p
+    holds rotary pair p of dimension d); the model expects the two halves one
+    after the other (row p*dim + d). `rows` is [n_rows, bytes per row]: a row
+    of blocks never spans rows, so whole rows move as they are."""
     n = rows.shape[0]
     if n_head <= 0 or n % (2 * n_head):
-        raise UnsupportedGGUF(f"cannot undo the Llama q/k row permutation of shape {tuple(shape)} for "
-                              f"n_head={n_head}")
-    return np.ascontiguousarray(rows.reshape(n_head, n // (2 * n_head), 2, -1).transpose(0, 2, 1, 3)
-                                .reshape(n, -1))
+        raise UnsupportedGGUF(f"{n} rows of a {tuple(shape)} tensor do not split into {n_head} heads of rotary "
+                              f"pairs (n_head={n_head})")
+    per = n // (2 * n_head)
+    return np.ascontiguousarray(rows.reshape(n_head, per, 2, -1).swapaxes(1, 2).reshape(n, -1))
 
 
 def load_tensor(f: GGUFFile, name: str, keep_blocks: bool = False, permute_heads: int | None = None,
                 device="hip"):
-    """One tensor of `f` (__init__.py:135-170 of the reference).
-
-    F32/F16/BF16 come back dense in their own dtype, bit for bit. A q4_0 or
-    q8_0 tensor comes back as a quantised tensor holding the file's blocks
-    (`keep_blocks=True`) or as their float32 dequantisation on the device.
-    `permute_heads` undoes llama.cpp's q/k row permutation for that many
-    heads, moving whole rows of blocks."""
+    """Tensor `name` of `f`, as the reference's `load_tensor`
+    (gguf/__init__.py:135-170) returns it: F32, F16 and BF16 dense in their own
+    dtype, bit for bit; q4_0, q8_0 and q4_k as a quantised tensor over the
+    file's blocks (`keep_blocks=True`) or as their float32 dequantisation.
+    `permute_heads=n` puts the q/k rows of n heads back in rotate-half order,
+    moving whole rows."""
     from . import _C
     from .tensor import Tensor
 
-    info = f.info(name)
-    why = refusal(info.ggml_type, name)
-    if why is not None:
-        raise why
-    raw = np.frombuffer(f.raw(name), dtype=np.uint8)
-    if info.kind == "dense":
-        dtype = GGML_TYPES[info.ggml_type][4]
-        host = raw.view({"float32": np.float32, "float16": np.float16, "bfloat16": np.uint16}[dtype])
-        host = host.reshape(info.shape)
+    e = f.info(name)
+    data = np.frombuffer(f.tensor_bytes(name), dtype=np.uint8)
+    t = GGML_TYPES[e.ggml_type]
+    if t.load == "dense":
+        host = data.view({"float32": np.float32, "float16": np.float16, "bfloat16": np.uint16}[t.what])
+        host = host.reshape(e.shape)
         if permute_heads is not None:
-            host = _unpermute_rows(host.reshape(info.shape[0], -1), permute_heads, info.shape).reshape(info.shape)
-        return Tensor.from_numpy(host.copy(), dtype=dtype, device=device)
+            host = _rows_to_rotate_half(host.reshape(e.shape[0], -1), permute_heads, e.shape).reshape(e.shape)
+        return Tensor.from_numpy(np.array(host), dtype=t.what, device=device)
     if permute_heads is not None:
-        raw = _unpermute_rows(raw.reshape(info.shape[0], -1), permute_heads, info.shape).reshape(-1)
-    q = _C._quantized_from_blob(raw.tobytes(), info.shape, info.format, device=device)
+        data = _rows_to_rotate_half(data.reshape(e.shape[0], -1), permute_heads, e.shape).reshape(-1)
+    q = _C._quantized_from_blob(data.tobytes(), e.shape, t.what, device=device)
     return q if keep_blocks else _C._dequantize(q)
 
 
 def quantized_linear(f: GGUFFile, name: str, bias=None, device="hip"):
-    """A QuantizedLinear whose weight is tensor `name`'s own blocks
-    (__init__.py:173-201 of the reference): a 2-D block tensor
-    (out_features, in_features); dense tensors are refused by name."""
+    """A QuantizedLinear over tensor `name`'s own blocks, as the reference's
+    `quantized_linear` (gguf/__init__.py:173-201) builds one: the tensor must
+    be a 2-D block tensor (out_features, in_features)."""
     from .quant import QuantizedLinear
 
-    info = f.info(name)
-    if info.kind != "block":
-        raise refusal(info.ggml_type, name) or UnsupportedGGUF(
-            f"tensor {name!r} is {info.type_name}, not a block-quantised type; use load_tensor() for a dense "
-            "weight")
-    if len(info.shape) != 2:
-        raise UnsupportedGGUF(f"tensor {name!r} has shape {info.shape}; a linear weight is 2-D")
+    e = f.info(name)
+    why = refusal(e.ggml_type, name)
+    if why is not None:
+        raise why
+    if e.kind != "block":
+        raise UnsupportedGGUF(f"tensor {name!r} is dense {e.type_name}; a QuantizedLinear needs block-quantised "
+                              "weights (load a dense weight with load_tensor)")
+    if len(e.shape) != 2:
+        raise UnsupportedGGUF(f"tensor {name!r} has shape {e.shape}; a QuantizedLinear weight is "
+                              "(out_features, in_features)")
     return QuantizedLinear(load_tensor(f, name, keep_blocks=True, device=device), bias)
