@@ -4,7 +4,7 @@ scaled_dot_product_attention -- behind a C ABI (include/tnhip.h,
 libtnhip.so) and a Python mirror of the reference's `torch._C` entry points.
 """
 
-from . import _C, device, gguf, quant, tensor
+from . import _C, device, gguf, nn, quant, tensor
 from ._C import (
     QTensor,
     _aten_dispatch,
@@ -23,11 +23,11 @@ from ._C import (
     scaled_dot_product_attention,
     sdpa_decode,
 )
-from .quant import QuantizedLinear, quantize_
+from .quant import QuantizedLinear, QuantizeReport, quantize_
 from .tensor import Event, Stream, Tensor, empty, synchronize, tensor, zeros
 
 __all__ = [
-    "QTensor", "QuantizedLinear", "quantize_", "Tensor", "Stream", "Event", "empty", "zeros", "tensor",
+    "QTensor", "QuantizedLinear", "QuantizeReport", "quantize_", "Tensor", "Stream", "Event", "empty", "zeros", "tensor",
     "synchronize", "_quantize", "_dequantize", "_quantized_linear", "_quantized_to", "_quantized_blob",
     "_quantized_from_blob", "_quantized_format", "_quantized_formats", "_quantized_nbytes", "_aten_dispatch",
     "scaled_dot_product_attention", "sdpa_decode", "_hip_probe", "_hip_counters", "_hip_ops",
