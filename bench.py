@@ -319,11 +319,137 @@ def bench_e2e(tn, L, prompt_len=256, n_new=128, seed=5, graph=True):
             "first_tokens": (tokens if graph else eager_tokens)[:16]}
 
 
+def host_cpu():
+    """The host's CPU model, physical cores (distinct (package, core id)
+    pairs) and logical CPUs this process may use."""
+    model, cores, pkg = None, set(), None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = (s.strip() for s in line.partition(":"))
+                if key == "model name" and model is None:
+                    model = val
+                elif key == "physical id":
+                    pkg = val
+                elif key == "core id":
+                    cores.add((pkg, val))
+    except OSError:
+        pass
+    logical = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return {"cpu_model": model, "physical_cores": len(cores) or None, "logical_cpus": logical}
+
+
+def cpu_threads():
+    """Threads for the CPU baselines: the reference's default is one per
+    physical core (candle-core/src/utils.rs:312-323); on a shared GPU box the
+    process's CPU share (OMP_NUM_THREADS, 16 there) caps it."""
+    h = host_cpu()
+    n = min(h["physical_cores"] or h["logical_cpus"], h["logical_cpus"])
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return max(1, min(n, share) if share > 0 else n)
+
+
+def _timed(fn, seconds):
+    fn()  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        sec = time.perf_counter() - t0
+        if sec >= seconds:
+            return reps, sec
+
+
+def _cpu_record(value, unit, threads, sample, **extra):
+    return {"value": value, "unit": unit, "cores": threads, "kind": "port", "sample": sample, **host_cpu(), **extra}
+
+
+def cpu_baseline_q4(threads, m, seconds, c1=True):
+    """The oracle's bit-exact restatement of the reference's x86 CPU q4_0
+    linear (Q8_0 activations, scalar vec_dot_unopt, the 4-column driver:
+    k_quants.rs:312-329, :2430-2582) on the config-1 shape (GB/s of the same
+    algorithmic bytes as the GPU line) or on m rows of the config-3 shape
+    (TFLOP/s of 2 m k n)."""
+    import oracle as O
+
+    if c1:
+        n, k = 1536, 576
+        blob = _synth_q4_0_blob(n, k, 0.02, 1).tobytes()
+        x = np.random.default_rng(1).standard_normal((1, k)).astype(np.float32)
+    else:
+        n, k = 14336, 4096
+        blob = _synth_q4_0_blob(n, k, 0.01, 33).tobytes()
+        x = O.bf16_to_f32(O.bf16_from_f32(np.random.default_rng(3).standard_normal((m, k)).astype(np.float32)))
+    reps, sec = _timed(lambda: O.q4_0_linear(x, blob, n, threads=threads), seconds)
+    if c1:
+        nbytes = n * k // 32 * 18 + k * 4 + n * 4
+        return _cpu_record(nbytes * reps / sec / 1e9, "GB/s", threads,
+                           f"config 1 in full ([1,576] x [1536,576]^T q4_0) x {reps} calls in {sec:.1f} s",
+                           us_per_call=sec / reps * 1e6)
+    flops = 2.0 * m * k * n
+    return _cpu_record(flops * reps / sec / 1e12, "TFLOP/s", threads,
+                       f"{m} of config 3's 512 rows ([{m},4096] x [14336,4096]^T q4_0, bf16 x widened) x {reps} "
+                       f"calls in {sec:.1f} s; a full config-3 call would take {sec / reps * 512 / m:.2f} s")
+
+
+def cpu_baseline_decode(threads, seconds):
+    """The oracle's default SDPA path at L=1 per sequence over the config-4
+    caches (B=16, 32/8 heads, D=128, bf16 widened to f32, the same lengths as
+    the GPU run), in GB/s of the same K/V bytes."""
+    import oracle as O
+
+    B, Hq, Hkv, D = 16, 32, 8, 128
+    rng = np.random.default_rng(4)
+    lens = rng.integers(512, 4097, size=B)
+    q = O.bf16_to_f32(O.bf16_from_f32(rng.standard_normal((B, Hq, D)).astype(np.float32)))
+    kv = [O.bf16_to_f32(O.bf16_from_f32(rng.standard_normal((2, Hkv, int(n), D)).astype(np.float32))) for n in lens]
+
+    def call():
+        for b in range(B):
+            O.bf16_from_f32(O.sdpa(q[b][None, :, None, :], kv[b][0][None], kv[b][1][None], threads=threads)[0])
+
+    reps, sec = _timed(call, seconds)
+    nbytes = int(lens.sum()) * Hkv * D * 2 * 2 + 2 * B * Hq * D * 2
+    return _cpu_record(nbytes * reps / sec / 1e9, "GB/s", threads,
+                       f"config 4 in full (16 sequences, lengths as the GPU run, sum {int(lens.sum())}) x {reps} "
+                       f"calls in {sec:.1f} s", us_per_call=sec / reps * 1e6)
+
+
+def cpu_baseline_e2e(threads, steps=12, start=256):
+    """The oracle's float32 decode step of the config-5 model (the C q4_0
+    linear bit-exact to the reference's x86 path, numpy for the rest) at
+    positions 256.. with the KV cache filled with random values, in tokens/s.
+    For context, the reference publishes 86.4 tok/s for SmolLM2-135M q4_0 on
+    an Apple M1 CPU with 4 threads (tests/bench/results_llama_cpp.json)."""
+    from oracle import decoder as OD
+
+    cfg = OD.LlamaConfig()
+    dec = OD.Decoder(cfg, 0, start + steps + 1, np.float32, threads=threads)
+    rng = np.random.default_rng(7)
+    for L in dec.layers:
+        L["k"][:] = rng.standard_normal(L["k"].shape).astype(np.float32)
+        L["v"][:] = rng.standard_normal(L["v"].shape).astype(np.float32)
+    tok = 17
+    dec.step(tok, start)  # warm
+    t0 = time.perf_counter()
+    for i in range(steps):
+        tok = OD.argmax(dec.step(tok, start + 1 + i))
+    sec = time.perf_counter() - t0
+    return _cpu_record(steps / sec, "tokens/s", threads,
+                       f"{steps} greedy steps of the config-5 model at positions {start + 1}..{start + steps} "
+                       f"(KV cache pre-filled), {sec:.1f} s",
+                       reference_published={"value": 86.4, "unit": "tokens/s",
+                                            "hardware": "Apple M1 CPU, 4 threads, SmolLM2-135M q4_0",
+                                            "source": "tests/bench/results_llama_cpp.json"})
+
+
 def cpu_baseline_sdpa(threads, seconds=10.0):
     """The oracle's restatement of the reference's default SDPA path (f32
     body, bf16 in/out) on the full config 2 (9/3 heads, causal, S=2048),
     repeated until about `seconds` of wall time have passed, in TFLOP/s of the
-    same algorithmic flop count as the GPU line."""
+    same algorithmic flop count as the GPU line. The oracle's products are
+    plain triple loops, so this understates the reference's default path,
+    whose two products run in the gemm crate with runtime SIMD dispatch."""
     import oracle as O
 
     rng = np.random.default_rng(2)
@@ -342,9 +468,10 @@ def cpu_baseline_sdpa(threads, seconds=10.0):
         if sec >= seconds:
             break
     flops = 4.0 * D * hq * S * (S + 1) / 2 * reps
-    return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"config 2 in full (9 q heads / 3 kv heads, causal, S=2048, bf16 inputs widened to f32, "
-                      f"output narrowed to bf16) x {reps} repetitions: {sec:.1f} s for {flops / 1e9:.1f} GFLOP"}
+    return _cpu_record(flops / sec / 1e12, "TFLOP/s", threads,
+                       f"config 2 in full (9 q heads / 3 kv heads, causal, S=2048, bf16 inputs widened to f32, "
+                       f"output narrowed to bf16) x {reps} repetitions: {sec:.1f} s for {flops / 1e9:.1f} GFLOP; "
+                       "scalar loops for the two products, so below the reference's gemm-crate default path")
 
 
 # The copy kernel that scales the PMC byte counters: tn_q4_0_from_blob over a
@@ -378,11 +505,6 @@ def profiled_traffic(name):
     except OSError:
         return None
     return None
-
-
-def cpu_threads():
-    n = os.cpu_count() or 1
-    return max(1, min(16, n))
 
 
 def main():
@@ -446,8 +568,18 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        print("bench: cpu baseline", file=sys.stderr, flush=True)
-        cpu = cpu_baseline_sdpa(cpu_threads())
+        th = cpu_threads()
+        print(f"bench: cpu baselines ({th} threads)", file=sys.stderr, flush=True)
+        cpu = cpu_baseline_sdpa(th, seconds=8.0)
+        legs = {"c1_q4_gemv": lambda: cpu_baseline_q4(th, 1, 3.0),
+                "c3_q4_gemm": lambda: cpu_baseline_q4(th, 16, 4.0, c1=False),
+                "c4_decode_attention": lambda: cpu_baseline_decode(th, 3.0),
+                "c5_e2e_decode": lambda: cpu_baseline_e2e(th)}
+        for name, fn in legs.items():
+            if name in parts:
+                parts[name]["cpu_baseline"] = fn()
+        if "c2_sdpa_prefill_fp32" in parts:
+            parts["c2_sdpa_prefill_fp32"]["cpu_baseline"] = cpu
 
     line = {
         "metric": "q4 GEMV HBM GB/s + SDPA TFLOP/s (% roofline); decode tokens/s, 1 GPU",

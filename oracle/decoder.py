@@ -68,13 +68,13 @@ def argmax(x) -> int:
     return int(nan[0]) if nan.size else int(np.argmax(x))
 
 
-def linear(x, blob, n, dtype=np.float32):
+def linear(x, blob, n, dtype=np.float32, threads=1):
     """Q8_0(x) . W^T for one row x [K]: the C oracle (float32), or the exact
     value of the same quantised product (float64; x is rounded to float32
     first because the activation quantiser is defined on float32)."""
     x32 = np.asarray(x, np.float32).reshape(1, -1)
     if dtype == np.float32:
-        return O.q4_0_linear(x32, blob, n)[0]
+        return O.q4_0_linear(x32, blob, n, threads=threads)[0]
     k = x32.shape[1]
     value, _, _ = O.exact_linear_q4_0(O.q8_0_quantize(x32), blob, 1, n, k)
     return value[0]
@@ -83,8 +83,8 @@ def linear(x, blob, n, dtype=np.float32):
 class Decoder:
     """The same model on the CPU, one token per step, KV cache in `dtype`."""
 
-    def __init__(self, cfg: LlamaConfig, seed: int, cap: int, dtype=np.float32, layers=None, top=None):
-        self.cfg, self.dtype, self.cap = cfg, dtype, cap
+    def __init__(self, cfg: LlamaConfig, seed: int, cap: int, dtype=np.float32, layers=None, top=None, threads=1):
+        self.cfg, self.dtype, self.cap, self.threads = cfg, dtype, cap, threads
         top = top if top is not None else model_weights(cfg, seed)
         self.embed = top["embed"]
         self.norm = top["norm"]
@@ -108,20 +108,20 @@ class Decoder:
         h = self.embed[token].astype(dt)
         for L in self.layers:
             x = rmsnorm(h, L["ln1"], c.eps, dt)
-            qkv = linear(x, L["qkv"], (Hq + 2 * Hkv) * D, dt).astype(dt)
+            qkv = linear(x, L["qkv"], (Hq + 2 * Hkv) * D, dt, self.threads).astype(dt)
             q = rope(qkv[:Hq * D].reshape(Hq, D), pos, self.freqs, dt)
             k = rope(qkv[Hq * D:(Hq + Hkv) * D].reshape(Hkv, D), pos, self.freqs, dt)
             v = qkv[(Hq + Hkv) * D:].reshape(Hkv, D)
             L["k"][:, pos] = k
             L["v"][:, pos] = v
             a, _ = O.sdpa(q[None, :, None, :], L["k"][None, :, :pos + 1], L["v"][None, :, :pos + 1], dtype=dt)
-            h = (h + linear(a.reshape(-1), L["o"], c.hidden, dt).astype(dt)).astype(dt)
+            h = (h + linear(a.reshape(-1), L["o"], c.hidden, dt, self.threads).astype(dt)).astype(dt)
             x = rmsnorm(h, L["ln2"], c.eps, dt)
-            gu = linear(x, L["gate_up"], 2 * I, dt).astype(dt)
+            gu = linear(x, L["gate_up"], 2 * I, dt, self.threads).astype(dt)
             act = silu_mul(gu[:I], gu[I:], dt)
-            h = (h + linear(act, L["down"], c.hidden, dt).astype(dt)).astype(dt)
+            h = (h + linear(act, L["down"], c.hidden, dt, self.threads).astype(dt)).astype(dt)
         x = rmsnorm(h, self.norm, c.eps, dt)
-        return linear(x, self.lm_blob, c.vocab, dt).astype(dt)
+        return linear(x, self.lm_blob, c.vocab, dt, self.threads).astype(dt)
 
 
 def linear_rows(x, blob, n, dtype=np.float32, threads=8):
