@@ -27,6 +27,21 @@ def test_a_read_behind_a_branch_is_found():
     assert len(found) == 1 and "v_max_f32" in found[0][2] and found[0][3] == 1
 
 
+def test_a_path_with_no_active_lane_reads_nothing_until_exec_is_set():
+    # the fall-through of s_cbranch_execnz runs with exec == 0: no read there ...
+    asm = _fn(MFMA, "s_cbranch_execnz .LBB0_2", "v_max_f32 v40, v3, v4", ".LBB0_2:", "s_nop 7", "s_nop 7", "s_nop 3",
+              "v_add_f32 v9, v1, v2")
+    assert H.scan_text(asm) == []
+    # ... until exec is written again
+    asm = _fn(MFMA, "s_cbranch_execnz .LBB0_2", "s_mov_b64 exec, -1", "v_max_f32 v40, v3, v4", ".LBB0_2:",
+              "s_nop 7", "s_nop 7", "s_nop 3")
+    assert len(H.scan_text(asm)) == 1
+    # the taken branch of s_cbranch_execz likewise
+    asm = _fn(MFMA, "s_cbranch_execz .LBB0_2", "s_nop 7", "s_nop 7", "s_nop 3", "s_endpgm", ".LBB0_2:",
+              "v_max_f32 v40, v3, v4")
+    assert H.scan_text(asm) == []
+
+
 def test_enough_wait_states_and_accumulation_are_not_hazards():
     assert H.scan_text(_fn(MFMA, "s_nop 7", "s_nop 7", "s_nop 1", "v_max_f32 v40, v3, v4")) == []
     # another product accumulating into the same registers (srcC) is not a read

@@ -52,6 +52,14 @@ tn_status decode_launch(hipStream_t st, int dtype, const void* q, const void* k_
                         int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t D, const int32_t* lens,
                         int64_t max_len, double scale, void* out, float* lse, float* part_o, float2* part_ml);
 constexpr int DECODE_SPLIT_KEYS = 256;  // keys per split of the decode attention
+// The bf16 / f16 prefill at head dim 64 (flash64.hip): one workgroup per
+// (batch, head, 64-query block), no split rows, nothing allocated. mk is the
+// mask kind (0 none, 1 f32, 2 the input format, 3 bool) with the mask's
+// element strides over (B, Hq, L, S); scale >= 0, folded into sl2 =
+// scale * log2(e).
+tn_status flash64_launch(hipStream_t st, bool f16, int mk, const void* mask, int64_t msb, int64_t msh, int64_t msl,
+                         int64_t msk, const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t B, int64_t Hq,
+                         int64_t Hkv, int64_t L, int64_t S, float sl2, int causal, uint16_t* out, float* lse);
 
 #define TN_HIP(call)                                              \
     do {                                                          \

@@ -10,7 +10,10 @@ the fall-through and into branch targets, and reports any instruction that
 reads one of the destination registers before the result's wait states
 have passed (a 32x32 product needs 18, a 16x16 one 8; `s_nop n` counts
 n + 1, any other instruction 1). A following MFMA that only accumulates
-into the same registers (srcC) is not a read.
+into the same registers (srcC) is not a read. Along a path on which no lane
+is active (the fall-through of `s_cbranch_execnz`, the target of
+`s_cbranch_execz`) vector instructions read nothing until a scalar
+instruction writes `exec` again.
 
 `python -m torchnative_amd.hazard_scan` compiles every source to assembly
 with the build's flags and prints the findings; tests/test_hazard_scan.py
@@ -81,23 +84,27 @@ def scan_function(lines, name="?", max_depth=4):
         if not dst:
             continue
         need = WAIT["32x32"] if "32x32" in op else WAIT["16x16"]
-        todo, seen = [(i + 1, 0, 0)], set()
+        todo, seen = [(i + 1, 0, 0, False)], set()
         while todo:
-            j, waited, depth = todo.pop()
+            j, waited, depth, idle = todo.pop()  # idle: exec is zero on this path
             while j < len(ins) and waited < need:
-                if (j, waited) in seen:
+                if (j, waited, idle) in seen:
                     break
-                seen.add((j, waited))
+                seen.add((j, waited, idle))
                 op2, args2, text2 = ins[j]
-                if _reads(op2, args2) & dst:
+                if not idle and _reads(op2, args2) & dst:
                     found.append((name, text, text2, waited))
                     break
+                if op2.startswith("s_") and args2 and args2[0] == "exec":
+                    idle = False
                 if op2.startswith("s_cbranch") or op2 == "s_branch":
                     target = args2[0] if args2 else ""
                     if target in labels and depth < max_depth:
-                        todo.append((labels[target], waited + 1, depth + 1))
+                        todo.append((labels[target], waited + 1, depth + 1, idle or op2 == "s_cbranch_execz"))
                     if op2 == "s_branch":
                         break
+                    if op2 == "s_cbranch_execnz":
+                        idle = True  # the fall-through runs with no lane active
                 if op2 == "s_endpgm":
                     break
                 waited += int(args2[0], 0) + 1 if op2 == "s_nop" else 1
