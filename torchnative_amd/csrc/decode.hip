@@ -27,6 +27,25 @@ __global__ __launch_bounds__(256) void k_embedding(const int32_t* __restrict__ i
     out[(int64_t)i * dim + c] = (id >= 0 && id < vocab) ? table[(int64_t)id * dim + c] : NAN;
 }
 
+// The decode step's first launch: the token's embedding row into h (as
+// k_embedding), and the cosine and sine of this position's RoPE angles,
+// cosf/sinf of pos * inv_freq[j] as k_rope computes them, so that every
+// layer's rotation reads them instead of evaluating both functions again.
+// It also clears the ticket of the step's argmax epilogue.
+__global__ __launch_bounds__(256) void k_step_begin(const int32_t* __restrict__ state,
+                                                    const float* __restrict__ table, int64_t vocab, int dim,
+                                                    float* __restrict__ h, const float* __restrict__ inv_freq,
+                                                    int half, float2* __restrict__ rope, uint32_t* ticket) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c == 0) *ticket = 0;  // the lm_head's argmax epilogue counts its workgroups from 0
+    const int32_t id = state[2];
+    if (c < dim) h[c] = (id >= 0 && id < vocab) ? table[(int64_t)id * dim + c] : NAN;
+    if (blockIdx.x == 0 && threadIdx.x < half) {
+        const float f = (float)state[0] * inv_freq[threadIdx.x];
+        rope[threadIdx.x] = make_float2(cosf(f), sinf(f));
+    }
+}
+
 // thread t adds the squares of elements 1024p + 4t .. 1024p + 4t + 3, p =
 // 0, 1, ..., in order, then block_sum256: the order the q4_0 GEMV's fused
 // RMSNorm prologue reproduces
@@ -97,7 +116,8 @@ __global__ void k_rope_append(float* __restrict__ qkv, int hq, int hkv, int d, c
 // workgroup per (split, kv head) covers the NR query heads that share the kv
 // head: it rotates their queries (into LDS) and, in the split that holds the
 // new position, rotates the new key, writes it and the new value to the
-// caches and uses them for that row (other rows come from the caches). D/4
+// caches and uses them for that row (other rows come from the caches); the
+// rotation's cosines and sines come from the step's table (k_step_begin). D/4
 // lanes share a row, a float4 each, all of the split's K and V rows in flight
 // at once; row dot products reduce with DPP. Each split writes an (O, m, l)
 // partial per query head (m in log2 units), merged by the o projection's
@@ -106,7 +126,7 @@ constexpr float STEP_LOG2E = 1.4426950408889634f;
 
 template <int D, int NR>
 __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv, int hq, int hkv,
-                                                  const float* __restrict__ inv_freq,
+                                                  const float2* __restrict__ rope,
                                                   const int32_t* __restrict__ state, float* __restrict__ kc,
                                                   float* __restrict__ vc, int cap, float sl2, int nsplit,
                                                   float* __restrict__ part_o, float2* __restrict__ part_ml) {
@@ -139,17 +159,19 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
     // query heads, thread i < D/2 also pair i of the new key
     constexpr int half = D / 2;
     constexpr int QP = (NR * half + 255) / 256;  // query pairs per thread
-    float qx1[QP], qx2[QP], qf[QP], kx1 = 0.f, kx2 = 0.f, kvv1 = 0.f, kvv2 = 0.f, kf = 0.f;
+    float qx1[QP], qx2[QP], kx1 = 0.f, kx2 = 0.f, kvv1 = 0.f, kvv2 = 0.f;
+    float2 qcs[QP], kcs = make_float2(1.f, 0.f);
 #pragma unroll
     for (int i = 0; i < QP; i++) {
         const int pi = tid + 256 * i;
-        qx1[i] = qx2[i] = qf[i] = 0.0f;
+        qx1[i] = qx2[i] = 0.0f;
+        qcs[i] = make_float2(1.f, 0.f);
         if (pi < NR * half) {
             const int hh = pi / half, j = pi - hh * half;
             const float* xr = qkv + (int64_t)(kvh * NR + hh) * D;
             qx1[i] = xr[j];
             qx2[i] = xr[j + half];
-            qf[i] = inv_freq[j];
+            qcs[i] = rope[j];
         }
     }
     if (tid < half) {
@@ -159,7 +181,7 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
         kx2 = xk[tid + half];
         kvv1 = xv[tid];
         kvv2 = xv[tid + half];
-        kf = inv_freq[tid];
+        kcs = rope[tid];
     }
     const int pos = state[0];
     const int len = pos < 0 ? 0 : (pos + 1 < cap ? pos + 1 : cap);
@@ -180,16 +202,14 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
         const int pi = tid + 256 * i;
         if (pi < NR * half) {
             const int hh = pi / half, j = pi - hh * half;
-            const float f = (float)pos * qf[i];
-            const float cs = cosf(f), sn = sinf(f);
+            const float cs = qcs[i].x, sn = qcs[i].y;
             const float x1 = qx1[i], x2 = qx2[i];
             sq[hh][j] = x1 * cs + (-x2) * sn;
             sq[hh][j + half] = x2 * cs + x1 * sn;
         }
     }
     if (fresh && tid < half) {
-        const float f = (float)pos * kf;
-        const float cs = cosf(f), sn = sinf(f);
+        const float cs = kcs.x, sn = kcs.y;
         const float x1 = kx1, x2 = kx2;
         const float y1 = x1 * cs + (-x2) * sn, y2 = x2 * cs + x1 * sn;
         const float v1 = kvv1, v2 = kvv2;
@@ -310,25 +330,8 @@ __global__ __launch_bounds__(256) void k_add(const float* a, const float* b, int
 
 // (v, i) before (w, j) in argmax order: a NaN first (the earliest), then the
 // larger value, then the smaller index
-__device__ inline bool arg_before(float v, int i, float w, int j) {
-    const bool nv = v != v, nw = w != w;
-    if (nv || nw) return nv && (!nw || i < j);
-    return v > w || (v == w && i < j);
-}
-
 constexpr int ARGMAX_THREADS = 1024;
 constexpr int ARGMAX_U = 12;  // loads in flight per thread (49152 f32 = one batch of float4s)
-
-// end of a decode step: advance the position, pick the next input token
-__device__ inline void llama_advance(int32_t* state, int32_t* tokens, const int32_t* prompt, int prompt_len,
-                                     int cap) {
-    const int pos = state[0] + 1;
-    const int next = pos < prompt_len ? prompt[pos] : state[3];
-    if (pos < cap) tokens[pos] = next;
-    state[0] = pos;
-    state[1] = pos + 1;
-    state[2] = next;
-}
 
 // One workgroup per row. arg_before is a strict total order on (value,
 // index) pairs, so the winner does not depend on how the pairs are reduced:
@@ -444,7 +447,7 @@ __global__ void k_kv_append(const float* __restrict__ k, const float* __restrict
 
 // scratch layout of a decode step, in floats
 struct LlamaWork {
-    int64_t h, qkv, attn, gu, part_o, part_ml, total;
+    int64_t h, qkv, attn, gu, part_o, part_ml, rope, arg_v, arg_i, ticket, total;
 };
 
 static LlamaWork llama_work(const tn_llama* m) {
@@ -464,6 +467,10 @@ static LlamaWork llama_work(const tn_llama* m) {
     w.gu = take(2 * m->inter);
     w.part_o = take(m->n_heads * nsplit * m->head_dim);
     w.part_ml = take(m->n_heads * nsplit * 2);
+    w.rope = take(m->head_dim);  // (cos, sin) of the step's position per rotated pair
+    w.arg_v = take(GEMV_ARG_MAX_PARTS);   // the lm_head's per-workgroup argmax (values
+    w.arg_i = take(GEMV_ARG_MAX_PARTS);   // and indices, as int32) and its ticket
+    w.ticket = take(1);
     w.total = o;
     return w;
 }
@@ -596,7 +603,9 @@ int64_t tn_llama_work_floats(const tn_llama* model) {
 //   h = h + Q4(silu(gate) * up)                  linear_decode, SiLU prologue
 // A longer cache replaces the middle two by k_rope_append, the split-KV decode
 // attention with its combine, and the o projection on its output.
-// Then logits = Q4(rmsnorm(h, norm)) and the argmax that advances the state.
+// Then logits = Q4(rmsnorm(h, norm)), with their argmax and the state's
+// advance in the same launch (a separate k_argmax when the GEMV would need
+// more workgroups than the partials hold).
 // The fused linears are bit-identical to the separate ops (tn_rmsnorm,
 // tn_q4_0_linear, tn_add, tn_silu_mul); RoPE is tn_rope's arithmetic.
 tn_status tn_llama_step(void* stream, const tn_llama* m) {
@@ -610,12 +619,13 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
     float* gu = m->work + w.gu;
     float* part_o = m->work + w.part_o;
     float2* part_ml = reinterpret_cast<float2*>(m->work + w.part_ml);
+    float2* rope = reinterpret_cast<float2*>(m->work + w.rope);
+    uint32_t* ticket = reinterpret_cast<uint32_t*>(m->work + w.ticket);
     const int64_t H = m->hidden, D = m->head_dim, Hq = m->n_heads, Hkv = m->n_kv_heads, I = m->inter;
     const int64_t nqkv = (Hq + 2 * Hkv) * D;
     const float eps = (float)m->eps;
     int32_t* pos = m->state;      // [0]: position of this token
     int32_t* len = m->state + 1;  // [1]: KV length after appending it
-    int32_t* tok = m->state + 2;  // [2]: this token
     const double nan = std::nan("");
     GemvPro none, ln1, ln2, fin, comb;
     ln1.eps = ln2.eps = fin.eps = eps;
@@ -632,7 +642,9 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
     comb.head_dim = (int)D;
     comb.cap = (int)m->cap;
     const float sl2 = (float)(1.0 / std::sqrt((double)D)) * STEP_LOG2E;
-    TN_TRY(tn_embedding(st, tok, 1, m->embed, m->vocab, H, h));
+    hipLaunchKernelGGL(k_step_begin, dim3((unsigned)cdiv(H, 256)), dim3(256), 0, st, m->state, m->embed, m->vocab,
+                       (int)H, h, m->inv_freq, (int)(D / 2), rope, ticket);
+    TN_LAUNCHED();
     for (int64_t l = 0; l < m->n_layers; l++) {
         const tn_llama_layer& L = m->layers[l];
         ln1.w = L.ln1;
@@ -641,7 +653,7 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
         if (fused) {
             const dim3 grid((unsigned)nsplit_step, (unsigned)Hkv);
 #define TN_STEP_ATTN(DD, NR)                                                                                  \
-    hipLaunchKernelGGL((k_step_attn<DD, NR>), grid, dim3(256), 0, st, qkv, (int)Hq, (int)Hkv, m->inv_freq, pos, \
+    hipLaunchKernelGGL((k_step_attn<DD, NR>), grid, dim3(256), 0, st, qkv, (int)Hq, (int)Hkv, rope, pos,        \
                        L.k_cache, L.v_cache, (int)m->cap, sl2, (int)nsplit_step, part_o, part_ml)
 #define TN_STEP_ATTN_D(DD)                    \
     switch (nrep) {                           \
@@ -671,6 +683,18 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
         TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, ln2, L.gate_up.qs, L.gate_up.d, 2 * I, nullptr, gu));
         TN_TRY(linear_decode(st, gu, I, PRO_SILU, none, L.down.qs, L.down.d, H, h, h));
     }
+    // the logits and, in the same launch, their argmax and the state's advance
+    fin.arg_v = m->work + w.arg_v;
+    fin.arg_i = reinterpret_cast<int32_t*>(m->work + w.arg_i);
+    fin.ticket = ticket;
+    fin.state = m->state;
+    fin.tokens = m->tokens;
+    fin.prompt = m->prompt;
+    fin.prompt_len = (int)m->prompt_len;
+    fin.cap = (int)m->cap;
+    s = linear_decode_argmax(st, h, H, fin, m->lm_head.qs, m->lm_head.d, m->vocab, m->logits);
+    if (s != TN_ENOTIMPL) return s;
+    // more workgroups than the partials hold: the logits, then k_argmax
     TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, fin, m->lm_head.qs, m->lm_head.d, m->vocab, nullptr, m->logits));
     if (m->vocab % 4 == 0 && reinterpret_cast<uintptr_t>(m->logits) % 16 == 0)
         hipLaunchKernelGGL((k_argmax<true, true>), dim3(1), dim3(ARGMAX_THREADS), 0, st, m->logits, (int)m->vocab,

@@ -29,11 +29,9 @@ namespace {
 constexpr int QKK = 256;
 constexpr int QK4K_BYTES = 144;
 
-__device__ inline int sat_i8k(float v) {  // `v.clamp(-128, 127) as i8`, NaN -> 0
-    if (v != v) return 0;
-    if (v >= 127.0f) return 127;
-    if (v <= -128.0f) return -128;
-    return (int)v;
+__device__ inline int sat_i8k(float v) {  // `v.clamp(-128, 127) as i8`, NaN -> 0 (selects, not branches)
+    const int q = (int)fminf(fmaxf(v, -128.0f), 127.0f);
+    return v != v ? 0 : q;
 }
 
 // llama.cpp's nearest_int (candle utils.rs:292-295): ties to even.

@@ -41,18 +41,17 @@ struct Fmt<FMT_Q8_0> {
 
 // ---- Rust cast semantics ---------------------------------------------------
 
+// Truncation toward zero after clamping to the type's range, NaN to 0. The
+// clamp and the NaN test are selects: written as early returns they became
+// three nested exec-mask branches per element.
 __device__ inline int sat_i8(float v) {  // `f as i8`
-    if (v != v) return 0;
-    if (v >= 127.0f) return 127;
-    if (v <= -128.0f) return -128;
-    return (int)v;
+    const int q = (int)fminf(fmaxf(v, -128.0f), 127.0f);
+    return v != v ? 0 : q;
 }
 
 __device__ inline int sat_u8(float v) {  // `f as u8`
-    if (v != v) return 0;
-    if (v >= 255.0f) return 255;
-    if (v <= 0.0f) return 0;
-    return (int)v;
+    const int q = (int)fminf(fmaxf(v, 0.0f), 255.0f);
+    return v != v ? 0 : q;
 }
 
 template <typename XT>
@@ -266,13 +265,82 @@ __device__ inline int dot_block_q8(const uint4& w0, const uint4& w1, const int* 
 // output's thread reads its residual before writing it), never x. x must be 16-byte aligned.
 constexpr int GEMV_HOLD = 4;  // passes of 32 blocks held in registers (K <= 4096 per row at once)
 
-template <int FMT, int MR, typename XT, int PRO>
+// The best (value, index) over a workgroup of GEMV_THREADS threads, in
+// thread 0 (arg_before's order: any pairing gives the same winner).
+__device__ inline void block_arg_best(float& v, int& i) {
+    __shared__ float sv[GEMV_THREADS / 64];
+    __shared__ int si[GEMV_THREADS / 64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(v, off);
+        const int oi = __shfl_xor(i, off);
+        if (arg_before(ov, oi, v, i)) {
+            v = ov;
+            i = oi;
+        }
+    }
+    if (lane == 0) {
+        sv[w] = v;
+        si[w] = i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int k = 1; k < GEMV_THREADS / 64; k++)
+            if (arg_before(sv[k], si[k], v, i)) {
+                v = sv[k];
+                i = si[k];
+            }
+    }
+}
+
+// The argmax epilogue after a workgroup's last tile: its best output goes to
+// the partials, then a ticket. The partials are stored and loaded as
+// agent-scope atomics (they cross XCDs, whose L2s are not coherent) and the
+// ticket is an acquire-release add at agent scope, so the workgroup that
+// draws the last ticket sees every partial. It reduces them and advances the
+// decode state as k_argmax<true, ...> does.
+__device__ inline void gemv_argmax_epilogue(float v, int i, int n, const GemvPro& po) {
+    __shared__ int s_last;
+    block_arg_best(v, i);
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(po.arg_v + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(po.arg_i + blockIdx.x, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t t = __hip_atomic_fetch_add(po.ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = t == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    v = -INFINITY;
+    i = INT32_MAX;
+    for (int g = threadIdx.x; g < (int)gridDim.x; g += GEMV_THREADS) {
+        const float gv = __hip_atomic_load(po.arg_v + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int gi = __hip_atomic_load(po.arg_i + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (arg_before(gv, gi, v, i)) {
+            v = gv;
+            i = gi;
+        }
+    }
+    __syncthreads();  // block_arg_best's LDS is reused
+    block_arg_best(v, i);
+    if (threadIdx.x == 0) {
+        po.state[3] = i < n ? i : 0;
+        llama_advance(po.state, po.tokens, po.prompt, po.prompt_len, po.cap);
+    }
+}
+
+// Epilogue ARG (MR == 1, f32 y; linear_decode_argmax): argmax of y and the
+// decode step's advance, reduced over the workgroups through po.arg_v/arg_i
+// and a ticket (see GemvPro).
+template <int FMT, int MR, typename XT, int PRO, bool ARG = false>
 __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x, int K, int nb,
                                                      const uint8_t* __restrict__ qs,
                                                      const uint16_t* __restrict__ dw, int N, int rows,
                                                      const float* __restrict__ bias, const float* resid, void* y,
                                                      int y_bf16, const GemvPro po) {
     static_assert(PRO == PRO_NONE || (MR == 1 && sizeof(XT) == 4), "prologues take one f32 row");
+    static_assert(!ARG || MR == 1, "the argmax epilogue takes one row");
     constexpr int HOLD = PRO == PRO_COMBINE ? 1 : GEMV_HOLD;
     constexpr int ITEMS = Fmt<FMT>::GEMV_ITEMS, NV = Fmt<FMT>::CODE_BYTES / 16;
     extern __shared__ __align__(16) char smem[];
@@ -452,6 +520,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
     // phase 2/3, persistent over row tiles: the next tile's weight loads are in
     // flight while this tile's terms are computed and summed; the terms live
     // in two LDS buffers, so one barrier per tile suffices
+    float best_v = -INFINITY;  // ARG: this thread's best output so far
+    int best_i = INT32_MAX;    // loses every tie against a real output
     for (int buf = 0; tile < ntiles; tile += tstride, buf ^= 1) {
         const int next = tile + tstride;
         if (next < ntiles) gload(next, wn, dn);
@@ -510,6 +580,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
             }
             for (; b < nb; b++) acc = acc + tr[b];
             if (bias || resid) acc = acc + add;
+            if constexpr (ARG) {
+                if (arg_before(acc, (int)n, best_v, best_i)) {
+                    best_v = acc;
+                    best_i = (int)n;
+                }
+            }
             if (y_bf16)
                 reinterpret_cast<uint16_t*>(y)[(int64_t)mr * N + n] = bf16_from_f32(acc);
             else
@@ -522,6 +598,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
             dv[it] = dn[it];
         }
     }
+    if constexpr (ARG) gemv_argmax_epilogue(best_v, best_i, N, po);
 }
 
 // ---- prefill GEMM on MFMA ---------------------------------------------------------
@@ -1044,7 +1121,7 @@ tn_status check_weight(const char* op, const char* fmt, int64_t n, int64_t k) {
     return TN_OK;
 }
 
-template <int FMT, int MR, typename XT, int PRO = PRO_NONE>
+template <int FMT, int MR, typename XT, int PRO = PRO_NONE, bool ARG = false>
 tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, const uint16_t* dw, int N,
                       const float* bias, void* y, int y_bf16, const float* resid = nullptr,
                       const GemvPro& po = GemvPro()) {
@@ -1076,12 +1153,13 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     // workgroup that had to wait for a slot would start its whole share of
     // tiles late)
     int resident = 0;
-    tn_status s =
-        resident_workgroups(reinterpret_cast<const void*>(&k_gemv<FMT, MR, XT, PRO>), GEMV_THREADS, lds, &resident);
+    tn_status s = resident_workgroups(reinterpret_cast<const void*>(&k_gemv<FMT, MR, XT, PRO, ARG>), GEMV_THREADS,
+                                      lds, &resident);
     if (s != TN_OK) return s;
     const unsigned grid = (unsigned)(ntiles < resident ? ntiles : resident);
-    hipLaunchKernelGGL((k_gemv<FMT, MR, XT, PRO>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N, rows,
-                       bias, resid, y, y_bf16, po);
+    if (ARG && grid > (unsigned)GEMV_ARG_MAX_PARTS) return TN_ENOTIMPL;
+    hipLaunchKernelGGL((k_gemv<FMT, MR, XT, PRO, ARG>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N,
+                       rows, bias, resid, y, y_bf16, po);
     TN_LAUNCHED();
     return TN_OK;
 }
@@ -1244,6 +1322,16 @@ tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, cons
     }
     if (s == TN_ENOTIMPL) return fail(TN_ENOTIMPL, "linear_decode: the activation row does not fit the GEMV");
     return s;
+}
+
+tn_status linear_decode_argmax(hipStream_t st, const float* x, int64_t k, const GemvPro& po, const uint8_t* qs,
+                               const uint16_t* d, int64_t n, float* y) {
+    tn_status s = check_weight("linear_decode_argmax", "q4_0", n, k);
+    if (s != TN_OK) return s;
+    if (k > LINEAR_DECODE_MAX_K || n > INT32_MAX || n < 1) return TN_ENOTIMPL;
+    if (!po.arg_v || !po.arg_i || !po.ticket || !po.state || !po.tokens || (po.prompt_len > 0 && !po.prompt))
+        return fail(TN_EINVAL, "linear_decode_argmax: missing argmax operands");
+    return launch_gemv<FMT_Q4_0, 1, float, PRO_RMSNORM, true>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, nullptr, po);
 }
 
 }  // namespace tn

@@ -240,6 +240,28 @@ __device__ inline float block_sum256(float v, float* red) {
 // sqrt then reciprocal as the reference's rsqrt (aten.rs:11112-11133).
 __device__ inline float rms_scale(float ss, int n, float eps) { return 1.0f / sqrtf(ss / (float)n + eps); }
 
+// argmax's order on (value, index): NaN first (the lower index among NaNs),
+// then the larger value, then the lower index. A strict total order, so the
+// winner does not depend on how a reduction pairs the candidates.
+__device__ inline bool arg_before(float v, int i, float w, int j) {
+    const bool nv = v != v, nw = w != w;
+    if (nv || nw) return nv && (!nw || i < j);
+    return v > w || (v == w && i < j);
+}
+
+// end of a decode step (state = [position, KV length, token, argmax]):
+// advance the position and pick the next input token, the prompt's while
+// the position is inside it, else the argmax
+__device__ inline void llama_advance(int32_t* state, int32_t* tokens, const int32_t* prompt, int prompt_len,
+                                     int cap) {
+    const int pos = state[0] + 1;
+    const int next = pos < prompt_len ? prompt[pos] : state[3];
+    if (pos < cap) tokens[pos] = next;
+    state[0] = pos;
+    state[1] = pos + 1;
+    state[2] = next;
+}
+
 // Input transforms a decode linear can apply while it quantises its input.
 // PRO_COMBINE builds the row from split attention partials (the decode
 // step's o projection).
@@ -262,7 +284,22 @@ struct GemvPro {
     const float2* part_ml = nullptr;
     const int32_t* len = nullptr;
     int nsplit = 0, head_dim = 0, cap = 0;
+    // argmax epilogue (linear_decode_argmax): every workgroup's best (value,
+    // index) of y goes to arg_v/arg_i[workgroup]; the workgroup that takes
+    // the last ticket reduces them and advances the decode state (state,
+    // tokens, prompt, prompt_len, cap) as llama_advance. *ticket must be 0 at
+    // the launch; nothing resets it afterwards.
+    float* arg_v = nullptr;
+    int32_t* arg_i = nullptr;
+    uint32_t* ticket = nullptr;
+    int32_t* state = nullptr;
+    int32_t* tokens = nullptr;
+    const int32_t* prompt = nullptr;
+    int prompt_len = 0;
 };
+
+// Most workgroups an argmax epilogue launch may have (partials per launch).
+constexpr int GEMV_ARG_MAX_PARTS = 4096;
 
 // One f32 row through a q4_0 linear (qlinear.hip), y[n] = Q8_0(pro(x)) . W^T
 // (+ resid[n]): pro is a LinearPrologue (PRO_RMSNORM scales by po.w with
@@ -272,5 +309,11 @@ struct GemvPro {
 constexpr int64_t LINEAR_DECODE_MAX_K = 24576;  // 768 blocks: one per (row, block) item of the workgroup
 tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, const GemvPro& po, const uint8_t* qs,
                         const uint16_t* d, int64_t n, const float* resid, float* y);
+// The decode step's last linear: y = Q4(rmsnorm(x, po.w)) as linear_decode
+// with PRO_RMSNORM, then the argmax of y and the state's advance (po's
+// argmax fields) in the same launch. TN_ENOTIMPL when the launch would need
+// more than GEMV_ARG_MAX_PARTS workgroups.
+tn_status linear_decode_argmax(hipStream_t st, const float* x, int64_t k, const GemvPro& po, const uint8_t* qs,
+                               const uint16_t* d, int64_t n, float* y);
 
 }  // namespace tn
