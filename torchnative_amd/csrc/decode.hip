@@ -604,8 +604,7 @@ int64_t tn_llama_work_floats(const tn_llama* model) {
 // A longer cache replaces the middle two by k_rope_append, the split-KV decode
 // attention with its combine, and the o projection on its output.
 // Then logits = Q4(rmsnorm(h, norm)), with their argmax and the state's
-// advance in the same launch (a separate k_argmax when the GEMV would need
-// more workgroups than the partials hold).
+// advance in the same launch.
 // The fused linears are bit-identical to the separate ops (tn_rmsnorm,
 // tn_q4_0_linear, tn_add, tn_silu_mul); RoPE is tn_rope's arithmetic.
 tn_status tn_llama_step(void* stream, const tn_llama* m) {
@@ -694,7 +693,8 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
     fin.cap = (int)m->cap;
     s = linear_decode_argmax(st, h, H, fin, m->lm_head.qs, m->lm_head.d, m->vocab, m->logits);
     if (s != TN_ENOTIMPL) return s;
-    // more workgroups than the partials hold: the logits, then k_argmax
+    // a row the GEMV does not hold (linear_decode refuses it by name): the
+    // logits, then k_argmax
     TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, fin, m->lm_head.qs, m->lm_head.d, m->vocab, nullptr, m->logits));
     if (m->vocab % 4 == 0 && reinterpret_cast<uintptr_t>(m->logits) % 16 == 0)
         hipLaunchKernelGGL((k_argmax<true, true>), dim3(1), dim3(ARGMAX_THREADS), 0, st, m->logits, (int)m->vocab,

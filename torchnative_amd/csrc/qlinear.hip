@@ -296,18 +296,28 @@ __device__ inline void block_arg_best(float& v, int& i) {
 }
 
 // The argmax epilogue after a workgroup's last tile: its best output goes to
-// the partials, then a ticket. The partials are stored and loaded as
-// agent-scope atomics (they cross XCDs, whose L2s are not coherent) and the
-// ticket is an acquire-release add at agent scope, so the workgroup that
-// draws the last ticket sees every partial. It reduces them and advances the
-// decode state as k_argmax<true, ...> does.
+// the partials with device-coherent stores (sc1: written through to memory,
+// past this XCD's non-coherent L2), the thread waits until they are
+// acknowledged, then takes a ticket (a relaxed agent-scope add). The
+// workgroup that draws the last ticket reads the partials back with
+// device-coherent loads, reduces them and advances the decode state as
+// k_argmax<true, ...> does. No fence is needed, as in sdpa.hip's split-row
+// merge: only the partials cross workgroups, and they never sit in a
+// non-coherent cache. (An acquire-release ticket at agent scope writes back
+// the XCD's whole L2 in every workgroup: measured 30.8 us for the C5 lm_head
+// launch against 9.0 us without the epilogue.)
 __device__ inline void gemv_argmax_epilogue(float v, int i, int n, const GemvPro& po) {
+    constexpr uint32_t SC1 = 16;  // cache policy: device scope
     __shared__ int s_last;
+    const uint32_t parts = gridDim.x * 4u;
+    const buf_rsrc rv = make_rsrc(po.arg_v, parts), ri = make_rsrc(po.arg_i, parts);
     block_arg_best(v, i);
+#if __HIP_DEVICE_COMPILE__
     if (threadIdx.x == 0) {
-        __hip_atomic_store(po.arg_v + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(po.arg_i + blockIdx.x, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t t = __hip_atomic_fetch_add(po.ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rv, blockIdx.x * 4u, 0, SC1);
+        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)i, ri, blockIdx.x * 4u, 0, SC1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // acknowledged by memory
+        const uint32_t t = __hip_atomic_fetch_add(po.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = t == gridDim.x - 1;
     }
     __syncthreads();
@@ -315,8 +325,8 @@ __device__ inline void gemv_argmax_epilogue(float v, int i, int n, const GemvPro
     v = -INFINITY;
     i = INT32_MAX;
     for (int g = threadIdx.x; g < (int)gridDim.x; g += GEMV_THREADS) {
-        const float gv = __hip_atomic_load(po.arg_v + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int gi = __hip_atomic_load(po.arg_i + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float gv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, (uint32_t)g * 4u, 0, SC1));
+        const int gi = (int)__builtin_amdgcn_raw_buffer_load_b32(ri, (uint32_t)g * 4u, 0, SC1);
         if (arg_before(gv, gi, v, i)) {
             v = gv;
             i = gi;
@@ -328,6 +338,7 @@ __device__ inline void gemv_argmax_epilogue(float v, int i, int n, const GemvPro
         po.state[3] = i < n ? i : 0;
         llama_advance(po.state, po.tokens, po.prompt, po.prompt_len, po.cap);
     }
+#endif
 }
 
 // Epilogue ARG (MR == 1, f32 y; linear_decode_argmax): argmax of y and the
@@ -1156,8 +1167,8 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     tn_status s = resident_workgroups(reinterpret_cast<const void*>(&k_gemv<FMT, MR, XT, PRO, ARG>), GEMV_THREADS,
                                       lds, &resident);
     if (s != TN_OK) return s;
-    const unsigned grid = (unsigned)(ntiles < resident ? ntiles : resident);
-    if (ARG && grid > (unsigned)GEMV_ARG_MAX_PARTS) return TN_ENOTIMPL;
+    unsigned grid = (unsigned)(ntiles < resident ? ntiles : resident);
+    if (ARG && grid > (unsigned)GEMV_ARG_MAX_PARTS) grid = (unsigned)GEMV_ARG_MAX_PARTS;
     hipLaunchKernelGGL((k_gemv<FMT, MR, XT, PRO, ARG>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N,
                        rows, bias, resid, y, y_bf16, po);
     TN_LAUNCHED();

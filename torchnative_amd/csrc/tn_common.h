@@ -298,8 +298,11 @@ struct GemvPro {
     int prompt_len = 0;
 };
 
-// Most workgroups an argmax epilogue launch may have (partials per launch).
-constexpr int GEMV_ARG_MAX_PARTS = 4096;
+// Workgroups of an argmax-epilogue launch, each writing one partial: the
+// ticket is one address every workgroup adds to, and device-scope adds to
+// one address serialise, so the launch uses fewer, longer-lived workgroups
+// (the GEMV is persistent over row tiles).
+constexpr int GEMV_ARG_MAX_PARTS = 256;
 
 // One f32 row through a q4_0 linear (qlinear.hip), y[n] = Q8_0(pro(x)) . W^T
 // (+ resid[n]): pro is a LinearPrologue (PRO_RMSNORM scales by po.w with
@@ -311,8 +314,8 @@ tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, cons
                         const uint16_t* d, int64_t n, const float* resid, float* y);
 // The decode step's last linear: y = Q4(rmsnorm(x, po.w)) as linear_decode
 // with PRO_RMSNORM, then the argmax of y and the state's advance (po's
-// argmax fields) in the same launch. TN_ENOTIMPL when the launch would need
-// more than GEMV_ARG_MAX_PARTS workgroups.
+// argmax fields) in the same launch. TN_ENOTIMPL when the activation row
+// does not fit the GEMV.
 tn_status linear_decode_argmax(hipStream_t st, const float* x, int64_t k, const GemvPro& po, const uint8_t* qs,
                                const uint16_t* d, int64_t n, float* y);
 
