@@ -758,6 +758,10 @@ __device__ inline uint32_t codes_pair23(uint32_t x) { return __builtin_amdgcn_pe
 constexpr int GM_AS = QK + 8;  // LDS row stride (bf16) of the code tiles: 80 B, conflict-free b128 reads
 constexpr int GM_RS = 4;       // K blocks whose operands are in flight ahead of the one computed
 
+// WR x WC waves over a GM_BM x BN tile, each wave TI x TJ MFMA tiles of
+// 16x16: <2, 2> is 128 x 128 (waves of 64 x 64), <4, 1> is 128 x 112 (waves
+// of 32 x 112), chosen at launch so the tiles fill the device evenly.
+template <int WR, int WC>
 __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict__ xc,
                                                     const float* __restrict__ dxT,
                                                     const float* __restrict__ corrT, int M, int M_pad, int nb,
@@ -765,15 +769,20 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
                                                     const uint16_t* __restrict__ dw, int N,
                                                     const float* __restrict__ bias, void* __restrict__ y,
                                                     int y_bf16) {
+    static_assert(WR * WC == GM_THREADS / 64, "one wave per sub-tile");
+    constexpr int TI = GM_BM / (16 * WR);  // MFMA row tiles per wave
+    constexpr int TJ = WR == 2 ? 4 : 7;    // MFMA column tiles per wave
+    constexpr int BN = 16 * TJ * WC;       // columns per workgroup: 128 or 112
+    static_assert(2 * BN <= GM_THREADS && GM_BM + BN <= GM_THREADS, "staging threads");
     __shared__ __align__(16) uint16_t sA[2][GM_BM * GM_AS];
-    __shared__ __align__(16) uint16_t sB[2][GM_BN * GM_AS];
+    __shared__ __align__(16) uint16_t sB[2][BN * GM_AS];
     __shared__ __align__(16) float sdx[2][GM_BM];
     __shared__ __align__(16) float scr[2][GM_BM];
-    __shared__ __align__(16) float sdw[2][GM_BN];
+    __shared__ __align__(16) float sdw[2][BN];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;  // wave's 64x64 sub-tile
+    const int wm = wave / WC, wn = wave % WC;  // wave's (16 TI) x (16 TJ) sub-tile
     const int lrow = lane & 15, lgrp = lane >> 4;
 
     // XCD-aware tile order: workgroup id -> (row tile, column tile)
@@ -782,13 +791,13 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
     const int id = (int)(blockIdx.y * gridDim.x + blockIdx.x);
     int tile = id;
     if (ntot % NUM_XCD == 0) tile = (id % NUM_XCD) * (ntot / NUM_XCD) + id / NUM_XCD;
-    const int m0 = (tile % mt) * GM_BM, n0 = (tile / mt) * GM_BN;
+    const int m0 = (tile % mt) * GM_BM, n0 = (tile / mt) * BN;
 
-    f32x4 acc[4][4];
+    f32x4 acc[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < TI; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TJ; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     // Per-thread staging registers, GM_RS register sets: block b's operands are
     // requested GM_RS blocks before they are computed (about 1.7 us of
@@ -796,77 +805,122 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
     // the LDS double buffer one block ahead. The set index is a compile-time
     // constant (the K loop is unrolled by GM_RS), so the sets stay in VGPRs.
     // one register set: two 16-byte chunks of activation codes, 8 bytes of
-    // weight nibbles, and (threads < GM_BM) the row's Q8_0 scale and
-    // accumulator start or (threads >= GM_BM) the column's f16 weight scale
+    // weight nibbles (threads < 2 BN), and (threads < GM_BM) the row's Q8_0
+    // scale and accumulator start or (GM_BM <= threads < GM_BM + BN) the
+    // column's f16 weight scale
     const int bcol = tid >> 1, bhalf = tid & 1;
     const int ar0 = tid >> 2, ar1 = (tid + GM_THREADS) >> 2, apart = tid & 3;  // the two A chunks
-    auto gload = [&](int b, uint4& a0, uint4& a1, uint2& w, float& dx, float& corr, uint32_t& dws) {
-        a0 = *reinterpret_cast<const uint4*>(xc + ((int64_t)(m0 + ar0) * nb + b) * QK + apart * 8);
-        a1 = *reinterpret_cast<const uint4*>(xc + ((int64_t)(m0 + ar1) * nb + b) * QK + apart * 8);
-        w = make_uint2(0x88888888u, 0x88888888u);
-        if (n0 + bcol < N) w = *reinterpret_cast<const uint2*>(qs + ((int64_t)(n0 + bcol) * nb + b) * 16 + bhalf * 8);
+    // Every load is an unconditional buffer load: a descriptor per operand
+    // over this tile's rows or columns, a per-thread offset computed once and
+    // the block's offset in a scalar register, so a step costs no address
+    // arithmetic. What lies past a descriptor's range (columns past N, the
+    // threads that stage nothing of an operand, blocks past the last) reads
+    // as zero and is not used; loads behind branches made the compiler's wait
+    // counting fall back to waiting for every load in flight.
+    const uint32_t OOB = 0x80000000u;  // an offset past every range here
+    const int ncols = min(BN, N - n0);
+    const buf_rsrc ra = make_rsrc(xc + (int64_t)m0 * nb * QK, (uint32_t)(GM_BM * nb * QK * 2));
+    const buf_rsrc rw = make_rsrc(qs + (int64_t)n0 * nb * 16, (uint32_t)(ncols * nb * 16));
+    const buf_rsrc rdx = make_rsrc(dxT + m0, (uint32_t)(((int64_t)nb * M_pad - m0) * 4));
+    const buf_rsrc rcr = make_rsrc(corrT + m0, (uint32_t)(((int64_t)nb * M_pad - m0) * 4));
+    const buf_rsrc rdw = make_rsrc(dw + (int64_t)n0 * nb, (uint32_t)(ncols * nb * 2));
+    const uint32_t va0 = (uint32_t)((ar0 * nb * QK + apart * 8) * 2), va1 = (uint32_t)((ar1 * nb * QK + apart * 8) * 2);
+    const uint32_t vw = bcol < BN ? (uint32_t)(bcol * nb * 16 + bhalf * 8) : OOB;
+    const uint32_t vs = tid < GM_BM ? (uint32_t)(tid * 4) : OOB;
+    const uint32_t vd = (tid >= GM_BM && tid < GM_BM + BN) ? (uint32_t)((tid - GM_BM) * nb * 2) : OOB;
+    auto gload = [&](int b, uint4& a0, uint4& a1, uint2& w, float& dx, float& corr, uint32_t& dws)
+                     __attribute__((always_inline)) {
+#if __HIP_DEVICE_COMPILE__
+        typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x4_t x0 = __builtin_amdgcn_raw_buffer_load_b128(ra, va0, (uint32_t)(b * QK * 2), 0);
+        const u32x4_t x1 = __builtin_amdgcn_raw_buffer_load_b128(ra, va1, (uint32_t)(b * QK * 2), 0);
+        const u32x2_t ww = __builtin_amdgcn_raw_buffer_load_b64(rw, vw, (uint32_t)(b * 16), 0);
+        a0 = make_uint4(x0[0], x0[1], x0[2], x0[3]);
+        a1 = make_uint4(x1[0], x1[1], x1[2], x1[3]);
+        w = make_uint2(ww[0], ww[1]);
+        dx = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rdx, vs, (uint32_t)(b * M_pad * 4), 0));
+        corr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rcr, vs, (uint32_t)(b * M_pad * 4), 0));
+        dws = __builtin_amdgcn_raw_buffer_load_b16(rdw, vd, (uint32_t)(b * 2), 0);
+#else
+        (void)b;
+        a0 = a1 = make_uint4(0, 0, 0, 0);
+        w = make_uint2(0, 0);
         dx = corr = 0.0f;
         dws = 0;
-        if (tid < GM_BM) {
-            dx = dxT[(int64_t)b * M_pad + m0 + tid];
-            corr = corrT[(int64_t)b * M_pad + m0 + tid];
-        } else {
-            const int n = n0 + tid - GM_BM;
-            dws = (n < N) ? dw[(int64_t)n * nb + b] : 0u;
-        }
+#endif
     };
     auto lstore = [&](int buf, const uint4& a0, const uint4& a1, const uint2& w, float dx, float corr,
-                      uint32_t dws) {
+                      uint32_t dws) __attribute__((always_inline)) {
         *reinterpret_cast<uint4*>(&sA[buf][ar0 * GM_AS + apart * 8]) = a0;
         *reinterpret_cast<uint4*>(&sA[buf][ar1 * GM_AS + apart * 8]) = a1;
         // weight dwords g = 2*bhalf, 2*bhalf+1 -> K slots 8g..8g+7 each
         const uint32_t w0 = w.x, w1 = w.y;
         const uint32_t lo0 = w0 & 0x0f0f0f0fu, hi0 = (w0 >> 4) & 0x0f0f0f0fu;
         const uint32_t lo1 = w1 & 0x0f0f0f0fu, hi1 = (w1 >> 4) & 0x0f0f0f0fu;
-        uint4* dst = reinterpret_cast<uint4*>(&sB[buf][bcol * GM_AS + bhalf * 16]);
-        dst[0] = make_uint4(codes_pair01(lo0), codes_pair23(lo0), codes_pair01(hi0), codes_pair23(hi0));
-        dst[1] = make_uint4(codes_pair01(lo1), codes_pair23(lo1), codes_pair01(hi1), codes_pair23(hi1));
+        if (bcol < BN) {
+            uint4* dst = reinterpret_cast<uint4*>(&sB[buf][bcol * GM_AS + bhalf * 16]);
+            dst[0] = make_uint4(codes_pair01(lo0), codes_pair23(lo0), codes_pair01(hi0), codes_pair23(hi0));
+            dst[1] = make_uint4(codes_pair01(lo1), codes_pair23(lo1), codes_pair01(hi1), codes_pair23(hi1));
+        }
         if (tid < GM_BM) {
             sdx[buf][tid] = dx;
             scr[buf][tid] = corr;
-        } else {
+        } else if (tid < GM_BM + BN) {
             sdw[buf][tid - GM_BM] = f16_bits_hw((uint16_t)dws);
         }
     };
     // one K block from LDS buffer `buf`: the exact block dot on MFMA, then
     // the reference's two roundings and the ordered addition
-    auto compute = [&](int buf) {
-        bf16x8 afr[4], bfr[4];
+    auto compute = [&](int buf) __attribute__((always_inline)) {
+        constexpr int WROWS = 16 * TI, WCOLS = 16 * TJ;  // the wave's sub-tile
+        bf16x8 afr[TI], bfr[TJ];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            afr[i] = *reinterpret_cast<const bf16x8*>(&sA[buf][(wm * 64 + i * 16 + lrow) * GM_AS + lgrp * 8]);
+        for (int i = 0; i < TI; i++)
+            afr[i] = *reinterpret_cast<const bf16x8*>(&sA[buf][(wm * WROWS + i * 16 + lrow) * GM_AS + lgrp * 8]);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            bfr[j] = *reinterpret_cast<const bf16x8*>(&sB[buf][(wn * 64 + j * 16 + lrow) * GM_AS + lgrp * 8]);
-        float dwv[4];
-        f32x4 dxv[4], crv[4];
+        for (int j = 0; j < TJ; j++)
+            bfr[j] = *reinterpret_cast<const bf16x8*>(&sB[buf][(wn * WCOLS + j * 16 + lrow) * GM_AS + lgrp * 8]);
+        float dwv[TJ];
+        f32x4 dxv[TI], crv[TI];
 #pragma unroll
-        for (int j = 0; j < 4; j++) dwv[j] = sdw[buf][wn * 64 + j * 16 + lrow];
+        for (int j = 0; j < TJ; j++) dwv[j] = sdw[buf][wn * WCOLS + j * 16 + lrow];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            dxv[i] = *reinterpret_cast<const f32x4*>(&sdx[buf][wm * 64 + i * 16 + lgrp * 4]);
-            crv[i] = *reinterpret_cast<const f32x4*>(&scr[buf][wm * 64 + i * 16 + lgrp * 4]);
+        for (int i = 0; i < TI; i++) {
+            dxv[i] = *reinterpret_cast<const f32x4*>(&sdx[buf][wm * WROWS + i * 16 + lgrp * 4]);
+            crv[i] = *reinterpret_cast<const f32x4*>(&scr[buf][wm * WROWS + i * 16 + lgrp * 4]);
         }
+        // C[row][col]: col = lane & 15 (weight column), row = 4*(lane>>4) + r;
+        // A = activation rows, B = weight columns; C starts at -136*sum(x codes).
+        // Tile k + 1's product is issued before tile k's recurrence, in that
+        // order (the scheduling barriers pin it), so each product runs on the
+        // matrix core under the previous tile's VALU work.
+        constexpr int NT = TI * TJ;
+        f32x4 sv[2];
+        sv[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[0], bfr[0], crv[0], 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int k = 0; k < NT; k++) {
+            const int i = k / TJ, j = k % TJ;
+            if (k + 1 < NT) {
+                const int i1 = (k + 1) / TJ, j1 = (k + 1) % TJ;
+                __builtin_amdgcn_sched_barrier(0);
+                sv[(k + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[i1], bfr[j1], crv[i1], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                // C[row][col]: col = lane & 15 (weight column), row = 4*(lane>>4) + r;
-                // A = activation rows, B = weight columns; C starts at -136*sum(x codes)
-                const f32x4 sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[i], bfr[j], crv[i], 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    float t = sv[r] * dwv[j];
-                    t = t * dxv[i][r];
-                    acc[i][j][r] = acc[i][j][r] + t;
-                }
+            for (int r = 0; r < 4; r++) {
+                float t = sv[k & 1][r] * dwv[j];
+                t = t * dxv[i][r];
+                acc[i][j][r] = acc[i][j][r] + t;
             }
         }
+        // the block's additions are done here, before the step's barrier: left
+        // to itself the compiler sinks them past the next steps' products and
+        // holds several blocks' products in registers at once
+#pragma unroll
+        for (int i = 0; i < TI; i++)
+#pragma unroll
+            for (int j = 0; j < TJ; j++) asm volatile("" : "+v"(acc[i][j]));
     };
     // Four register sets, named: step b refills set b % 4 with block b + 4
     // (set b's data went to LDS at the end of step b - 1), computes block b,
@@ -877,38 +931,45 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
     uint32_t dw_0, dw_1, dw_2, dw_3;
     static_assert(GM_RS == 4, "the unrolled K loop below names four register sets");
 #define TN_GM_SET(S) a0_##S, a1_##S, w_##S, dx_##S, cr_##S, dw_##S
-#define TN_GM_STEP(S, NEXT, B)                                    \
-    {                                                             \
-        if ((B) + GM_RS < nb) gload((B) + GM_RS, TN_GM_SET(S));   \
-        compute((B)&1);                                           \
-        if ((B) + 1 < nb) lstore(((B) + 1) & 1, TN_GM_SET(NEXT)); \
-        __syncthreads();                                          \
+    // (the last steps load and stage blocks past the end: a clamped block,
+    // into the LDS buffer no later step reads)
+#define TN_GM_STEP(S, NEXT, B)                          \
+    {                                                   \
+        gload((B) + GM_RS, TN_GM_SET(S));               \
+        compute((B)&1);                                 \
+        lstore(((B) + 1) & 1, TN_GM_SET(NEXT));         \
+        __syncthreads();                                \
     }
     gload(0, TN_GM_SET(0));
-    if (1 < nb) gload(1, TN_GM_SET(1));
-    if (2 < nb) gload(2, TN_GM_SET(2));
-    if (3 < nb) gload(3, TN_GM_SET(3));
+    gload(1, TN_GM_SET(1));
+    gload(2, TN_GM_SET(2));
+    gload(3, TN_GM_SET(3));
     lstore(0, TN_GM_SET(0));
     __syncthreads();
-    for (int b = 0; b < nb; b += GM_RS) {
+    // whole rounds of four steps as straight-line code, then the rest
+    int b = 0;
+    for (; b + GM_RS <= nb; b += GM_RS) {
         TN_GM_STEP(0, 1, b)
-        if (b + 1 < nb) TN_GM_STEP(1, 2, b + 1)
-        if (b + 2 < nb) TN_GM_STEP(2, 3, b + 2)
-        if (b + 3 < nb) TN_GM_STEP(3, 0, b + 3)
+        TN_GM_STEP(1, 2, b + 1)
+        TN_GM_STEP(2, 3, b + 2)
+        TN_GM_STEP(3, 0, b + 3)
     }
+    if (b < nb) TN_GM_STEP(0, 1, b)
+    if (b + 1 < nb) TN_GM_STEP(1, 2, b + 1)
+    if (b + 2 < nb) TN_GM_STEP(2, 3, b + 2)
 #undef TN_GM_STEP
 #undef TN_GM_SET
 
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < TI; i++) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int n = n0 + wn * 64 + j * 16 + lrow;
+        for (int j = 0; j < TJ; j++) {
+            const int n = n0 + wn * 16 * TJ + j * 16 + lrow;
             if (n >= N) continue;
             const float bv = bias ? bias[n] : 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm * 64 + i * 16 + lgrp * 4 + r;
+                const int m = m0 + wm * 16 * TI + i * 16 + lgrp * 4 + r;
                 if (m >= M) continue;
                 float v = acc[i][j][r];
                 if (bias) v = v + bv;
@@ -1243,8 +1304,16 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
             hipLaunchKernelGGL((k_q8_rows<XT>), dim3(pgrid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
                                dxT, corrT);
         TN_LAUNCHED();
-        hipLaunchKernelGGL(k_gemm, grid, dim3(GM_THREADS), 0, st, xc, dxT, corrT, (int)m, (int)M_pad, nb, qs, d,
-                           (int)n, bias, y, y_bf16);
+        // 112-column tiles when they fill the device in whole rounds of two
+        // workgroups per CU and 128-column ones would not
+        const int64_t mt = M_pad / GM_BM;
+        const bool t112 = n % 112 == 0 && (mt * (n / 112)) % 512 == 0 && (mt * cdiv(n, GM_BN)) % 512 != 0;
+        if (t112)
+            hipLaunchKernelGGL((k_gemm<4, 1>), dim3((unsigned)(n / 112), (unsigned)mt), dim3(GM_THREADS), 0, st, xc,
+                               dxT, corrT, (int)m, (int)M_pad, nb, qs, d, (int)n, bias, y, y_bf16);
+        else
+            hipLaunchKernelGGL((k_gemm<2, 2>), grid, dim3(GM_THREADS), 0, st, xc, dxT, corrT, (int)m, (int)M_pad, nb,
+                               qs, d, (int)n, bias, y, y_bf16);
         TN_LAUNCHED();
     }
     return TN_OK;
