@@ -672,19 +672,63 @@ constexpr int PF_BQ = 64, PF_BK = 64;
 
 // ---------------------------------------------------------------------------
 // f32 prefill: the same decomposition on v_mfma_f32_16x16x4_f32 (K = 4 per op).
-//   S^T : lane (key lq, group g) feeds K[key][4c + g]; Q^T from registers.
-//   O^T : for key slot r of tile kt, lane group g feeds V[16kt + 4g + r][d]
-//         and its own P at (kt, r), so V stays in natural layout in LDS.
-// Row strides are padded to 4 mod 64 dwords, so the 64 lanes of each LDS read
-// hit 64 distinct banks.
+// The head dim is permuted inside each product so that every operand a lane
+// needs is contiguous in LDS and comes in 16-byte reads:
+//   S^T : product c sums d = 16g + c over lane groups g (g = lane >> 4), so
+//         lane (key lq, g) feeds K[key][16g + c] for c = 0..15: its 16 K
+//         operands of a 16-key slice are four ds_read_b128; Q^T likewise from
+//         registers (q[16g + c]).
+//   O^T : output tile dt holds d = 4i + dt in its row i, so for key slot r of
+//         slice kt lane (lq, g) feeds V[16kt + 4g + r][4lq + dt], dt = 0..3:
+//         one ds_read_b128 serves all four tiles; lane (q, g) ends up holding
+//         d = 16g .. 16g + 15 of query q.
+// The next slice's K operands are read while the current slice's products
+// run. Row strides are padded to 4 mod 32 dwords, so each 8-lane phase of a
+// 16-byte read covers all 32 banks.
 // ---------------------------------------------------------------------------
+
+// Stream-K partition of the f32 prefill. A unit is one key tile of one
+// 64-query block; units run over (batch * head, query block, key tile) in
+// that order, a query block qt having nt(qt) key tiles. The persistent grid's
+// G workgroups take equal unit ranges [g T / G, (g+1) T / G), so every
+// workgroup does the same MFMA work whatever the causal shape. A workgroup
+// writes a query block it covers whole straight to the output; a block cut
+// by a range boundary leaves an unnormalised (O, m, l) partial per
+// workgroup: in slot 2g if it is workgroup g's first block, else 2g + 1 (a
+// workgroup cuts at most its first and its last block), and
+// k_prefill_combine merges them in workgroup order.
+struct SkGeo {
+    int nqb, NS, c, causal;  // query blocks, key tiles of S, key tiles per query block (PF_BQ / BK)
+    int64_t Tbh, T, G;       // units per (batch, head), all units, workgroups (G <= T)
+    __host__ __device__ int nt(int qt) const { return causal ? (c * (qt + 1) < NS ? c * (qt + 1) : NS) : NS; }
+    // units of query blocks 0 .. qt-1 of one (batch, head)
+    __host__ __device__ int64_t P(int qt) const {
+        if (!causal) return (int64_t)qt * NS;
+        const int64_t m = qt < NS / c ? qt : NS / c;  // blocks below qt whose tiles stop before S
+        return (int64_t)c * m * (m + 1) / 2 + ((int64_t)qt - m) * NS;
+    }
+    __host__ __device__ int64_t lo(int64_t g) const { return g * T / G; }
+    __host__ __device__ int64_t wg_of(int64_t u) const { return ((u + 1) * G + T - 1) / T - 1; }
+    // the query block (bh, qt) that holds unit u, and u's tile in it
+    __host__ __device__ void locate(int64_t u, int64_t& bh, int& qt, int& t) const {
+        bh = u / Tbh;
+        const int64_t r = u - bh * Tbh;
+        int a = 0, b = nqb;  // the largest qt with P(qt) <= r (every block has a tile)
+        while (b - a > 1) {
+            const int mid = (a + b) >> 1;
+            if (P(mid) <= r) a = mid; else b = mid;
+        }
+        qt = a;
+        t = (int)(r - P(a));
+    }
+};
 
 // MASK: 1 adds an f32 mask, 3 a bool one (MaskRef), to the scaled scores
 // (aten.rs:10383-10389)
 template <int D, int BK, int MASK = 0>
 __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, const float* __restrict__ Kg,
                                               const float* __restrict__ Vg, int Hq, int Hkv, int L, int S,
-                                              float sl2, int causal, int tiles_per, int nsplit,
+                                              float sl2, int causal, const SkGeo geo,
                                               float* __restrict__ Og, float* __restrict__ lse,
                                               float* __restrict__ part_o, float2* __restrict__ part_ml,
                                               const MaskRef mask) {
@@ -696,183 +740,264 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int lq = lane & 15, g = lane >> 4;
-    const int nqb = (L + BQ - 1) / BQ;
-    const int item = (int)blockIdx.x;
-    const int qt = nqb - 1 - item / nsplit;
-    const int split = item % nsplit;
-    const int h = blockIdx.y, b = blockIdx.z;
-    const int kvh = h / (Hq / Hkv);
-    const int q0 = qt * BQ;
-    const int qi = q0 + w * 16 + lq;
-    const int kend = causal ? min(S, q0 + BQ) : S;
-    const int ntiles_row = (kend + BK - 1) / BK;
-    const int nsplit_row = row_splits(ntiles_row, tiles_per);
-    if (split >= nsplit_row) return;
-    const int t_begin = split * ntiles_row / nsplit_row;
-    const int t_end = (split + 1) * ntiles_row / nsplit_row;
+    const int64_t gw = blockIdx.x;
+    const int64_t u_hi = geo.lo(gw + 1);
 
-    const float* qp = Qg + ((int64_t)b * Hq + h) * L * D;
-    const float* kp = Kg + ((int64_t)b * Hkv + kvh) * S * D;
-    const float* vp = Vg + ((int64_t)b * Hkv + kvh) * S * D;
+    // query block qt of (batch, head) bh, key tiles t_begin .. t_end-1;
+    // slot < 0: the whole block, written to the output
+    auto block = [&](int64_t bh, int qt, int t_begin, int t_end, int slot) __attribute__((always_inline)) {
+        const int h = (int)(bh % Hq), b = (int)(bh / Hq);
+        const int kvh = h / (Hq / Hkv);
+        const int q0 = qt * BQ;
+        const int qi = q0 + w * 16 + lq;
+        const float* qp = Qg + ((int64_t)b * Hq + h) * L * D;
+        const float* kp = Kg + ((int64_t)b * Hkv + kvh) * S * D;
+        const float* vp = Vg + ((int64_t)b * Hkv + kvh) * S * D;
 
-    float qf[D / 4];
-#pragma unroll
-    for (int c = 0; c < D / 4; c++) qf[c] = (qi < L) ? qp[(int64_t)qi * D + 4 * c + g] : 0.0f;
-    f32x4 o[D / 16];
-#pragma unroll
-    for (int i = 0; i < D / 16; i++) o[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    float m = -INFINITY, l = 0.0f;
+            // q[16g + c] for the D/16 row slices of 16: slice e holds d = 64e + 16g + c
+            constexpr int DS = D / 64;  // 64-wide slices of the head dim
+            static_assert(D % 64 == 0, "head dim");
+            float qf[DS][16];
+        #pragma unroll
+            for (int e = 0; e < DS; e++)
+        #pragma unroll
+                for (int c4 = 0; c4 < 4; c4++) {
+                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (qi < L) v = *reinterpret_cast<const float4*>(qp + (int64_t)qi * D + 64 * e + 16 * g + 4 * c4);
+                    qf[e][4 * c4] = v.x;
+                    qf[e][4 * c4 + 1] = v.y;
+                    qf[e][4 * c4 + 2] = v.z;
+                    qf[e][4 * c4 + 3] = v.w;
+                }
+            // o[e][dt] row i holds d = 64e + 4i + dt
+            f32x4 o[DS][4];
+        #pragma unroll
+            for (int e = 0; e < DS; e++)
+        #pragma unroll
+                for (int i = 0; i < 4; i++) o[e][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            float m = -INFINITY, l = 0.0f;
 
-    float4 kr[CH], vr[CH];
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int it = 0; it < CH; it++) {
-            const int c = tid + it * 256;
-            const int r = c / (D / 4), part = c % (D / 4);
-            kr[it] = vr[it] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (k0 + r < S) {
-                kr[it] = *reinterpret_cast<const float4*>(kp + (int64_t)(k0 + r) * D + part * 4);
-                vr[it] = *reinterpret_cast<const float4*>(vp + (int64_t)(k0 + r) * D + part * 4);
-            }
-        }
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int it = 0; it < CH; it++) {
-            const int c = tid + it * 256;
-            const int r = c / (D / 4), part = c % (D / 4);
-            *reinterpret_cast<float4*>(&sK[buf][r * RS + part * 4]) = kr[it];
-            *reinterpret_cast<float4*>(&sV[buf][r * RS + part * 4]) = vr[it];
-        }
-    };
+            float4 kr[CH], vr[CH];
+            auto gload = [&](int k0) {
+        #pragma unroll
+                for (int it = 0; it < CH; it++) {
+                    const int c = tid + it * 256;
+                    const int r = c / (D / 4), part = c % (D / 4);
+                    kr[it] = vr[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (k0 + r < S) {
+                        kr[it] = *reinterpret_cast<const float4*>(kp + (int64_t)(k0 + r) * D + part * 4);
+                        vr[it] = *reinterpret_cast<const float4*>(vp + (int64_t)(k0 + r) * D + part * 4);
+                    }
+                }
+            };
+            auto lstore = [&](int buf) {
+        #pragma unroll
+                for (int it = 0; it < CH; it++) {
+                    const int c = tid + it * 256;
+                    const int r = c / (D / 4), part = c % (D / 4);
+                    *reinterpret_cast<float4*>(&sK[buf][r * RS + part * 4]) = kr[it];
+                    *reinterpret_cast<float4*>(&sV[buf][r * RS + part * 4]) = vr[it];
+                }
+            };
+            // lane (lq, g)'s K operands of slice kt, head-dim slice e: K[16kt + lq][64e + 16g .. +15]
+            auto kread = [&](int buf, int kt, int e, float4* kf) __attribute__((always_inline)) {
+                const float* kp4 = &sK[buf][(16 * kt + lq) * RS + 64 * e + 16 * g];
+        #pragma unroll
+                for (int j = 0; j < 4; j++) kf[j] = *reinterpret_cast<const float4*>(kp4 + 4 * j);
+            };
 
-    gload(t_begin * BK);
-    lstore(0);
-    __syncthreads();
-    for (int t = t_begin; t < t_end; t++) {
-        const int buf = (t - t_begin) & 1;
-        const int k0 = t * BK;
-        if (t + 1 < t_end) gload(k0 + BK);
+            gload(t_begin * BK);
+            lstore(0);
+            __syncthreads();
+            for (int t = t_begin; t < t_end; t++) {
+                const int buf = (t - t_begin) & 1;
+                const int k0 = t * BK;
+                if (t + 1 < t_end) gload(k0 + BK);
 
-        f32x4 s[BK / 16];
-#pragma unroll
-        for (int kt = 0; kt < BK / 16; kt++) {
-            s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-            const float* krow = &sK[buf][(16 * kt + lq) * RS + g];
-#pragma unroll
-            for (int c = 0; c < D / 4; c++) s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(krow[4 * c], qf[c], s[kt], 0, 0, 0);
-        }
-        if constexpr (MASK != 0) {
-            // scores to log2 units with the mask added; from here on the scale is 1
-            if (qi < L) {
-                const int64_t mrow = (int64_t)b * mask.sb + (int64_t)h * mask.sh + (int64_t)qi * mask.sl;
-#pragma unroll
+                f32x4 s[BK / 16];
+                float4 kf[2][4];
+                kread(buf, 0, 0, kf[0]);
+        #pragma unroll
                 for (int kt = 0; kt < BK / 16; kt++) {
-                    const f32x4 mv = mask_quad<MASK, false>(mask, mrow, k0 + 16 * kt + 4 * g, S);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) s[kt][r] = s[kt][r] * sl2 + mv[r] * LOG2E;
+                    s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+                    for (int e = 0; e < DS; e++) {
+                        const int cur = (kt * DS + e) & 1;
+                        // the next slice's operands while these products run
+                        if (e + 1 < DS) kread(buf, kt, e + 1, kf[cur ^ 1]);
+                        else if (kt + 1 < BK / 16) kread(buf, kt + 1, 0, kf[cur ^ 1]);
+        #pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[cur][j].x, qf[e][4 * j], s[kt], 0, 0, 0);
+                            s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[cur][j].y, qf[e][4 * j + 1], s[kt], 0, 0, 0);
+                            s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[cur][j].z, qf[e][4 * j + 2], s[kt], 0, 0, 0);
+                            s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[cur][j].w, qf[e][4 * j + 3], s[kt], 0, 0, 0);
+                        }
+                    }
                 }
-            }
-        }
-        const float scl = MASK ? 1.0f : sl2;  // scores' factor to log2 units
-        if (k0 + BK > S || (causal && k0 + BK - 1 > q0 + w * 16)) {
-#pragma unroll
-            for (int kt = 0; kt < BK / 16; kt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int key = k0 + 16 * kt + 4 * g + r;
-                    if (key >= S || (causal && key > qi)) s[kt][r] = -INFINITY;
+                if constexpr (MASK != 0) {
+                    // scores to log2 units with the mask added; from here on the scale is 1
+                    if (qi < L) {
+                        const int64_t mrow = (int64_t)b * mask.sb + (int64_t)h * mask.sh + (int64_t)qi * mask.sl;
+        #pragma unroll
+                        for (int kt = 0; kt < BK / 16; kt++) {
+                            const f32x4 mv = mask_quad<MASK, false>(mask, mrow, k0 + 16 * kt + 4 * g, S);
+        #pragma unroll
+                            for (int r = 0; r < 4; r++) s[kt][r] = s[kt][r] * sl2 + mv[r] * LOG2E;
+                        }
+                    }
                 }
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < BK / 16; kt++)
-            mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
-        mx = wave_xor_max(mx) * scl;
-        const bool need = mx > m + RESCALE_SLACK;
-        if (__any(need)) {
-            const float mn = need ? mx : m;
-            const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);  // no key seen yet: 1, not 2^NaN
-            l = l * alpha;
-#pragma unroll
-            for (int i = 0; i < D / 16; i++) o[i] = o[i] * alpha;
-            m = mn;
-        }
-        const float mu = (m == -INFINITY) ? 0.0f : m;
-#pragma unroll
-        for (int kt = 0; kt < BK / 16; kt++) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float p = exp2f(__builtin_fmaf(s[kt][r], scl, -mu));
-                l = l + p;
-                const float* vrow = &sV[buf][(16 * kt + 4 * g + r) * RS + lq];
-#pragma unroll
-                for (int dt = 0; dt < D / 16; dt++)
-                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * dt], p, o[dt], 0, 0, 0);
+                const float scl = MASK ? 1.0f : sl2;  // scores' factor to log2 units
+                if (k0 + BK > S || (causal && k0 + BK - 1 > q0 + w * 16)) {
+        #pragma unroll
+                    for (int kt = 0; kt < BK / 16; kt++)
+        #pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const int key = k0 + 16 * kt + 4 * g + r;
+                            if (key >= S || (causal && key > qi)) s[kt][r] = -INFINITY;
+                        }
+                }
+                float mx = -INFINITY;
+        #pragma unroll
+                for (int kt = 0; kt < BK / 16; kt++)
+                    mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
+                mx = wave_xor_max(mx) * scl;
+                const bool need = mx > m + RESCALE_SLACK;
+                if (__any(need)) {
+                    const float mn = need ? mx : m;
+                    const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);  // no key seen yet: 1, not 2^NaN
+                    l = l * alpha;
+        #pragma unroll
+                    for (int e = 0; e < DS; e++)
+        #pragma unroll
+                        for (int i = 0; i < 4; i++) o[e][i] = o[e][i] * alpha;
+                    m = mn;
+                }
+                const float mu = (m == -INFINITY) ? 0.0f : m;
+                // lane (lq, g)'s V operands of key slot (kt, r): V[16kt + 4g + r][64e + 4lq .. +3]
+                auto vread = [&](int kt, int r, float4* vv) __attribute__((always_inline)) {
+                    const float* vrow = &sV[buf][(16 * kt + 4 * g + r) * RS + 4 * lq];
+        #pragma unroll
+                    for (int e = 0; e < DS; e++) vv[e] = *reinterpret_cast<const float4*>(vrow + 64 * e);
+                };
+                float4 vv[2][DS];
+                vread(0, 0, vv[0]);
+        #pragma unroll
+                for (int kt = 0; kt < BK / 16; kt++) {
+        #pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int cur = (4 * kt + r) & 1;
+                        // the next key slot's operands while these products run
+                        if (4 * kt + r + 1 < BK / 4) vread((4 * kt + r + 1) >> 2, (r + 1) & 3, vv[cur ^ 1]);
+                        // exp2 of a value <= RESCALE_SLACK; v_exp_f32 flushes results
+                        // below 2^-126 to zero, a change far below the f32 tolerance
+                        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], scl, -mu));
+                        l = l + p;
+        #pragma unroll
+                        for (int e = 0; e < DS; e++) {
+                            o[e][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[cur][e].x, p, o[e][0], 0, 0, 0);
+                            o[e][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[cur][e].y, p, o[e][1], 0, 0, 0);
+                            o[e][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[cur][e].z, p, o[e][2], 0, 0, 0);
+                            o[e][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[cur][e].w, p, o[e][3], 0, 0, 0);
+                        }
+                    }
+                }
+                if (t + 1 < t_end) lstore(buf ^ 1);
+                __syncthreads();
             }
-        }
-        if (t + 1 < t_end) lstore(buf ^ 1);
-        __syncthreads();
-    }
 
-    l = wave_xor_sum(l);
-    if (qi >= L) return;
-    const int64_t row = ((int64_t)b * Hq + h) * L + qi;
-    if (nsplit_row == 1) {
-        const float inv = 1.0f / l;
-        float* op = Og + row * D;
+
+        l = wave_xor_sum(l);
+        if (qi >= L) return;
+        // lane (q, g) holds d = 64e + 16g + 4r + dt in o[e][dt][r]
+        if (slot < 0) {
+            const int64_t row = bh * L + qi;
+            const float inv = 1.0f / l;
+            float* op = Og + row * D;
 #pragma unroll
-        for (int dt = 0; dt < D / 16; dt++)
-            *reinterpret_cast<float4*>(op + 16 * dt + 4 * g) =
-                make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
-        if (lse && g == 0) lse[row] = m == -INFINITY ? NAN : m * LN2 + logf(l);
-    } else {
-        float* po = part_o + (row * nsplit + split) * D;
+            for (int e = 0; e < DS; e++)
 #pragma unroll
-        for (int dt = 0; dt < D / 16; dt++)
-            *reinterpret_cast<float4*>(po + 16 * dt + 4 * g) = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
-        if (g == 0) part_ml[row * nsplit + split] = make_float2(m, l);
+                for (int r = 0; r < 4; r++)
+                    *reinterpret_cast<float4*>(op + 64 * e + 16 * g + 4 * r) =
+                        make_float4(o[e][0][r] * inv, o[e][1][r] * inv, o[e][2][r] * inv, o[e][3][r] * inv);
+            if (lse && g == 0) lse[row] = m == -INFINITY ? NAN : m * LN2 + logf(l);
+        } else {
+            const int64_t prow = (int64_t)slot * BQ + w * 16 + lq;
+            float* po = part_o + prow * D;
+#pragma unroll
+            for (int e = 0; e < DS; e++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    *reinterpret_cast<float4*>(po + 64 * e + 16 * g + 4 * r) =
+                        make_float4(o[e][0][r], o[e][1][r], o[e][2][r], o[e][3][r]);
+            if (g == 0) part_ml[prow] = make_float2(m, l);
+        }
+    };
+
+    int64_t u = geo.lo(gw);
+    bool first = true;
+    while (u < u_hi) {  // uniform over the workgroup
+        int64_t bh;
+        int qt, t0;
+        geo.locate(u, bh, qt, t0);
+        const int n = geo.nt(qt);
+        const int t1 = (int)(t0 + (u_hi - u) < n ? t0 + (u_hi - u) : n);
+        block(bh, qt, t0, t1, (t0 == 0 && t1 == n) ? -1 : (int)(2 * gw + (first ? 0 : 1)));
+        u += t1 - t0;
+        first = false;
     }
 }
 
-// Merge the partials of the rows whose key range was split. 1-D grid over
-// (row block, batch*head) for query rows row_lo .. L-1 (a causal row's tile
-// count grows with its query block, so the split rows are the last ones);
-// D/4 threads per row, each merging four output columns of every split with
-// float4 loads.
-template <int D, typename OT>
+// Merges the partials of the query blocks that workgroup boundaries cut, in
+// workgroup order. Boundary gb (the first unit of workgroup gb, gb >= 1)
+// handles the block it falls inside if it is that block's first boundary;
+// D/4 threads per row, each merging four output columns with float4 loads.
+// Partial slots: the block's first workgroup g_lo holds it in slot 2 g_lo + 1
+// if the block is not where g_lo started, else 2 g_lo; every later one, which
+// starts inside the block, in slot 2g.
+template <int D>
 __global__ __launch_bounds__(256) void k_prefill_combine(const float* __restrict__ part_o,
-                                                       const float2* __restrict__ part_ml, int L, int S, int causal,
-                                                       int bq, int bk, int target, int nsplit, int row_lo,
-                                                       int nrb, OT* __restrict__ out, float* __restrict__ lse) {
-    constexpr int TPR = D / 4;      // threads per row
-    constexpr int RPB = 256 / TPR;  // rows per workgroup
-    const int rb = (int)(blockIdx.x % (unsigned)nrb);
-    const int64_t bh = blockIdx.x / (unsigned)nrb;
-    const int qi = row_lo + rb * RPB + (int)threadIdx.x / TPR;
+                                                       const float2* __restrict__ part_ml, const SkGeo geo, int L,
+                                                       float* __restrict__ out, float* __restrict__ lse) {
+    constexpr int TPR = D / 4;           // threads per row
+    constexpr int RPB = 256 / TPR;       // rows per workgroup
+    constexpr int NRB = PF_BQ / RPB;     // workgroups per query block
+    const int64_t gb = 1 + (int64_t)(blockIdx.x / NRB);
+    const int rg = (int)(blockIdx.x % NRB);
+    if (gb >= geo.G) return;
+    const int64_t ub = geo.lo(gb);
+    int64_t bh;
+    int qt, t0;
+    geo.locate(ub, bh, qt, t0);
+    const int64_t u0 = ub - t0;                  // the block's first unit
+    if (t0 == 0 || geo.lo(gb - 1) > u0) return;  // no cut here, or an earlier boundary's block
+    const int n = geo.nt(qt);
+    const int64_t g_lo = gb - 1, g_hi = geo.wg_of(u0 + n - 1);
+    const int r = rg * RPB + (int)threadIdx.x / TPR;
     const int c4 = ((int)threadIdx.x % TPR) * 4;
+    const int qi = qt * PF_BQ + r;
     if (qi >= L) return;
-    const int q0 = qi / bq * bq;
-    const int kend = causal ? min(S, q0 + bq) : S;
-    const int ns = row_splits((kend + bk - 1) / bk, target);
-    if (ns <= 1) return;  // written directly by the prefill kernel
-    const int64_t row = bh * L + qi;
-    const float2* ml = part_ml + row * nsplit;
-    const float* pr = part_o + row * nsplit * D + c4;
-    // the first CMAX splits' partials are all requested before any is used
-    // (one memory round trip); rows with more splits loop for the rest
+    auto slot_of = [&](int64_t gg) { return gg == g_lo && geo.lo(g_lo) < u0 ? 2 * gg + 1 : 2 * gg; };
+    // the first CMAX partials are all requested before any is used (one
+    // memory round trip); blocks cut more often loop for the rest
     constexpr int CMAX = 4;
+    const int64_t np = g_hi - g_lo + 1;
     float2 mlv[CMAX];
     float4 pv[CMAX];
 #pragma unroll
-    for (int s = 0; s < CMAX; s++) {
-        mlv[s] = s < ns ? ml[s] : make_float2(-INFINITY, 0.0f);
-        pv[s] = s < ns ? *reinterpret_cast<const float4*>(pr + s * D) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < CMAX; i++) {
+        mlv[i] = make_float2(-INFINITY, 0.0f);
+        pv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < np) {
+            const int64_t prow = slot_of(g_lo + i) * PF_BQ + r;
+            mlv[i] = part_ml[prow];
+            pv[i] = *reinterpret_cast<const float4*>(part_o + prow * D + c4);
+        }
     }
     float mm = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < CMAX; s++) mm = fmaxf(mm, mlv[s].x);  // absent splits hold -inf
-    for (int s = CMAX; s < ns; s++) mm = fmaxf(mm, ml[s].x);
+    for (int i = 0; i < CMAX; i++) mm = fmaxf(mm, mlv[i].x);  // absent partials hold -inf
+    for (int64_t i = CMAX; i < np; i++) mm = fmaxf(mm, part_ml[slot_of(g_lo + i) * PF_BQ + r].x);
     const float mu = (mm == -INFINITY) ? 0.0f : mm;
     float tl = 0.0f;
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
@@ -885,15 +1010,15 @@ __global__ __launch_bounds__(256) void k_prefill_combine(const float* __restrict
         a3 = a3 + v.w * f;
     };
 #pragma unroll
-    for (int s = 0; s < CMAX; s++)
-        if (s < ns) add(mlv[s], pv[s]);
-    for (int s = CMAX; s < ns; s++) add(ml[s], *reinterpret_cast<const float4*>(pr + s * D));
+    for (int i = 0; i < CMAX; i++)
+        if (i < np) add(mlv[i], pv[i]);
+    for (int64_t i = CMAX; i < np; i++) {
+        const int64_t prow = slot_of(g_lo + i) * PF_BQ + r;
+        add(part_ml[prow], *reinterpret_cast<const float4*>(part_o + prow * D + c4));
+    }
     const float inv = 1.0f / tl;
-    if constexpr (sizeof(OT) == 2)
-        *reinterpret_cast<uint2*>(out + row * D + c4) = make_uint2(pack2_bf16(a0 * inv, a1 * inv),
-                                                                   pack2_bf16(a2 * inv, a3 * inv));
-    else
-        *reinterpret_cast<float4*>(out + row * D + c4) = make_float4(a0 * inv, a1 * inv, a2 * inv, a3 * inv);
+    const int64_t row = bh * L + qi;
+    *reinterpret_cast<float4*>(out + row * D + c4) = make_float4(a0 * inv, a1 * inv, a2 * inv, a3 * inv);
     if (lse && c4 == 0) lse[row] = mm == -INFINITY ? NAN : mu * LN2 + logf(tl);
 }
 
@@ -1960,27 +2085,6 @@ tn_status refuse_head_dim(int64_t D) {
     return fail(TN_ENOTIMPL, buf);
 }
 
-// KV tiles per split for a prefill: long rows are split so that the longest
-// work item is about a quarter of the longest row once there are fewer query
-// blocks than it takes to fill the device; rows that fit stay whole.
-int prefill_tiles_per_split(int64_t B, int64_t Hq, int64_t L, int64_t S, int causal, int bk) {
-    const int64_t nqb = (L + PF_BQ - 1) / PF_BQ;
-    const int64_t kend = causal ? std::min<int64_t>(S, nqb * PF_BQ) : S;
-    const int64_t ntiles = (kend + bk - 1) / bk;
-    const int64_t items = B * Hq * nqb;
-    if (items >= 2048 || ntiles <= 8) return (int)std::max<int64_t>(ntiles, 1);
-    return (int)std::max<int64_t>(8, (ntiles + 3) / 4);
-}
-
-// First query row of the query blocks whose rows are split (L when none is):
-// a causal row's tile count grows with its block, so they are the last ones.
-int64_t first_split_row(int64_t L, int64_t S, int causal, int bq, int bk, int target) {
-    const int64_t nqb = cdiv(L, bq);
-    for (int64_t qt = 0; qt < nqb; qt++)
-        if (row_splits((int)cdiv(causal ? std::min<int64_t>(S, (qt + 1) * bq) : S, bk), target) > 1) return qt * bq;
-    return L;
-}
-
 // Work list of the bf16 prefill (see FlashWork). Items aim at the tiles of
 // the whole call spread over the device's resident workgroups (two per CU),
 // at least 16 tiles (1024 keys) each: a split row costs its items a
@@ -2249,23 +2353,33 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         return TN_OK;
     }
     const int bk = (D == 128) ? 32 : PF_BK;
-    const int64_t nqb = cdiv(L, PF_BQ);
-    const int64_t kend_max = is_causal ? std::min<int64_t>(S, nqb * PF_BQ) : S;
-    const int tiles_per = prefill_tiles_per_split(B, Hq, L, S, c, bk);
-    const int nsplit = (int)cdiv(cdiv(kend_max, bk), tiles_per);
+    // the stream-K grid: one workgroup per resident slot, at most one per unit
+    int slots = 0;
+    {
+        tn_status sp = resident_workgroups(D == 64 ? reinterpret_cast<const void*>(&k_fa_f32<64, 64, 0>)
+                                                    : reinterpret_cast<const void*>(&k_fa_f32<128, 32, 0>),
+                                           256, 0, &slots);
+        if (sp != TN_OK) return sp;
+    }
+    SkGeo geo;
+    geo.nqb = (int)cdiv(L, PF_BQ);
+    geo.NS = (int)cdiv(S, bk);
+    geo.c = PF_BQ / bk;
+    geo.causal = c;
+    geo.Tbh = geo.P(geo.nqb);
+    geo.T = B * Hq * geo.Tbh;
+    geo.G = std::min<int64_t>(std::max(slots, 1), geo.T);
     float* part_o = nullptr;
     float2* part_ml = nullptr;
-    if (nsplit > 1) {
-        const size_t po = (size_t)rows * nsplit * D * sizeof(float);
-        const size_t pm = (size_t)rows * nsplit * sizeof(float2);
+    if (geo.G > 1) {
+        const size_t po = (size_t)(2 * geo.G) * PF_BQ * D * sizeof(float);
+        const size_t pm = (size_t)(2 * geo.G) * PF_BQ * sizeof(float2);
         void* ws = nullptr;
         tn_status s = workspace(st, po + pm, &ws);
         if (s != TN_OK) return s;
         part_o = static_cast<float*>(ws);
         part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + po);
     }
-    if (nqb * nsplit > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": shape too large");
-    dim3 grid((unsigned)(nqb * nsplit), (unsigned)Hq, (unsigned)B);
     {
         auto qq = static_cast<const float*>(q);
         auto kk = static_cast<const float*>(k);
@@ -2273,8 +2387,8 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         auto oo = static_cast<float*>(out);
         // an f32 query takes an f32 mask (mk 1) or a bool one (mk 3)
 #define TN_FA(DD, BKK, MK)                                                                                       \
-    hipLaunchKernelGGL((k_fa_f32<DD, BKK, MK>), grid, dim3(256), 0, st, qq, kk, vv, (int)Hq, (int)Hkv, (int)L,   \
-                       (int)S, sl2, c, tiles_per, nsplit, oo, lse, part_o, part_ml, mref)
+    hipLaunchKernelGGL((k_fa_f32<DD, BKK, MK>), dim3((unsigned)geo.G), dim3(256), 0, st, qq, kk, vv, (int)Hq,    \
+                       (int)Hkv, (int)L, (int)S, sl2, c, geo, oo, lse, part_o, part_ml, mref)
         if (D == 64) {
             if (mk == 1) TN_FA(64, 64, 1);
             else if (mk == 3) TN_FA(64, 64, 3);
@@ -2286,17 +2400,15 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         }
 #undef TN_FA
         TN_LAUNCHED();
-        if (nsplit > 1) {
-            const int64_t row_lo = first_split_row(L, S, c, PF_BQ, bk, tiles_per);
-            const int64_t nrb = cdiv(L - row_lo, 256 / (D / 4));
-            if (nrb * B * Hq > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": shape too large");
-            const dim3 g2((unsigned)(nrb * B * Hq));
+        if (geo.G > 1) {
+            // (G - 1) boundaries, PF_BQ rows each, 256 / (D/4) rows per workgroup
+            const int64_t nwg = (geo.G - 1) * (PF_BQ / (256 / (D / 4)));
             if (D == 64)
-                hipLaunchKernelGGL((k_prefill_combine<64, float>), g2, dim3(256), 0, st, part_o, part_ml, (int)L,
-                                   (int)S, c, PF_BQ, bk, tiles_per, nsplit, (int)row_lo, (int)nrb, oo, lse);
+                hipLaunchKernelGGL((k_prefill_combine<64>), dim3((unsigned)nwg), dim3(256), 0, st, part_o, part_ml, geo,
+                                   (int)L, oo, lse);
             else
-                hipLaunchKernelGGL((k_prefill_combine<128, float>), g2, dim3(256), 0, st, part_o, part_ml, (int)L,
-                                   (int)S, c, PF_BQ, bk, tiles_per, nsplit, (int)row_lo, (int)nrb, oo, lse);
+                hipLaunchKernelGGL((k_prefill_combine<128>), dim3((unsigned)nwg), dim3(256), 0, st, part_o, part_ml,
+                                   geo, (int)L, oo, lse);
             TN_LAUNCHED();
         }
     }
