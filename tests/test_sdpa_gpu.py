@@ -131,6 +131,22 @@ def test_config2_causal_gqa_prefill_at_full_size(tn, dtype):
     print(f"config 2 {dtype}: worst error {worst:.3f} of the bound", flush=True)
 
 
+@pytest.mark.parametrize("shape,causal", [
+    ((1, 1, 1, 64, 4096, 64), False),   # one query block of 64 key tiles: 64 workgroups, 64 partials
+    ((1, 2, 1, 70, 3000, 128), False),  # two blocks per head of 94 32-key tiles, each cut into 94 partials
+    ((1, 1, 1, 600, 600, 64), True),    # causal blocks of 1..10 tiles over 55 units, one per workgroup
+])
+def test_f32_stream_partition_cuts_blocks_into_many_partials(tn, shape, causal):
+    """The f32 prefill cuts its (head, query block, key tile) units into
+    equal ranges over the resident workgroups, at most one workgroup per
+    unit. A short query range over long keys therefore splits each query
+    block across dozens of workgroups; the combine merges them past its
+    first batch of eight, in workgroup order."""
+    b, hq, hkv, l, s, d = shape
+    q, k, v = _det((b, hq, l, d), 11), _det((b, hkv, s, d), 12), _det((b, hkv, s, d), 13)
+    _check(tn, "float32", q, k, v, causal)
+
+
 def test_default_scale_and_explicit_scale_agree(tn):
     rng = np.random.default_rng(5)
     q, k, v = (tn.tensor(rng.standard_normal(s).astype(np.float32), device="hip")

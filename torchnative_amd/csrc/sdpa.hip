@@ -980,7 +980,7 @@ __global__ __launch_bounds__(256) void k_prefill_combine(const float* __restrict
     auto slot_of = [&](int64_t gg) { return gg == g_lo && geo.lo(g_lo) < u0 ? 2 * gg + 1 : 2 * gg; };
     // the first CMAX partials are all requested before any is used (one
     // memory round trip); blocks cut more often loop for the rest
-    constexpr int CMAX = 4;
+    constexpr int CMAX = 8;
     const int64_t np = g_hi - g_lo + 1;
     float2 mlv[CMAX];
     float4 pv[CMAX];
