@@ -79,9 +79,9 @@ constexpr int F3_BQ = 64, F3_BK = 64;  // queries per workgroup; key tile of the
 // device-coherent stores (sc1: written through to memory, past this XCD's
 // L2), waits until they are acknowledged, and takes a ticket from the block's
 // counter. The item that draws the last ticket reads every split's partials
-// back with device-coherent loads and merges them in split order -- the
-// arithmetic of k_prefill_combine, so the result does not depend on which
-// item finishes last -- then returns the counter to zero for the next launch.
+// back with device-coherent loads and merges them in split order -- the same
+// arithmetic whichever item finishes last -- then returns the counter to zero
+// for the next launch.
 // No fence is needed: only the partials cross workgroups, and they never sit
 // in a non-coherent cache. The partial stride is nsplit (the launch's
 // maximum); rows of the block are contiguous from `row0`.
@@ -695,8 +695,8 @@ constexpr int PF_BQ = 64, PF_BK = 64;
 // writes a query block it covers whole straight to the output; a block cut
 // by a range boundary leaves an unnormalised (O, m, l) partial per
 // workgroup: in slot 2g if it is workgroup g's first block, else 2g + 1 (a
-// workgroup cuts at most its first and its last block), and
-// k_prefill_combine merges them in workgroup order.
+// workgroup cuts at most its first and its last block), and the workgroup
+// that finishes the block last merges them in workgroup order.
 struct SkGeo {
     int nqb, NS, c, causal;  // query blocks, key tiles of S, key tiles per query block (PF_BQ / BK)
     int64_t Tbh, T, G;       // units per (batch, head), all units, workgroups (G <= T)
@@ -731,7 +731,7 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
                                               float sl2, int causal, const SkGeo geo,
                                               float* __restrict__ Og, float* __restrict__ lse,
                                               float* __restrict__ part_o, float2* __restrict__ part_ml,
-                                              const MaskRef mask) {
+                                              uint32_t* __restrict__ tickets, const MaskRef mask) {
     constexpr int BQ = PF_BQ;
     constexpr int RS = D + 4;
     constexpr int CH = (BK * D / 4) / 256;  // float4 chunks of K (and of V) per thread
@@ -745,7 +745,8 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
 
     // query block qt of (batch, head) bh, key tiles t_begin .. t_end-1;
     // slot < 0: the whole block, written to the output
-    auto block = [&](int64_t bh, int qt, int t_begin, int t_end, int slot) __attribute__((always_inline)) {
+    __shared__ uint32_t s_ticket;
+    auto block = [&](int64_t bh, int qt, int t_begin, int t_end, int slot, int64_t u0) __attribute__((always_inline)) {
         const int h = (int)(bh % Hq), b = (int)(bh / Hq);
         const int kvh = h / (Hq / Hkv);
         const int q0 = qt * BQ;
@@ -908,9 +909,9 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
 
 
         l = wave_xor_sum(l);
-        if (qi >= L) return;
         // lane (q, g) holds d = 64e + 16g + 4r + dt in o[e][dt][r]
         if (slot < 0) {
+            if (qi >= L) return;
             const int64_t row = bh * L + qi;
             const float inv = 1.0f / l;
             float* op = Og + row * D;
@@ -921,17 +922,100 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
                     *reinterpret_cast<float4*>(op + 64 * e + 16 * g + 4 * r) =
                         make_float4(o[e][0][r] * inv, o[e][1][r] * inv, o[e][2][r] * inv, o[e][3][r] * inv);
             if (lse && g == 0) lse[row] = m == -INFINITY ? NAN : m * LN2 + logf(l);
-        } else {
-            const int64_t prow = (int64_t)slot * BQ + w * 16 + lq;
-            float* po = part_o + prow * D;
+            return;
+        }
+        // A cut block: publish this workgroup's (O, m, l) with device-coherent
+        // stores (sc1: written through to memory, past this XCD's L2), wait
+        // until they are acknowledged, and take a ticket from the block's
+        // counter. The workgroup that draws the last ticket reads every
+        // partial back with device-coherent loads, merges them in workgroup
+        // order and returns the counter to zero for the next launch. No
+        // fence is needed: only the partials cross workgroups, and they never
+        // sit in a non-coherent cache.
+        constexpr uint32_t SC1 = 16;  // cache policy: device scope
+        typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const buf_rsrc ro = make_rsrc(part_o, (uint32_t)(2 * geo.G * BQ * D * 4));
+        const buf_rsrc rm = make_rsrc(part_ml, (uint32_t)(2 * geo.G * BQ * 8));
+#if __HIP_DEVICE_COMPILE__
+        {
+            const uint32_t prow = (uint32_t)(slot * BQ + w * 16 + lq);
 #pragma unroll
             for (int e = 0; e < DS; e++)
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    *reinterpret_cast<float4*>(po + 64 * e + 16 * g + 4 * r) =
-                        make_float4(o[e][0][r], o[e][1][r], o[e][2][r], o[e][3][r]);
-            if (g == 0) part_ml[prow] = make_float2(m, l);
+                for (int r = 0; r < 4; r++) {
+                    const u32x4_t v = {__float_as_uint(o[e][0][r]), __float_as_uint(o[e][1][r]),
+                                       __float_as_uint(o[e][2][r]), __float_as_uint(o[e][3][r])};
+                    __builtin_amdgcn_raw_buffer_store_b128(v, ro, (prow * D + 64 * e + 16 * g + 4 * r) * 4u, 0, SC1);
+                }
+            if (g == 0) {
+                const u32x2_t v = {__float_as_uint(m), __float_as_uint(l)};
+                __builtin_amdgcn_raw_buffer_store_b64(v, rm, prow * 8u, 0, SC1);
+            }
         }
+#endif
+        wait_vmcnt<0>();  // this thread's partials are acknowledged by memory
+        const int n = geo.nt(qt);
+        const int64_t g_lo = geo.wg_of(u0), g_hi = geo.wg_of(u0 + n - 1);
+        const int64_t tk = bh * geo.nqb + qt;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            s_ticket = __hip_atomic_fetch_add(tickets + tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (s_ticket != (uint32_t)(g_hi - g_lo)) return;  // uniform: another workgroup merges the block
+        // g_lo holds the block in slot 2 g_lo + 1 unless the block is where it
+        // started; every later workgroup starts inside the block: slot 2g
+        const int64_t s_lo = 2 * g_lo + (geo.lo(g_lo) < u0 ? 1 : 0);
+        const int np = (int)(g_hi - g_lo + 1);
+#if __HIP_DEVICE_COMPILE__
+        constexpr int TPR = D / 4;  // threads per row, four columns each
+        constexpr int CMAX = 8;     // partials whose loads are in flight together
+        const int c4 = (tid % TPR) * 4;
+        for (int rr = tid / TPR; rr < BQ; rr += 256 / TPR) {
+            const int qrow = qt * BQ + rr;
+            if (qrow >= L) break;
+            auto prow_of = [&](int i) { return (uint32_t)((i == 0 ? s_lo : 2 * (g_lo + i)) * BQ + rr); };
+            typedef float f32x2_t __attribute__((ext_vector_type(2)));
+            typedef float f32x4_t __attribute__((ext_vector_type(4)));
+            auto ld_ml = [&](int i) {
+                return __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rm, prow_of(i) * 8u, 0, SC1));
+            };
+            auto ld_o = [&](int i) {
+                return __builtin_bit_cast(f32x4_t,
+                                          __builtin_amdgcn_raw_buffer_load_b128(ro, (prow_of(i) * D + c4) * 4u, 0, SC1));
+            };
+            f32x2_t mlv[CMAX];
+            f32x4_t pv[CMAX];
+#pragma unroll
+            for (int i = 0; i < CMAX; i++) {
+                mlv[i] = i < np ? ld_ml(i) : (f32x2_t){-INFINITY, 0.0f};
+                pv[i] = i < np ? ld_o(i) : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+            }
+            float mm = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < CMAX; i++) mm = fmaxf(mm, mlv[i][0]);  // absent partials hold -inf
+            for (int i = CMAX; i < np; i++) mm = fmaxf(mm, ld_ml(i)[0]);
+            const float mu = (mm == -INFINITY) ? 0.0f : mm;
+            float tl = 0.0f, a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+            auto add = [&](f32x2_t m_l, f32x4_t v) {
+                const float f = exp2f(m_l[0] - mu);
+                tl = tl + m_l[1] * f;
+                a0 = a0 + v[0] * f;
+                a1 = a1 + v[1] * f;
+                a2 = a2 + v[2] * f;
+                a3 = a3 + v[3] * f;
+            };
+#pragma unroll
+            for (int i = 0; i < CMAX; i++)
+                if (i < np) add(mlv[i], pv[i]);
+            for (int i = CMAX; i < np; i++) add(ld_ml(i), ld_o(i));
+            const float inv = 1.0f / tl;
+            const int64_t row = bh * L + qrow;
+            *reinterpret_cast<float4*>(Og + row * D + c4) = make_float4(a0 * inv, a1 * inv, a2 * inv, a3 * inv);
+            if (lse && c4 == 0) lse[row] = mm == -INFINITY ? NAN : mu * LN2 + logf(tl);
+        }
+#endif
+        if (tid == 0) __hip_atomic_store(tickets + tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
 
     int64_t u = geo.lo(gw);
@@ -942,84 +1026,10 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
         geo.locate(u, bh, qt, t0);
         const int n = geo.nt(qt);
         const int t1 = (int)(t0 + (u_hi - u) < n ? t0 + (u_hi - u) : n);
-        block(bh, qt, t0, t1, (t0 == 0 && t1 == n) ? -1 : (int)(2 * gw + (first ? 0 : 1)));
+        block(bh, qt, t0, t1, (t0 == 0 && t1 == n) ? -1 : (int)(2 * gw + (first ? 0 : 1)), u - t0);
         u += t1 - t0;
         first = false;
     }
-}
-
-// Merges the partials of the query blocks that workgroup boundaries cut, in
-// workgroup order. Boundary gb (the first unit of workgroup gb, gb >= 1)
-// handles the block it falls inside if it is that block's first boundary;
-// D/4 threads per row, each merging four output columns with float4 loads.
-// Partial slots: the block's first workgroup g_lo holds it in slot 2 g_lo + 1
-// if the block is not where g_lo started, else 2 g_lo; every later one, which
-// starts inside the block, in slot 2g.
-template <int D>
-__global__ __launch_bounds__(256) void k_prefill_combine(const float* __restrict__ part_o,
-                                                       const float2* __restrict__ part_ml, const SkGeo geo, int L,
-                                                       float* __restrict__ out, float* __restrict__ lse) {
-    constexpr int TPR = D / 4;           // threads per row
-    constexpr int RPB = 256 / TPR;       // rows per workgroup
-    constexpr int NRB = PF_BQ / RPB;     // workgroups per query block
-    const int64_t gb = 1 + (int64_t)(blockIdx.x / NRB);
-    const int rg = (int)(blockIdx.x % NRB);
-    if (gb >= geo.G) return;
-    const int64_t ub = geo.lo(gb);
-    int64_t bh;
-    int qt, t0;
-    geo.locate(ub, bh, qt, t0);
-    const int64_t u0 = ub - t0;                  // the block's first unit
-    if (t0 == 0 || geo.lo(gb - 1) > u0) return;  // no cut here, or an earlier boundary's block
-    const int n = geo.nt(qt);
-    const int64_t g_lo = gb - 1, g_hi = geo.wg_of(u0 + n - 1);
-    const int r = rg * RPB + (int)threadIdx.x / TPR;
-    const int c4 = ((int)threadIdx.x % TPR) * 4;
-    const int qi = qt * PF_BQ + r;
-    if (qi >= L) return;
-    auto slot_of = [&](int64_t gg) { return gg == g_lo && geo.lo(g_lo) < u0 ? 2 * gg + 1 : 2 * gg; };
-    // the first CMAX partials are all requested before any is used (one
-    // memory round trip); blocks cut more often loop for the rest
-    constexpr int CMAX = 8;
-    const int64_t np = g_hi - g_lo + 1;
-    float2 mlv[CMAX];
-    float4 pv[CMAX];
-#pragma unroll
-    for (int i = 0; i < CMAX; i++) {
-        mlv[i] = make_float2(-INFINITY, 0.0f);
-        pv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (i < np) {
-            const int64_t prow = slot_of(g_lo + i) * PF_BQ + r;
-            mlv[i] = part_ml[prow];
-            pv[i] = *reinterpret_cast<const float4*>(part_o + prow * D + c4);
-        }
-    }
-    float mm = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < CMAX; i++) mm = fmaxf(mm, mlv[i].x);  // absent partials hold -inf
-    for (int64_t i = CMAX; i < np; i++) mm = fmaxf(mm, part_ml[slot_of(g_lo + i) * PF_BQ + r].x);
-    const float mu = (mm == -INFINITY) ? 0.0f : mm;
-    float tl = 0.0f;
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    auto add = [&](float2 m_l, float4 v) {
-        const float f = exp2f(m_l.x - mu);
-        tl = tl + m_l.y * f;
-        a0 = a0 + v.x * f;
-        a1 = a1 + v.y * f;
-        a2 = a2 + v.z * f;
-        a3 = a3 + v.w * f;
-    };
-#pragma unroll
-    for (int i = 0; i < CMAX; i++)
-        if (i < np) add(mlv[i], pv[i]);
-    for (int64_t i = CMAX; i < np; i++) {
-        const int64_t prow = slot_of(g_lo + i) * PF_BQ + r;
-        add(part_ml[prow], *reinterpret_cast<const float4*>(part_o + prow * D + c4));
-    }
-    const float inv = 1.0f / tl;
-    const int64_t row = bh * L + qi;
-    *reinterpret_cast<float4*>(out + row * D + c4) = make_float4(a0 * inv, a1 * inv, a2 * inv, a3 * inv);
-    if (lse && c4 == 0) lse[row] = mm == -INFINITY ? NAN : mu * LN2 + logf(tl);
 }
 
 // ---------------------------------------------------------------------------
@@ -2371,6 +2381,7 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     geo.G = std::min<int64_t>(std::max(slots, 1), geo.T);
     float* part_o = nullptr;
     float2* part_ml = nullptr;
+    uint32_t* tick = nullptr;
     if (geo.G > 1) {
         const size_t po = (size_t)(2 * geo.G) * PF_BQ * D * sizeof(float);
         const size_t pm = (size_t)(2 * geo.G) * PF_BQ * sizeof(float2);
@@ -2379,6 +2390,9 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         if (s != TN_OK) return s;
         part_o = static_cast<float*>(ws);
         part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + po);
+        // one counter per (batch, head, query block); only cut blocks take tickets
+        s = tickets(st, (size_t)(B * Hq) * (size_t)geo.nqb, &tick);
+        if (s != TN_OK) return s;
     }
     {
         auto qq = static_cast<const float*>(q);
@@ -2388,7 +2402,7 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         // an f32 query takes an f32 mask (mk 1) or a bool one (mk 3)
 #define TN_FA(DD, BKK, MK)                                                                                       \
     hipLaunchKernelGGL((k_fa_f32<DD, BKK, MK>), dim3((unsigned)geo.G), dim3(256), 0, st, qq, kk, vv, (int)Hq,    \
-                       (int)Hkv, (int)L, (int)S, sl2, c, geo, oo, lse, part_o, part_ml, mref)
+                       (int)Hkv, (int)L, (int)S, sl2, c, geo, oo, lse, part_o, part_ml, tick, mref)
         if (D == 64) {
             if (mk == 1) TN_FA(64, 64, 1);
             else if (mk == 3) TN_FA(64, 64, 3);
@@ -2400,17 +2414,6 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         }
 #undef TN_FA
         TN_LAUNCHED();
-        if (geo.G > 1) {
-            // (G - 1) boundaries, PF_BQ rows each, 256 / (D/4) rows per workgroup
-            const int64_t nwg = (geo.G - 1) * (PF_BQ / (256 / (D / 4)));
-            if (D == 64)
-                hipLaunchKernelGGL((k_prefill_combine<64>), dim3((unsigned)nwg), dim3(256), 0, st, part_o, part_ml, geo,
-                                   (int)L, oo, lse);
-            else
-                hipLaunchKernelGGL((k_prefill_combine<128>), dim3((unsigned)nwg), dim3(256), 0, st, part_o, part_ml,
-                                   geo, (int)L, oo, lse);
-            TN_LAUNCHED();
-        }
     }
     return TN_OK;
 }
