@@ -1238,6 +1238,16 @@ void k_decode_sk_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restric
     typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
     __shared__ int s_len[SK_MAXB];
     __shared__ int s_pre[SK_MAXB + 1];  // G * (units of sequences 0 .. b-1); the host checks it fits
+    // K of each ring slot, per wave: the chunk's CH * 16 rows, brought in by
+    // LDS DMA 1 KB (whole rows) per instruction and read back in the MFMA's
+    // layout. Row r's 16-byte chunk c sits at physical chunk c ^ (r % CPR), so
+    // the sixteen rows one read instruction touches hit distinct banks. One
+    // LDS object per slot lets the compiler tell a read of one slot from the
+    // DMA landing in another.
+    constexpr int KT_ELEMS = CH * 16 * D;  // 4 KB of K per chunk
+    constexpr int CPR = D / 8;             // 16-byte chunks per K row
+    __shared__ __align__(16) uint16_t sK0[4][KT_ELEMS], sK1[4][KT_ELEMS], sK2[4][KT_ELEMS], sK3[4][KT_ELEMS];
+    static_assert(NB <= 4 && KT_ELEMS * 2 == 4096, "K ring slots");
 
     const int groups = nrep / NR;
     const int G = Hkv * groups;  // segments per sequence
@@ -1340,11 +1350,23 @@ void k_decode_sk_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restric
     };
 
     struct Buf {
-        u32x4_t k[CH][D / 32];
         vchunk v[CH][4];
         u32x4_t q[D / 32];
     };
-    auto load = [&](Buf& f, const Chunk& c) {
+    const int wq = (int)(threadIdx.x >> 6);  // this wave's K slots
+    auto kslot = [&](int j) -> uint16_t* {
+        return j == 0 ? sK0[wq] : j == 1 ? sK1[wq] : j == 2 ? sK2[wq] : sK3[wq];
+    };
+    // lane's source offset (bytes, from the chunk's first row) for its i-th
+    // K DMA: LDS position p = 64 i + lane holds row p / CPR, logical chunk
+    // (p % CPR) ^ (row % CPR)
+    uint32_t kvoff[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int p = 64 * i + lane, row = p / CPR;
+        kvoff[i] = (uint32_t)((row * D + (((p % CPR) ^ (row % CPR)) * 8)) * 2);
+    }
+    auto load = [&](Buf& f, const Chunk& c, int j) {
         const int cb = rfl(c.b), csg = rfl(c.sg), ck0 = rfl(c.key0), cnk = rfl(c.nk);
         const int kvh = csg / groups, grp = csg % groups;
         const int64_t row0 = ((int64_t)cb * Hkv + kvh) * cap + ck0;
@@ -1355,12 +1377,15 @@ void k_decode_sk_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restric
                                       cnk ? (uint32_t)(NR * D * 2) : 0u);
 #if __HIP_DEVICE_COMPILE__
         constexpr int NT = 2;  // cache policy: non-temporal, the caches are read once
+        {
+            uint16_t* ks = kslot(j);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(ks + 512 * i),
+                                                         16, kvoff[i], 0, 0, NT);
+        }
 #pragma unroll
         for (int kt = 0; kt < CH; kt++) {
-#pragma unroll
-            for (int cc = 0; cc < D / 32; cc++)
-                f.k[kt][cc] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rk, (uint32_t)(((16 * kt + lq) * D + 32 * cc + 8 * g) * 2), 0, NT);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const uint32_t off = (uint32_t)(((16 * kt + 4 * g + r) * D + DL * lq) * 2);
@@ -1388,15 +1413,19 @@ void k_decode_sk_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restric
         for (int e = 0; e < DL; e++) o[hh][e] = 0.0f;
     float m = -INFINITY, l = 0.0f;  // this lane's head lq; l is the lane's share
 
-    auto compute = [&](const Buf& f, const Chunk& c) {
+    auto compute = [&](const Buf& f, const Chunk& c, int j) {
         f32x4 s[CH];
+        const uint16_t* ks = kslot(j);
 #pragma unroll
         for (int kt = 0; kt < CH; kt++) {
             s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            const int row = 16 * kt + lq;
 #pragma unroll
-            for (int cc = 0; cc < D / 32; cc++)
-                s[kt] = El<F16>::mfma16(__builtin_bit_cast(typename El<F16>::v8, f.k[kt][cc]),
-                                                                __builtin_bit_cast(typename El<F16>::v8, f.q[cc]), s[kt]);
+            for (int cc = 0; cc < D / 32; cc++) {
+                const u32x4_t ka = *reinterpret_cast<const u32x4_t*>(ks + row * D + (((4 * cc + g) ^ (row % CPR)) * 8));
+                s[kt] = El<F16>::mfma16(__builtin_bit_cast(typename El<F16>::v8, ka),
+                                        __builtin_bit_cast(typename El<F16>::v8, f.q[cc]), s[kt]);
+            }
         }
         float t[CH][4];
         float mx = -INFINITY;
@@ -1496,13 +1525,13 @@ void k_decode_sk_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restric
 #pragma unroll
     for (int i = 0; i < NB; i++) {
         c[i] = make();
-        load(f[i], c[i]);
+        load(f[i], c[i], i);
     }
     auto step = [&](int j) {
         if (c[j].nk == 0) return false;
-        compute(f[j], c[j]);
+        compute(f[j], c[j], j);
         c[j] = make();
-        load(f[j], c[j]);
+        load(f[j], c[j], j);
         __builtin_amdgcn_sched_barrier(0);
         return true;
     };
