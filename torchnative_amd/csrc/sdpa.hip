@@ -667,7 +667,11 @@ __global__ __launch_bounds__(256) void k_attn_any(const void* __restrict__ Qg, c
     }
 }
 
-constexpr int PF_BQ = 64, PF_BK = 64;
+// Eight waves per workgroup: each K/V tile staged in LDS serves 128 queries
+// (half the staging per product of a four-wave workgroup). At 121-149 VGPRs
+// two such workgroups share a CU.
+constexpr int PF_WAVES = 8, PF_THREADS = 64 * PF_WAVES;
+constexpr int PF_BQ = 16 * PF_WAVES, PF_BK = 64;
 
 
 // ---------------------------------------------------------------------------
@@ -688,7 +692,7 @@ constexpr int PF_BQ = 64, PF_BK = 64;
 // ---------------------------------------------------------------------------
 
 // Stream-K partition of the f32 prefill. A unit is one key tile of one
-// 64-query block; units run over (batch * head, query block, key tile) in
+// PF_BQ-query block; units run over (batch * head, query block, key tile) in
 // that order, a query block qt having nt(qt) key tiles. The persistent grid's
 // G workgroups take equal unit ranges [g T / G, (g+1) T / G), so every
 // workgroup does the same MFMA work whatever the causal shape. A workgroup
@@ -726,7 +730,7 @@ struct SkGeo {
 // MASK: 1 adds an f32 mask, 3 a bool one (MaskRef), to the scaled scores
 // (aten.rs:10383-10389)
 template <int D, int BK, int MASK = 0>
-__global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, const float* __restrict__ Kg,
+__global__ __launch_bounds__(PF_THREADS) void k_fa_f32(const float* __restrict__ Qg, const float* __restrict__ Kg,
                                               const float* __restrict__ Vg, int Hq, int Hkv, int L, int S,
                                               float sl2, int causal, const SkGeo geo,
                                               float* __restrict__ Og, float* __restrict__ lse,
@@ -734,7 +738,8 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
                                               uint32_t* __restrict__ tickets, const MaskRef mask) {
     constexpr int BQ = PF_BQ;
     constexpr int RS = D + 4;
-    constexpr int CH = (BK * D / 4) / 256;  // float4 chunks of K (and of V) per thread
+    constexpr int CH = (BK * D / 4) / PF_THREADS;  // float4 chunks of K (and of V) per thread
+    static_assert(CH * PF_THREADS == BK * D / 4, "tile staging");
     __shared__ __align__(16) float sK[2][BK * RS];
     __shared__ __align__(16) float sV[2][BK * RS];
 
@@ -782,7 +787,7 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
             auto gload = [&](int k0) {
         #pragma unroll
                 for (int it = 0; it < CH; it++) {
-                    const int c = tid + it * 256;
+                    const int c = tid + it * PF_THREADS;
                     const int r = c / (D / 4), part = c % (D / 4);
                     kr[it] = vr[it] = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (k0 + r < S) {
@@ -794,7 +799,7 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
             auto lstore = [&](int buf) {
         #pragma unroll
                 for (int it = 0; it < CH; it++) {
-                    const int c = tid + it * 256;
+                    const int c = tid + it * PF_THREADS;
                     const int r = c / (D / 4), part = c % (D / 4);
                     *reinterpret_cast<float4*>(&sK[buf][r * RS + part * 4]) = kr[it];
                     *reinterpret_cast<float4*>(&sV[buf][r * RS + part * 4]) = vr[it];
@@ -971,7 +976,7 @@ __global__ __launch_bounds__(256) void k_fa_f32(const float* __restrict__ Qg, co
         constexpr int TPR = D / 4;  // threads per row, four columns each
         constexpr int CMAX = 8;     // partials whose loads are in flight together
         const int c4 = (tid % TPR) * 4;
-        for (int rr = tid / TPR; rr < BQ; rr += 256 / TPR) {
+        for (int rr = tid / TPR; rr < BQ; rr += PF_THREADS / TPR) {
             const int qrow = qt * BQ + rr;
             if (qrow >= L) break;
             auto prow_of = [&](int i) { return (uint32_t)((i == 0 ? s_lo : 2 * (g_lo + i)) * BQ + rr); };
@@ -2397,7 +2402,7 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     {
         tn_status sp = resident_workgroups(D == 64 ? reinterpret_cast<const void*>(&k_fa_f32<64, 64, 0>)
                                                     : reinterpret_cast<const void*>(&k_fa_f32<128, 32, 0>),
-                                           256, 0, &slots);
+                                           PF_THREADS, 0, &slots);
         if (sp != TN_OK) return sp;
     }
     SkGeo geo;
@@ -2430,8 +2435,8 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
         auto oo = static_cast<float*>(out);
         // an f32 query takes an f32 mask (mk 1) or a bool one (mk 3)
 #define TN_FA(DD, BKK, MK)                                                                                       \
-    hipLaunchKernelGGL((k_fa_f32<DD, BKK, MK>), dim3((unsigned)geo.G), dim3(256), 0, st, qq, kk, vv, (int)Hq,    \
-                       (int)Hkv, (int)L, (int)S, sl2, c, geo, oo, lse, part_o, part_ml, tick, mref)
+    hipLaunchKernelGGL((k_fa_f32<DD, BKK, MK>), dim3((unsigned)geo.G), dim3(PF_THREADS), 0, st, qq, kk, vv,      \
+                       (int)Hq, (int)Hkv, (int)L, (int)S, sl2, c, geo, oo, lse, part_o, part_ml, tick, mref)
         if (D == 64) {
             if (mk == 1) TN_FA(64, 64, 1);
             else if (mk == 3) TN_FA(64, 64, 3);
