@@ -214,12 +214,14 @@ def test_fused_decode_linear_equals_the_separate_ops(tn, k, n):
 
 
 SMALL = OD.LlamaConfig(n_layers=2, hidden=128, n_heads=2, n_kv_heads=1, head_dim=64, inter=256, vocab=512)
+SMALL128 = OD.LlamaConfig(n_layers=2, hidden=256, n_heads=2, n_kv_heads=1, head_dim=128, inter=256, vocab=512)
 
 
-# cap 24: the fused split attention merged in the o projection; cap 600 (more
-# than 8 splits of 64 keys): RoPE + append, split-KV attention and its combine
-@pytest.mark.parametrize("cap", [24, 600])
-def test_decode_step_matches_the_oracle_teacher_forced(tn, cap):
+# cap 24: the fused split attention merged in the o projection (head dim 64
+# and 128); cap 600 (more than 8 splits of 64 keys): RoPE + append, split-KV
+# attention and its combine
+@pytest.mark.parametrize("cfg,cap", [(SMALL, 24), (SMALL, 600), (SMALL128, 24)], ids=["fused", "long", "fused-d128"])
+def test_decode_step_matches_the_oracle_teacher_forced(tn, cfg, cap):
     """A 2-layer model: the GPU's logits at every step within the bound of the
     oracle's float32 run on the same tokens, and its greedy token the
     oracle's wherever the oracle's top two logits are further apart than
@@ -228,9 +230,9 @@ def test_decode_step_matches_the_oracle_teacher_forced(tn, cap):
 
     prompt = [5, 77, 300, 12, 511, 0, 42, 9, 100, 250, 3, 64]
     n_new = 8
-    model = Q4Llama(SMALL, seed=11, cap=cap)
-    ref32 = OD.Decoder(SMALL, 11, cap, np.float32)
-    ref64 = OD.Decoder(SMALL, 11, cap, np.float64)
+    model = Q4Llama(cfg, seed=11, cap=cap)
+    ref32 = OD.Decoder(cfg, 11, cap, np.float32)
+    ref64 = OD.Decoder(cfg, 11, cap, np.float64)
     model.start(prompt)
     seq = list(prompt)
     for pos in range(len(prompt) + n_new - 1):
