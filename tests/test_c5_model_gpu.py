@@ -17,7 +17,7 @@ token (the step's argmax) must be the oracle's wherever the oracle's top two
 logits are further apart than twice the bound.
 
 Both attention paths of the step: cap 384 runs the fused split attention
-(6 splits of 64 keys, merged in the o projection's prologue), cap 600 the
+(12 splits of 32 keys, merged in the o projection's prologue), cap 600 the
 RoPE + append kernel, the split-KV decode attention and its combine.
 """
 
@@ -84,10 +84,10 @@ def test_config5_model_teacher_forced_against_the_oracle(tn, c5, cap):
           flush=True)
 
 
-# The fused split attention across several 64-key splits with a fresh row in
+# The fused split attention across several 32-key splits with a fresh row in
 # a later split, at config 5's head shape (head_dim 64, 3 query heads per kv
-# head) on a small model: a 150-token prompt crosses the 64- and 128-key split
-# boundaries, and cap 200 keeps the fused path (4 splits).
+# head) on a small model: a 150-token prompt crosses several split
+# boundaries, and cap 200 keeps the fused path (7 splits).
 NREP3 = OD.LlamaConfig(n_layers=2, hidden=384, n_heads=6, n_kv_heads=2, head_dim=64, inter=256, vocab=512)
 
 

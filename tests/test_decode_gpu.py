@@ -218,7 +218,7 @@ SMALL128 = OD.LlamaConfig(n_layers=2, hidden=256, n_heads=2, n_kv_heads=1, head_
 
 
 # cap 24: the fused split attention merged in the o projection (head dim 64
-# and 128); cap 600 (more than 8 splits of 64 keys): RoPE + append, split-KV
+# and 128); cap 600 (more than 16 splits of 32 keys): RoPE + append, split-KV
 # attention and its combine
 @pytest.mark.parametrize("cfg,cap", [(SMALL, 24), (SMALL, 600), (SMALL128, 24)], ids=["fused", "long", "fused-d128"])
 def test_decode_step_matches_the_oracle_teacher_forced(tn, cfg, cap):

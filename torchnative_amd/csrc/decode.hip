@@ -595,7 +595,7 @@ int64_t tn_llama_work_floats(const tn_llama* model) {
 }
 
 // One decode step. Per layer, for a cache of at most STEP_MAX_SPLITS *
-// STEP_SPLIT keys (four launches):
+// STEP_SPLIT keys (five launches):
 //   qkv = Q4(rmsnorm(h, ln1))                    linear_decode, RMSNorm prologue
 //   rope q, k; append k, v; split attention      k_step_attn -> partials
 //   h = h + Q4(merge(partials))                  linear_decode, PRO_COMBINE, residual

@@ -270,8 +270,8 @@ enum LinearPrologue { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU = 2, PRO_COMBINE =
 // Keys per workgroup of the decode step's fused attention, and the most
 // splits whose merge the o projection's prologue takes on; a longer cache
 // runs the split-KV attention with its own combine.
-constexpr int STEP_SPLIT = 64;
-constexpr int STEP_MAX_SPLITS = 8;
+constexpr int STEP_SPLIT = 32;
+constexpr int STEP_MAX_SPLITS = 16;
 
 // Prologue operands of the decode GEMV.
 struct GemvPro {
