@@ -5,7 +5,8 @@ linears bit for bit. The shapes are drawn once, at collection, from a fixed
 seed: odd lengths, q_len above and below kv_len, every GQA ratio the kernels
 take, head dims on the MFMA kernels and on the plain one, empty and
 truncated decode sequences, GEMV and GEMM row counts, rows of one block and
-long rows. Each case is sized so that the oracle finishes in a second or so.
+long rows, and bool masks broadcast from each shape the kernels read in
+place. Each case is sized so that the oracle finishes in a second or so.
 """
 
 import numpy as np
@@ -13,6 +14,7 @@ import pytest
 
 import oracle as O
 from test_sdpa_gpu import _check, _decode_case, _det
+from test_sdpa_mask_gpu import _bool_case
 
 pytestmark = pytest.mark.gpu
 
@@ -72,9 +74,29 @@ def _linear_cases(n, seed):
     return out
 
 
+def _mask_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        b = int(rng.integers(1, 3))
+        hkv = int(rng.choice([1, 2]))
+        hq = hkv * int(rng.choice([1, 2, 3, 4]))
+        d = int(rng.choice([64, 128, 80]))
+        l = int(rng.integers(1, 160))
+        s = int(rng.integers(1, 300))
+        shape = str(rng.choice(["full", "LS", "B1LS", "B11S"]))
+        density = float(rng.uniform(0.3, 0.95))
+        dtype = str(rng.choice(["float32", "bfloat16", "float16"]))
+        if b * hq * l * s * d > 40_000_000:
+            continue
+        out.append((b, hq, hkv, l, s, d, shape, density, dtype, int(rng.integers(0, 1 << 30))))
+    return out
+
+
 PREFILL = _prefill_cases(48, 2026)
 DECODE = _decode_cases(24, 2027)
 LINEAR = _linear_cases(36, 2028)
+MASKED = _mask_cases(24, 2029)
 
 
 @pytest.mark.parametrize("case", PREFILL, ids=[f"p{i}" for i in range(len(PREFILL))])
@@ -112,3 +134,18 @@ def test_linear_sweep(tn, case):
     bb = tn.tensor(bias, device="hip") if bias is not None else None
     got = tn._quantized_linear(tn.tensor(x, device="hip"), q, bb).numpy()
     assert got.tobytes() == want.tobytes(), np.argwhere(got != want)[:5]
+
+
+@pytest.mark.parametrize("case", MASKED, ids=[f"m{i}" for i in range(len(MASKED))])
+def test_bool_mask_sweep(tn, case):
+    """F.sdpa with a random bool mask, broadcast by strides from its own
+    shape; rows the mask hides entirely must come out NaN."""
+    b, hq, hkv, l, s, d, shape, density, dtype, seed = case
+    print("case", case, flush=True)
+    rng = np.random.default_rng(seed)
+    q, k, v = (rng.standard_normal(sh) for sh in ((b, hq, l, d), (b, hkv, s, d), (b, hkv, s, d)))
+    mshape = {"full": (b, hq, l, s), "LS": (l, s), "B1LS": (b, 1, l, s), "B11S": (b, 1, 1, s)}[shape]
+    mask = rng.random(mshape) < density
+    full = np.broadcast_to(mask, (b, hq, l, s))
+    nan_rows = [tuple(int(x) for x in r) for r in np.argwhere(~full.any(axis=-1))]
+    _bool_case(tn, dtype, q, k, v, mask, nan_rows=nan_rows)
