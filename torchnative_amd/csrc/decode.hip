@@ -31,13 +31,11 @@ __global__ __launch_bounds__(256) void k_embedding(const int32_t* __restrict__ i
 // k_embedding), and the cosine and sine of this position's RoPE angles,
 // cosf/sinf of pos * inv_freq[j] as k_rope computes them, so that every
 // layer's rotation reads them instead of evaluating both functions again.
-// It also clears the ticket of the step's argmax epilogue.
 __global__ __launch_bounds__(256) void k_step_begin(const int32_t* __restrict__ state,
                                                     const float* __restrict__ table, int64_t vocab, int dim,
                                                     float* __restrict__ h, const float* __restrict__ inv_freq,
-                                                    int half, float2* __restrict__ rope, uint32_t* ticket) {
+                                                    int half, float2* __restrict__ rope) {
     const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c == 0) *ticket = 0;  // the lm_head's argmax epilogue counts its workgroups from 0
     const int32_t id = state[2];
     if (c < dim) h[c] = (id >= 0 && id < vocab) ? table[(int64_t)id * dim + c] : NAN;
     if (blockIdx.x == 0 && threadIdx.x < half) {
@@ -447,7 +445,7 @@ __global__ void k_kv_append(const float* __restrict__ k, const float* __restrict
 
 // scratch layout of a decode step, in floats
 struct LlamaWork {
-    int64_t h, qkv, attn, gu, part_o, part_ml, rope, arg_v, arg_i, ticket, total;
+    int64_t h, qkv, attn, gu, part_o, part_ml, rope, arg_v, arg_i, total;
 };
 
 static LlamaWork llama_work(const tn_llama* m) {
@@ -469,8 +467,7 @@ static LlamaWork llama_work(const tn_llama* m) {
     w.part_ml = take(m->n_heads * nsplit * 2);
     w.rope = take(m->head_dim);  // (cos, sin) of the step's position per rotated pair
     w.arg_v = take(GEMV_ARG_MAX_PARTS);   // the lm_head's per-workgroup argmax (values
-    w.arg_i = take(GEMV_ARG_MAX_PARTS);   // and indices, as int32) and its ticket
-    w.ticket = take(1);
+    w.arg_i = take(GEMV_ARG_MAX_PARTS);   // and indices, as int32)
     w.total = o;
     return w;
 }
@@ -603,8 +600,8 @@ int64_t tn_llama_work_floats(const tn_llama* model) {
 //   h = h + Q4(silu(gate) * up)                  linear_decode, SiLU prologue
 // A longer cache replaces the middle two by k_rope_append, the split-KV decode
 // attention with its combine, and the o projection on its output.
-// Then logits = Q4(rmsnorm(h, norm)), with their argmax and the state's
-// advance in the same launch.
+// Then logits = Q4(rmsnorm(h, norm)) with per-workgroup argmax partials, and
+// one workgroup reducing them and advancing the state.
 // The fused linears are bit-identical to the separate ops (tn_rmsnorm,
 // tn_q4_0_linear, tn_add, tn_silu_mul); RoPE is tn_rope's arithmetic.
 tn_status tn_llama_step(void* stream, const tn_llama* m) {
@@ -619,7 +616,6 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
     float* part_o = m->work + w.part_o;
     float2* part_ml = reinterpret_cast<float2*>(m->work + w.part_ml);
     float2* rope = reinterpret_cast<float2*>(m->work + w.rope);
-    uint32_t* ticket = reinterpret_cast<uint32_t*>(m->work + w.ticket);
     const int64_t H = m->hidden, D = m->head_dim, Hq = m->n_heads, Hkv = m->n_kv_heads, I = m->inter;
     const int64_t nqkv = (Hq + 2 * Hkv) * D;
     const float eps = (float)m->eps;
@@ -642,7 +638,7 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
     comb.cap = (int)m->cap;
     const float sl2 = (float)(1.0 / std::sqrt((double)D)) * STEP_LOG2E;
     hipLaunchKernelGGL(k_step_begin, dim3((unsigned)cdiv(H, 256)), dim3(256), 0, st, m->state, m->embed, m->vocab,
-                       (int)H, h, m->inv_freq, (int)(D / 2), rope, ticket);
+                       (int)H, h, m->inv_freq, (int)(D / 2), rope);
     TN_LAUNCHED();
     for (int64_t l = 0; l < m->n_layers; l++) {
         const tn_llama_layer& L = m->layers[l];
@@ -682,10 +678,9 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
         TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, ln2, L.gate_up.qs, L.gate_up.d, 2 * I, nullptr, gu));
         TN_TRY(linear_decode(st, gu, I, PRO_SILU, none, L.down.qs, L.down.d, H, h, h));
     }
-    // the logits and, in the same launch, their argmax and the state's advance
+    // the logits with their argmax partials, then the argmax and the state's advance
     fin.arg_v = m->work + w.arg_v;
     fin.arg_i = reinterpret_cast<int32_t*>(m->work + w.arg_i);
-    fin.ticket = ticket;
     fin.state = m->state;
     fin.tokens = m->tokens;
     fin.prompt = m->prompt;

@@ -295,55 +295,48 @@ __device__ inline void block_arg_best(float& v, int& i) {
     }
 }
 
-// The argmax epilogue after a workgroup's last tile: its best output goes to
-// the partials with device-coherent stores (sc1: written through to memory,
-// past this XCD's non-coherent L2), the thread waits until they are
-// acknowledged, then takes a ticket (a relaxed agent-scope add). The
-// workgroup that draws the last ticket reads the partials back with
-// device-coherent loads, reduces them and advances the decode state as
-// k_argmax<true, ...> does. No fence is needed, as in sdpa.hip's split-row
-// merge: only the partials cross workgroups, and they never sit in a
-// non-coherent cache. (An acquire-release ticket at agent scope writes back
-// the XCD's whole L2 in every workgroup: measured 30.8 us for the C5 lm_head
-// launch against 9.0 us without the epilogue.)
-__device__ inline void gemv_argmax_epilogue(float v, int i, int n, const GemvPro& po) {
-    constexpr uint32_t SC1 = 16;  // cache policy: device scope
-    __shared__ int s_last;
-    const uint32_t parts = gridDim.x * 4u;
-    const buf_rsrc rv = make_rsrc(po.arg_v, parts), ri = make_rsrc(po.arg_i, parts);
+// The argmax epilogue after a workgroup's last tile: its best (value, index)
+// goes to arg_v/arg_i[workgroup] with plain stores. k_argmax_parts, the next
+// launch, reduces them: a kernel boundary is all the ordering the partials
+// need. (Reducing them inside this launch, the workgroup drawing the last
+// ticket reading the others' partials back, kept the lm_head on the step's
+// critical path for the stores' acknowledgement and the ticket's round trip:
+// 17.8 us for the C5 lm_head, against 9.0 us without the argmax.)
+__device__ inline void gemv_argmax_epilogue(float v, int i, const GemvPro& po) {
     block_arg_best(v, i);
-#if __HIP_DEVICE_COMPILE__
     if (threadIdx.x == 0) {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rv, blockIdx.x * 4u, 0, SC1);
-        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)i, ri, blockIdx.x * 4u, 0, SC1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // acknowledged by memory
-        const uint32_t t = __hip_atomic_fetch_add(po.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = t == gridDim.x - 1;
+        po.arg_v[blockIdx.x] = v;
+        po.arg_i[blockIdx.x] = i;
     }
-    __syncthreads();
-    if (!s_last) return;
-    v = -INFINITY;
-    i = INT32_MAX;
-    for (int g = threadIdx.x; g < (int)gridDim.x; g += GEMV_THREADS) {
-        const float gv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, (uint32_t)g * 4u, 0, SC1));
-        const int gi = (int)__builtin_amdgcn_raw_buffer_load_b32(ri, (uint32_t)g * 4u, 0, SC1);
+}
+
+// One workgroup: the best of `parts` (value, index) partials of an n-wide row
+// (argmax's order, arg_before), into state[3], then the decode step's
+// advance as k_argmax<true, ...> does.
+__global__ __launch_bounds__(GEMV_THREADS) void k_argmax_parts(const float* __restrict__ arg_v,
+                                                             const int32_t* __restrict__ arg_i, int parts, int n,
+                                                             int32_t* state, int32_t* tokens,
+                                                             const int32_t* __restrict__ prompt, int prompt_len,
+                                                             int cap) {
+    float v = -INFINITY;
+    int i = INT32_MAX;
+    for (int g = threadIdx.x; g < parts; g += GEMV_THREADS) {
+        const float gv = arg_v[g];
+        const int gi = arg_i[g];
         if (arg_before(gv, gi, v, i)) {
             v = gv;
             i = gi;
         }
     }
-    __syncthreads();  // block_arg_best's LDS is reused
     block_arg_best(v, i);
     if (threadIdx.x == 0) {
-        po.state[3] = i < n ? i : 0;
-        llama_advance(po.state, po.tokens, po.prompt, po.prompt_len, po.cap);
+        state[3] = i < n ? i : 0;
+        llama_advance(state, tokens, prompt, prompt_len, cap);
     }
-#endif
 }
 
-// Epilogue ARG (MR == 1, f32 y; linear_decode_argmax): argmax of y and the
-// decode step's advance, reduced over the workgroups through po.arg_v/arg_i
-// and a ticket (see GemvPro).
+// Epilogue ARG (MR == 1, f32 y; linear_decode_argmax): each workgroup's best
+// output of y to po.arg_v/arg_i[workgroup], for k_argmax_parts.
 template <int FMT, int MR, typename XT, int PRO, bool ARG = false>
 __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x, int K, int nb,
                                                      const uint8_t* __restrict__ qs,
@@ -609,7 +602,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
             dv[it] = dn[it];
         }
     }
-    if constexpr (ARG) gemv_argmax_epilogue(best_v, best_i, N, po);
+    if constexpr (ARG) gemv_argmax_epilogue(best_v, best_i, po);
 }
 
 // ---- prefill GEMM on MFMA ---------------------------------------------------------
@@ -1196,7 +1189,7 @@ tn_status check_weight(const char* op, const char* fmt, int64_t n, int64_t k) {
 template <int FMT, int MR, typename XT, int PRO = PRO_NONE, bool ARG = false>
 tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, const uint16_t* dw, int N,
                       const float* bias, void* y, int y_bf16, const float* resid = nullptr,
-                      const GemvPro& po = GemvPro()) {
+                      const GemvPro& po = GemvPro(), unsigned* grid_out = nullptr) {
     const int nb = K / QK;
     constexpr int ITEMS = Fmt<FMT>::GEMV_ITEMS;
     // rows per tile: as many as ITEMS items per thread allow, but no more
@@ -1233,6 +1226,7 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     hipLaunchKernelGGL((k_gemv<FMT, MR, XT, PRO, ARG>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N,
                        rows, bias, resid, y, y_bf16, po);
     TN_LAUNCHED();
+    if (grid_out) *grid_out = grid;
     return TN_OK;
 }
 
@@ -1409,9 +1403,16 @@ tn_status linear_decode_argmax(hipStream_t st, const float* x, int64_t k, const 
     tn_status s = check_weight("linear_decode_argmax", "q4_0", n, k);
     if (s != TN_OK) return s;
     if (k > LINEAR_DECODE_MAX_K || n > INT32_MAX || n < 1) return TN_ENOTIMPL;
-    if (!po.arg_v || !po.arg_i || !po.ticket || !po.state || !po.tokens || (po.prompt_len > 0 && !po.prompt))
+    if (!po.arg_v || !po.arg_i || !po.state || !po.tokens || (po.prompt_len > 0 && !po.prompt))
         return fail(TN_EINVAL, "linear_decode_argmax: missing argmax operands");
-    return launch_gemv<FMT_Q4_0, 1, float, PRO_RMSNORM, true>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, nullptr, po);
+    unsigned parts = 0;
+    s = launch_gemv<FMT_Q4_0, 1, float, PRO_RMSNORM, true>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, nullptr, po,
+                                                           &parts);
+    if (s != TN_OK) return s;
+    hipLaunchKernelGGL(k_argmax_parts, dim3(1), dim3(GEMV_THREADS), 0, st, po.arg_v, po.arg_i, (int)parts, (int)n,
+                       po.state, po.tokens, po.prompt, po.prompt_len, po.cap);
+    TN_LAUNCHED();
+    return TN_OK;
 }
 
 }  // namespace tn

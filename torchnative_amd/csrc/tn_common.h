@@ -285,24 +285,20 @@ struct GemvPro {
     const int32_t* len = nullptr;
     int nsplit = 0, head_dim = 0, cap = 0;
     // argmax epilogue (linear_decode_argmax): every workgroup's best (value,
-    // index) of y goes to arg_v/arg_i[workgroup]; the workgroup that takes
-    // the last ticket reduces them and advances the decode state (state,
-    // tokens, prompt, prompt_len, cap) as llama_advance. *ticket must be 0 at
-    // the launch; nothing resets it afterwards.
+    // index) of y goes to arg_v/arg_i[workgroup] (GEMV_ARG_MAX_PARTS
+    // entries); a one-workgroup launch then reduces them and advances the
+    // decode state (state, tokens, prompt, prompt_len, cap) as llama_advance.
     float* arg_v = nullptr;
     int32_t* arg_i = nullptr;
-    uint32_t* ticket = nullptr;
     int32_t* state = nullptr;
     int32_t* tokens = nullptr;
     const int32_t* prompt = nullptr;
     int prompt_len = 0;
 };
 
-// Workgroups of an argmax-epilogue launch, each writing one partial: the
-// ticket is one address every workgroup adds to, and device-scope adds to
-// one address serialise, so the launch uses fewer, longer-lived workgroups
-// (the GEMV is persistent over row tiles).
-constexpr int GEMV_ARG_MAX_PARTS = 256;
+// Workgroups of an argmax-epilogue launch at most, each writing one partial
+// (the GEMV is persistent over row tiles beyond this).
+constexpr int GEMV_ARG_MAX_PARTS = 2048;
 
 // One f32 row through a q4_0 linear (qlinear.hip), y[n] = Q8_0(pro(x)) . W^T
 // (+ resid[n]): pro is a LinearPrologue (PRO_RMSNORM scales by po.w with
@@ -313,9 +309,9 @@ constexpr int64_t LINEAR_DECODE_MAX_K = 24576;  // 768 blocks: one per (row, blo
 tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, const GemvPro& po, const uint8_t* qs,
                         const uint16_t* d, int64_t n, const float* resid, float* y);
 // The decode step's last linear: y = Q4(rmsnorm(x, po.w)) as linear_decode
-// with PRO_RMSNORM, then the argmax of y and the state's advance (po's
-// argmax fields) in the same launch. TN_ENOTIMPL when the activation row
-// does not fit the GEMV.
+// with PRO_RMSNORM, with per-workgroup argmax partials of y, then one
+// workgroup reducing them and advancing the state (po's argmax fields).
+// TN_ENOTIMPL when the activation row does not fit the GEMV.
 tn_status linear_decode_argmax(hipStream_t st, const float* x, int64_t k, const GemvPro& po, const uint8_t* qs,
                                const uint16_t* d, int64_t n, float* y);
 
