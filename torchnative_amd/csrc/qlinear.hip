@@ -310,28 +310,48 @@ __device__ inline void gemv_argmax_epilogue(float v, int i, const GemvPro& po) {
     }
 }
 
-// One workgroup: the best of `parts` (value, index) partials of an n-wide row
-// (argmax's order, arg_before), into state[3], then the decode step's
-// advance as k_argmax<true, ...> does.
+// One workgroup: the best of `parts` (<= GEMV_ARG_MAX_PARTS) (value, index)
+// partials of an n-wide row (argmax's order, arg_before), into state[3], then
+// the decode step's advance as k_argmax<true, ...> does. Every load is issued
+// at the start: the partials all at once, and the position with the prompt
+// token it may pick, so that nothing waits on memory after the reduction.
 __global__ __launch_bounds__(GEMV_THREADS) void k_argmax_parts(const float* __restrict__ arg_v,
                                                              const int32_t* __restrict__ arg_i, int parts, int n,
                                                              int32_t* state, int32_t* tokens,
                                                              const int32_t* __restrict__ prompt, int prompt_len,
                                                              int cap) {
-    float v = -INFINITY;
-    int i = INT32_MAX;
-    for (int g = threadIdx.x; g < parts; g += GEMV_THREADS) {
-        const float gv = arg_v[g];
-        const int gi = arg_i[g];
-        if (arg_before(gv, gi, v, i)) {
-            v = gv;
-            i = gi;
+    constexpr int PER = GEMV_ARG_MAX_PARTS / GEMV_THREADS;
+    static_assert(PER * GEMV_THREADS == GEMV_ARG_MAX_PARTS, "partials per thread");
+    int pos = 0, ptok = 0;
+    if (threadIdx.x == 0) {
+        pos = state[0] + 1;
+        if (pos < prompt_len) ptok = prompt[pos];
+    }
+    float pv[PER];
+    int pi[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int g = threadIdx.x + j * GEMV_THREADS;
+        pv[j] = -INFINITY;
+        pi[j] = INT32_MAX;
+        if (g < parts) {
+            pv[j] = arg_v[g];
+            pi[j] = arg_i[g];
         }
     }
+    float v = pv[0];
+    int i = pi[0];
+#pragma unroll
+    for (int j = 1; j < PER; j++)
+        if (arg_before(pv[j], pi[j], v, i)) {
+            v = pv[j];
+            i = pi[j];
+        }
     block_arg_best(v, i);
     if (threadIdx.x == 0) {
-        state[3] = i < n ? i : 0;
-        llama_advance(state, tokens, prompt, prompt_len, cap);
+        const int am = i < n ? i : 0;
+        state[3] = am;
+        llama_commit(state, tokens, pos, pos < prompt_len ? ptok : am, cap);
     }
 }
 

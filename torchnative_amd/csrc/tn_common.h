@@ -252,14 +252,16 @@ __device__ inline bool arg_before(float v, int i, float w, int j) {
 // end of a decode step (state = [position, KV length, token, argmax]):
 // advance the position and pick the next input token, the prompt's while
 // the position is inside it, else the argmax
-__device__ inline void llama_advance(int32_t* state, int32_t* tokens, const int32_t* prompt, int prompt_len,
-                                     int cap) {
-    const int pos = state[0] + 1;
-    const int next = pos < prompt_len ? prompt[pos] : state[3];
+__device__ inline void llama_commit(int32_t* state, int32_t* tokens, int pos, int next, int cap) {
     if (pos < cap) tokens[pos] = next;
     state[0] = pos;
     state[1] = pos + 1;
     state[2] = next;
+}
+__device__ inline void llama_advance(int32_t* state, int32_t* tokens, const int32_t* prompt, int prompt_len,
+                                     int cap) {
+    const int pos = state[0] + 1;
+    llama_commit(state, tokens, pos, pos < prompt_len ? prompt[pos] : state[3], cap);
 }
 
 // Input transforms a decode linear can apply while it quantises its input.
