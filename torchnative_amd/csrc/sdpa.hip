@@ -32,6 +32,7 @@
 
 #include "tn_common.h"
 #include "attn_common.h"
+#include "skgeo.h"
 
 namespace tn {
 namespace {
@@ -690,42 +691,6 @@ constexpr int PF_BQ = 16 * PF_WAVES, PF_BK = 64;
 // run. Row strides are padded to 4 mod 32 dwords, so each 8-lane phase of a
 // 16-byte read covers all 32 banks.
 // ---------------------------------------------------------------------------
-
-// Stream-K partition of the f32 prefill. A unit is one key tile of one
-// PF_BQ-query block; units run over (batch * head, query block, key tile) in
-// that order, a query block qt having nt(qt) key tiles. The persistent grid's
-// G workgroups take equal unit ranges [g T / G, (g+1) T / G), so every
-// workgroup does the same MFMA work whatever the causal shape. A workgroup
-// writes a query block it covers whole straight to the output; a block cut
-// by a range boundary leaves an unnormalised (O, m, l) partial per
-// workgroup: in slot 2g if it is workgroup g's first block, else 2g + 1 (a
-// workgroup cuts at most its first and its last block), and the workgroup
-// that finishes the block last merges them in workgroup order.
-struct SkGeo {
-    int nqb, NS, c, causal;  // query blocks, key tiles of S, key tiles per query block (PF_BQ / BK)
-    int64_t Tbh, T, G;       // units per (batch, head), all units, workgroups (G <= T)
-    __host__ __device__ int nt(int qt) const { return causal ? (c * (qt + 1) < NS ? c * (qt + 1) : NS) : NS; }
-    // units of query blocks 0 .. qt-1 of one (batch, head)
-    __host__ __device__ int64_t P(int qt) const {
-        if (!causal) return (int64_t)qt * NS;
-        const int64_t m = qt < NS / c ? qt : NS / c;  // blocks below qt whose tiles stop before S
-        return (int64_t)c * m * (m + 1) / 2 + ((int64_t)qt - m) * NS;
-    }
-    __host__ __device__ int64_t lo(int64_t g) const { return g * T / G; }
-    __host__ __device__ int64_t wg_of(int64_t u) const { return ((u + 1) * G + T - 1) / T - 1; }
-    // the query block (bh, qt) that holds unit u, and u's tile in it
-    __host__ __device__ void locate(int64_t u, int64_t& bh, int& qt, int& t) const {
-        bh = u / Tbh;
-        const int64_t r = u - bh * Tbh;
-        int a = 0, b = nqb;  // the largest qt with P(qt) <= r (every block has a tile)
-        while (b - a > 1) {
-            const int mid = (a + b) >> 1;
-            if (P(mid) <= r) a = mid; else b = mid;
-        }
-        qt = a;
-        t = (int)(r - P(a));
-    }
-};
 
 // MASK: 1 adds an f32 mask, 3 a bool one (MaskRef), to the scaled scores
 // (aten.rs:10383-10389)
