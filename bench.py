@@ -494,7 +494,7 @@ def calibrate_copy(tn, L, steps):
 
 
 def profiled_traffic(name):
-    """HBM bytes per launch of the headline kernel, as committed in
+    """HBM bytes per launch of a config's dominant kernel, as committed in
     profiles/<name> (line `traffic_bytes_per_launch: N`), or None."""
     path = os.path.join(ROOT, "profiles", name)
     try:
@@ -565,6 +565,12 @@ def main():
     print("bench: c2 SDPA prefill bf16 (headline)", file=sys.stderr, flush=True)
     head = bench_sdpa(tn, L, "bfloat16", args.steps, args.warmup)
     head["roofline"]["traffic"] = profiled_traffic("flash_bf16_c2_traffic.md")
+    # the parts' dominant kernels, measured the same way (rocprofv3 FETCH_SIZE
+    # and WRITE_SIZE passes scaled by the copy calibration)
+    for part, prof in (("c1_q4_gemv", "q4_gemv_c1.md"), ("c2_sdpa_prefill_fp32", "flash_f32_c2.md"),
+                       ("c3_q4_gemm", "q4_gemm_c3.md"), ("c4_decode_attention", "decode_attention_c4.md")):
+        if part in parts:
+            parts[part]["roofline"]["traffic"] = profiled_traffic(prof)
 
     cpu = None
     if not args.no_cpu_baseline:
