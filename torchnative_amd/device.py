@@ -12,8 +12,8 @@ tests can branch on the code rather than parse prose:
   wrong_arch  the current GPU is not a gfx950 (the library is built for it only).
 
 The reference's device namespace (torchnative/python/torchnative/device)
-would take this as one more member: INTEGRATION.md shows the small class it
-would register, which forwards its availability question to `probe()`.
+would take this as one more member: a small class registered there that
+forwards its availability question to `probe()`.
 """
 
 from __future__ import annotations
