@@ -99,8 +99,10 @@ def test_capture_refuses_a_call_that_would_allocate_then_replays_what_it_recorde
         g = ctypes.c_void_p()
         end = f.tn_stream_end_capture(st, ctypes.byref(g))
         assert status == L.TN_EINVAL and "graph capture cannot allocate" in msg, msg
-        if end == L.TN_OK and g.value:
-            L.check(f.tn_graph_destroy(g.value))
+        # ending that capture fails too, naming the refusal, and hands back no graph
+        end_msg = L.last_error()
+        assert end == L.TN_EINVAL and not g.value, (end, g.value)
+        assert "refused during the capture" in end_msg and "graph capture cannot allocate" in end_msg, end_msg
         # one eager call sizes the buffers; then the same call records
         L.check(call())
         L.check(f.tn_stream_synchronize(st))

@@ -843,6 +843,12 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
     const uint32_t vd = (tid >= GM_BM && tid < GM_BM + BN) ? (uint32_t)((tid - GM_BM) * nb * 2) : OOB;
     auto gload = [&](int b, uint4& a0, uint4& a1, uint2& w, float& dx, float& corr, uint32_t& dws)
                      __attribute__((always_inline)) {
+        // Blocks past the last (the prefetches of the final steps, and the
+        // first four when nb < 4) are clamped to the last block. The block
+        // offset travels in the scalar offset, which the descriptor's range
+        // check does not cover, so it must itself stay inside the operands.
+        // The clamped data lands in an LDS buffer no later step reads.
+        b = min(b, nb - 1);
 #if __HIP_DEVICE_COMPILE__
         typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
         typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -944,8 +950,8 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
     uint32_t dw_0, dw_1, dw_2, dw_3;
     static_assert(GM_RS == 4, "the unrolled K loop below names four register sets");
 #define TN_GM_SET(S) a0_##S, a1_##S, w_##S, dx_##S, cr_##S, dw_##S
-    // (the last steps load and stage blocks past the end: a clamped block,
-    // into the LDS buffer no later step reads)
+    // (the last steps load and stage a block past the end, clamped by gload
+    // to the last one, into the LDS buffer no later step reads)
 #define TN_GM_STEP(S, NEXT, B)                          \
     {                                                   \
         gload((B) + GM_RS, TN_GM_SET(S));               \

@@ -38,11 +38,12 @@ Counters& counters() {
 }
 
 namespace {
-// A stream's scratch. Buffers are never freed while the stream lives: a
-// graph captured from it keeps the addresses it saw, so a buffer outgrown by
-// a later, larger call is retired (kept) rather than freed, and all of them
-// go with tn_stream_destroy. Growth at least doubles, so the retired ones
-// total less than the live one.
+// A stream's scratch. A graph captured from a stream keeps the addresses it
+// saw, so once a stream has been captured a buffer outgrown by a later,
+// larger call is retired (kept) rather than freed, and all of them go with
+// tn_stream_destroy; growth at least doubles, so the retired ones total less
+// than the live one. A stream never captured (the default stream cannot be)
+// frees the outgrown buffer at once, after a synchronisation.
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
@@ -50,19 +51,41 @@ struct Workspace {
     size_t ntickets = 0;
     std::vector<void*> retired;
     size_t retired_bytes = 0;
+    bool captured = false;  // a capture has begun on this stream
+    std::string refused;    // a call refused while the stream was capturing
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
 // Growth allocates, which a stream under graph capture must not do (and a
-// graph could not replay): refused by name.
-tn_status refuse_if_capturing(hipStream_t stream, const char* what) {
+// graph could not replay): refused by name. The refusal is also recorded, so
+// that ending the capture fails instead of returning a graph that lacks the
+// refused launch.
+tn_status refuse_if_capturing(Workspace& w, hipStream_t stream, const char* what) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     TN_HIP(hipStreamIsCapturing(stream, &cs));
-    if (cs != hipStreamCaptureStatusNone)
-        return fail(TN_EINVAL, std::string("tnhip: this call needs more ") + what +
-                                   " than the stream holds, and a stream under graph capture cannot allocate; make "
-                                   "the same call (or a larger one) once before capturing");
+    if (cs != hipStreamCaptureStatusNone) {
+        const std::string msg = std::string("tnhip: this call needs more ") + what +
+                                " than the stream holds, and a stream under graph capture cannot allocate; make "
+                                "the same call (or a larger one) once before capturing";
+        if (w.refused.empty()) w.refused = msg;
+        return fail(TN_EINVAL, msg);
+    }
+    return TN_OK;
+}
+
+// An outgrown buffer: kept for the stream's graphs, or freed at once when the
+// stream has never been captured.
+tn_status retire(Workspace& w, hipStream_t stream, void* old, size_t bytes) {
+    if (!old) return TN_OK;
+    if (w.captured) {
+        w.retired.push_back(old);
+        w.retired_bytes += bytes;
+        return TN_OK;
+    }
+    TN_HIP(hipStreamSynchronize(stream));  // kernels already queued may still read it
+    TN_HIP(hipFree(old));
+    counters().workspace_bytes.fetch_sub(bytes);
     return TN_OK;
 }
 }  // namespace
@@ -73,15 +96,12 @@ tn_status workspace(hipStream_t stream, size_t bytes, void** out) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace& w = g_ws[{dev, stream}];
     if (w.bytes < bytes) {
-        TN_TRY(refuse_if_capturing(stream, "workspace"));
+        TN_TRY(refuse_if_capturing(w, stream, "workspace"));
         size_t want = std::max(bytes, std::max((size_t)1 << 20, 2 * w.bytes));
         want = (want + 4095) & ~(size_t)4095;
         void* p = nullptr;
         TN_HIP(hipMalloc(&p, want));
-        if (w.ptr) {
-            w.retired.push_back(w.ptr);
-            w.retired_bytes += w.bytes;
-        }
+        TN_TRY(retire(w, stream, w.ptr, w.bytes));
         w.ptr = p;
         w.bytes = want;
         counters().workspace_bytes.fetch_add(want);
@@ -96,17 +116,14 @@ tn_status tickets(hipStream_t stream, size_t n, uint32_t** out) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace& w = g_ws[{dev, stream}];
     if (w.ntickets < n) {
-        TN_TRY(refuse_if_capturing(stream, "ticket counters"));
+        TN_TRY(refuse_if_capturing(w, stream, "ticket counters"));
         size_t want = std::max(n, std::max((size_t)4096, 2 * w.ntickets));
         want = (want + 4095) & ~(size_t)4095;
         uint32_t* p = nullptr;
         TN_HIP(hipMalloc(reinterpret_cast<void**>(&p), want * 4));
         // zeroed once, ahead of the first kernel on this stream that takes a ticket
         TN_HIP(hipMemsetAsync(p, 0, want * 4, stream));
-        if (w.tickets) {
-            w.retired.push_back(w.tickets);
-            w.retired_bytes += w.ntickets * 4;
-        }
+        TN_TRY(retire(w, stream, w.tickets, w.ntickets * 4));
         w.tickets = p;
         w.ntickets = want;
         counters().workspace_bytes.fetch_add(want * 4);
@@ -316,6 +333,14 @@ tn_status tn_stream_destroy(void* stream) {
 
 tn_status tn_stream_begin_capture(void* stream) {
     if (!stream) return fail(TN_EVALUE, "tn_stream_begin_capture: the default stream cannot be captured");
+    {
+        int dev = 0;
+        TN_HIP(hipGetDevice(&dev));
+        std::lock_guard<std::mutex> lock(g_ws_mu);
+        Workspace& w = g_ws[{dev, (hipStream_t)stream}];
+        w.captured = true;  // from now on outgrown buffers are kept for the graph
+        w.refused.clear();
+    }
     TN_HIP(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
     return TN_OK;
 }
@@ -325,9 +350,23 @@ tn_status tn_stream_end_capture(void* stream, void** graph) {
     *graph = nullptr;
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture((hipStream_t)stream, &g);
+    std::string refused;
+    {
+        int dev = 0;
+        TN_HIP(hipGetDevice(&dev));
+        std::lock_guard<std::mutex> lock(g_ws_mu);
+        auto it = g_ws.find({dev, (hipStream_t)stream});
+        if (it != g_ws.end()) refused.swap(it->second.refused);
+    }
     if (e != hipSuccess) {
         if (g) (void)hipGraphDestroy(g);
         return hip_fail(e, "hipStreamEndCapture");
+    }
+    // a call refused during the capture is missing from the graph: no graph
+    if (!refused.empty()) {
+        if (g) (void)hipGraphDestroy(g);
+        return fail(TN_EINVAL, "tn_stream_end_capture: a call was refused during the capture, so the graph would "
+                               "lack its launch; no graph was made. The refusal: " + refused);
     }
     hipGraphExec_t exec = nullptr;
     const hipError_t ei = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
