@@ -48,6 +48,15 @@ struct El<false> {
     }
     static __device__ inline uint32_t pack_p(float a, float b) { return pack2_bf16_hw(a, b); }
     static __device__ inline uint32_t pack_out(float a, float b) { return pack2_bf16(a, b); }
+    // pack_out's bits through v_cvt_pk_bf16_f32 (round to nearest even, as
+    // bf16_from_f32 for every number), with a NaN given bf16_from_f32's
+    // quieted payload
+    static __device__ inline uint32_t pack_out_hw(float a, float b) {
+        uint32_t r = pack2_bf16_hw(a, b);
+        if (a != a) r = (r & 0xffff0000u) | ((__float_as_uint(a) >> 16) | 0x40u);
+        if (b != b) r = (r & 0xffffu) | (((__float_as_uint(b) >> 16) | 0x40u) << 16);
+        return r;
+    }
     static __device__ inline float widen(uint16_t h) { return bf16_to_f32(h); }
     static __device__ inline f32x4 mfma16(v8 a, v8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -69,6 +78,15 @@ struct El<true> {
     }
     static __device__ inline uint32_t pack_out(float a, float b) {
         return (uint32_t)f16_from_f32(a) | ((uint32_t)f16_from_f32(b) << 16);
+    }
+    // pack_out's bits through v_cvt_f16_f32 (equal to f16_from_f32 for every
+    // number, subnormals and overflow included), with a NaN given
+    // f16_from_f32's quieted payload
+    static __device__ inline uint32_t pack_out_hw(float a, float b) {
+        uint32_t r = pack_p(a, b);
+        if (a != a) r = (r & 0xffff0000u) | f16_from_f32(a);
+        if (b != b) r = (r & 0xffffu) | ((uint32_t)f16_from_f32(b) << 16);
+        return r;
     }
     static __device__ inline float widen(uint16_t h) { return f16_to_f32(h); }
     static __device__ inline f32x4 mfma16(v8 a, v8 b, f32x4 c) {
