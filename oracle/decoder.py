@@ -101,8 +101,10 @@ class Decoder:
             })
         self.freqs = inv_freq(cfg)
 
-    def step(self, token: int, pos: int) -> np.ndarray:
-        """Process `token` at `pos`; returns the logits [vocab] in self.dtype."""
+    def step(self, token: int, pos: int, trace=None) -> np.ndarray:
+        """Process `token` at `pos`; returns the logits [vocab] in self.dtype.
+        `trace`, a list, receives per layer the attention output [Hq*D] and
+        the value rows the attention read [Hkv, pos+1, D]."""
         c, dt = self.cfg, self.dtype
         Hq, Hkv, D, I = c.n_heads, c.n_kv_heads, c.head_dim, c.inter
         h = self.embed[token].astype(dt)
@@ -115,6 +117,8 @@ class Decoder:
             L["k"][:, pos] = k
             L["v"][:, pos] = v
             a, _ = O.sdpa(q[None, :, None, :], L["k"][None, :, :pos + 1], L["v"][None, :, :pos + 1], dtype=dt)
+            if trace is not None:
+                trace.append({"a": a.reshape(-1).copy(), "v": L["v"][:, :pos + 1].copy()})
             h = (h + linear(a.reshape(-1), L["o"], c.hidden, dt, self.threads).astype(dt)).astype(dt)
             x = rmsnorm(h, L["ln2"], c.eps, dt)
             gu = linear(x, L["gate_up"], 2 * I, dt, self.threads).astype(dt)
@@ -140,12 +144,14 @@ def linear_rows(x, blob, n, dtype=np.float32, threads=8):
     return xd @ wd.T
 
 
-def teacher_forced_logits(dec: "Decoder", tokens, want, threads=8) -> dict:
+def teacher_forced_logits(dec: "Decoder", tokens, want, threads=8, trace=None) -> dict:
     """Logits of `dec`'s model at the positions in `want` when `tokens` are
     fed one per position from 0: the same values as step() called on each
     token in turn (every op is row-wise except the attention, which sees keys
     0..t for row t, i.e. upper-left causal over the sequence), computed a
-    whole sequence at a time. Returns {position: logits in dec.dtype}."""
+    whole sequence at a time. Returns {position: logits in dec.dtype}.
+    `trace`, a list, receives per layer the attention output [T, Hq*D] and
+    the value rows [T, Hkv, D]."""
     c, dt = dec.cfg, dec.dtype
     Hq, Hkv, D, I = c.n_heads, c.n_kv_heads, c.head_dim, c.inter
     toks = np.asarray(tokens, np.int64)
@@ -170,6 +176,8 @@ def teacher_forced_logits(dec: "Decoder", tokens, want, threads=8) -> dict:
         a, _ = O.sdpa(q.transpose(1, 0, 2)[None], k.transpose(1, 0, 2)[None], v.transpose(1, 0, 2)[None],
                       is_causal=True, threads=threads, dtype=dt)
         a = a[0].transpose(1, 0, 2).reshape(T, Hq * D)
+        if trace is not None:
+            trace.append({"a": a.copy(), "v": v.copy()})
         h = (h + linear_rows(a, L["o"], c.hidden, dt, threads).astype(dt)).astype(dt)
         x = rmsnorm(h, L["ln2"], c.eps, dt)
         gu = linear_rows(x, L["gate_up"], 2 * I, dt, threads).astype(dt)

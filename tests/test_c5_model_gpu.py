@@ -2,11 +2,12 @@
 
 30 layers, hidden 576, 9 query / 3 key-value heads of 64, SiLU MLP 1536,
 RMSNorm 1e-5, RoPE theta 1e5, vocab 49152, every linear (lm_head included)
-q4_0 -- the model the bench decodes. It is fed a 263-token sequence one token
+q4_0 -- the model the bench decodes. It is fed a 384-token sequence one token
 per step (teacher-forced: every position gets the same token on both sides)
-and its logits are compared at positions 0-7 and 255-262 with the oracle's
-float32 run (oracle/decoder.py, the reference's x86 q4 linear bit for bit and
-its default SDPA path), computed a whole sequence at a time.
+and its logits are compared at positions 0-7, 255-262, 300-303 and 380-383
+(the bench's timed steps are positions 256-383 of a 384-entry cache) with the
+oracle's float32 run (oracle/decoder.py, the reference's x86 q4 linear bit for
+bit and its default SDPA path), computed a whole sequence at a time.
 
 Bound: oracle.sdpa_tolerance per position, i.e. 4x the oracle's own
 float32-vs-float64 distance on the same tokens, floored at 1.186e-6 of the
@@ -30,8 +31,8 @@ from oracle import decoder as OD
 pytestmark = pytest.mark.gpu
 
 SEED = 20
-N_TOK = 263
-WANT = list(range(8)) + list(range(255, 263))
+N_TOK = 384
+WANT = list(range(8)) + list(range(255, 263)) + list(range(300, 304)) + list(range(380, 384))
 
 
 @pytest.fixture(scope="module")
@@ -115,3 +116,57 @@ def test_fused_split_attention_across_split_boundaries(tn, cap):
         if pos + 1 >= len(prompt):
             seq.append(nxt)
     assert model.generated(len(prompt), n_new) == seq[len(prompt):]
+
+
+# The decoder's composition on the device, with weights that make the answer
+# known (the oracle's composition is pinned the same way on the CPU,
+# tests/test_oracle_decoder.py): every o and down projection zero, so the
+# logits are lm_head(rmsnorm(embed[t])) at every position; the q and k rows
+# zero, so every head attends uniformly to positions 0..t of its key/value
+# head h // 3. Both on the cap-200 fused split attention and the cap-600
+# split-KV path, over 150 teacher-forced tokens.
+GQA3 = OD.LlamaConfig(n_layers=3, hidden=384, n_heads=6, n_kv_heads=2, head_dim=64, inter=256, vocab=512)
+
+
+def _zeroed(cfg, seed, *, qk=False, o_down=False):
+    D = cfg.head_dim
+    layers = []
+    for i in range(cfg.n_layers):
+        w = dict(OD.layer_weights(cfg, i, seed))
+        if qk:
+            w["qkv"] = w["qkv"].copy()
+            w["qkv"][:(cfg.n_heads + cfg.n_kv_heads) * D] = 0.0
+        if o_down:
+            w["o"] = np.zeros_like(w["o"])
+            w["down"] = np.zeros_like(w["down"])
+        layers.append(w)
+    return layers, OD.model_weights(cfg, seed)
+
+
+@pytest.mark.parametrize("cap", [200, 600])
+@pytest.mark.parametrize("which", ["o_down", "qk"])
+def test_decoder_composition_with_zeroed_projections(tn, cap, which):
+    from torchnative_amd.decoder import Q4Llama
+
+    layers, top = _zeroed(GQA3, 31, qk=which == "qk", o_down=which == "o_down")
+    toks = np.random.default_rng(cap).integers(0, GQA3.vocab, 150).astype(np.int32)
+    want = list(range(0, 150, 7)) + [149]
+    r32 = OD.teacher_forced_logits(OD.Decoder(GQA3, 31, 150, np.float32, layers, top), toks, want)
+    r64 = OD.teacher_forced_logits(OD.Decoder(GQA3, 31, 150, np.float64, layers, top), toks, want)
+    model = Q4Llama(GQA3, seed=31, cap=cap, weights=(lambda i: layers[i], top))
+    model.start(toks)
+    lm = O.q4_0_quantize(top["lm_head"])
+    for pos in range(len(toks)):
+        model.step()
+        if pos not in r32:
+            continue
+        got = model.logits.numpy().astype(np.float64)
+        l32, l64 = r32[pos].astype(np.float64), r64[pos]
+        tol = O.sdpa_tolerance(l32, l64, "float32")
+        w = float(np.max(np.abs(got - l32) / tol))
+        assert w <= 1.0, f"{which} cap {cap} position {pos}: {w:.3g}x the bound"
+        if which == "o_down":
+            # the closed form itself: the oracle's logits are exactly it (CPU test), the device's within the bound
+            x = OD.rmsnorm(top["embed"][int(toks[pos])], top["norm"], GQA3.eps)
+            closed = O.q4_0_linear(x.reshape(1, -1), lm, GQA3.vocab)[0].astype(np.float64)
+            assert np.array_equal(closed, l32)

@@ -138,3 +138,97 @@ def test_the_float64_linear_rows_is_the_exact_quantised_product():
     # and the float32 rows are the C oracle's one-row calls, bit for bit
     f32 = OD.linear_rows(x, blob, 40, np.float32, threads=3)
     assert all(np.array_equal(f32[i], O.q4_0_linear(x[i:i + 1], blob, 40)[0]) for i in range(5))
+
+
+# ---- the composition, pinned by models whose answer the mathematics fixes ----
+#
+# The checks above pin each op; these pin how the decoder puts them together
+# (pre-norm, the residual stream, the final norm and lm_head, the causal
+# extent of the attention and its GQA head map) with weights that make the
+# answer known in closed form. A zero q4_0 weight quantises to zero scales, so
+# its linear is exactly 0 for any input.
+GQA = OD.LlamaConfig(n_layers=3, hidden=384, n_heads=6, n_kv_heads=2, head_dim=64, inter=256, vocab=512)
+
+
+def _zeroed(cfg, seed, *, qk=False, o_down=False):
+    """cfg's seeded weights with the q and k rows of every qkv projection, or
+    every o and down projection, set to zero."""
+    D = cfg.head_dim
+    layers = []
+    for i in range(cfg.n_layers):
+        w = dict(OD.layer_weights(cfg, i, seed))
+        if qk:
+            w["qkv"] = w["qkv"].copy()
+            w["qkv"][:(cfg.n_heads + cfg.n_kv_heads) * D] = 0.0
+        if o_down:
+            w["o"] = np.zeros_like(w["o"])
+            w["down"] = np.zeros_like(w["down"])
+        layers.append(w)
+    return layers, OD.model_weights(cfg, seed)
+
+
+def test_zero_weight_linear_is_exactly_zero():
+    x = np.random.default_rng(0).standard_normal((3, 96)).astype(np.float32)
+    blob = O.q4_0_quantize(np.zeros((40, 96), np.float32))
+    assert np.array_equal(O.q4_0_linear(x, blob, 40), np.zeros((3, 40), np.float32))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_without_o_and_down_the_logits_are_lm_head_of_the_normed_embedding(dtype):
+    """With every o and down projection zero, each layer adds exact zeros to
+    the residual stream, so at every position h is the token's embedding row
+    and the logits are lm_head(rmsnorm(embed[t], norm)): this pins that the
+    layers add to the residual stream (not to a normed copy), that nothing
+    else is added, and the final norm and lm_head."""
+    layers, top = _zeroed(GQA, 7, o_down=True)
+    toks = [5, 400, 5, 17, 256, 0, 511, 99]
+    dec = OD.Decoder(GQA, 7, 16, dtype, layers, top)
+    batched = OD.teacher_forced_logits(OD.Decoder(GQA, 7, 16, dtype, layers, top), toks, range(len(toks)))
+    for p, t in enumerate(toks):
+        x = OD.rmsnorm(top["embed"][t].astype(dtype), top["norm"], GQA.eps, dtype)
+        want = OD.linear(x, dec.lm_blob, GQA.vocab, dtype).astype(dtype)
+        assert np.array_equal(dec.step(t, p), want), p
+        assert np.array_equal(batched[p], want), p
+
+
+@pytest.mark.parametrize("batched", [False, True])
+def test_with_q_and_k_zero_each_head_attends_uniformly_to_keys_0_to_t(batched):
+    """With the q and k rows zero, every score is 0, so the attention of the
+    row at position t is the plain mean of the value rows 0..t of its key/value
+    head h // (Hq / Hkv): this pins the causal extent (position t itself
+    included, nothing after it) and the GQA head map, in every layer, for the
+    step and the whole-sequence run. float64, so the mean is compared at
+    1e-13 of the values' scale."""
+    layers, top = _zeroed(GQA, 8, qk=True)
+    toks = [3, 3, 450, 12, 77, 0, 300, 511, 2, 2, 64]
+    T, Hq, Hkv, D = len(toks), GQA.n_heads, GQA.n_kv_heads, GQA.head_dim
+    rep = Hq // Hkv
+    if batched:
+        trace = []
+        OD.teacher_forced_logits(OD.Decoder(GQA, 8, 16, np.float64, layers, top), toks, [T - 1], trace=trace)
+        per_layer = [(tr["a"], tr["v"]) for tr in trace]  # a [T, Hq*D], v [T, Hkv, D]
+    else:
+        dec = OD.Decoder(GQA, 8, 16, np.float64, layers, top)
+        steps = []
+        for p, t in enumerate(toks):
+            tr = []
+            dec.step(t, p, trace=tr)
+            steps.append(tr)
+        per_layer = []
+        for li in range(GQA.n_layers):
+            a = np.stack([steps[p][li]["a"] for p in range(T)])
+            v = steps[-1][li]["v"].transpose(1, 0, 2)  # the full cache after the last step [T, Hkv, D]
+            # the cache rows a step read are the rows the last step sees (no row is rewritten)
+            for p in range(T):
+                assert np.array_equal(steps[p][li]["v"], steps[-1][li]["v"][:, :p + 1])
+            per_layer.append((a, v))
+    assert len(per_layer) == GQA.n_layers
+    for a, v in per_layer:
+        a = a.reshape(T, Hq, D)
+        scale = float(np.max(np.abs(v)))
+        for t in range(T):
+            for h in range(Hq):
+                want = v[:t + 1, h // rep].mean(axis=0)
+                assert np.max(np.abs(a[t, h] - want)) <= 1e-13 * scale, (t, h)
+        # and the map is not the identity or a modulo: heads of different kv heads differ
+        assert not np.allclose(a[:, 0], a[:, rep])
