@@ -265,7 +265,11 @@ def bench_e2e(tn, L, prompt_len=256, n_new=128, seed=5, graph=True):
     bench does (tests/bench/bench_llama_cpp.py:540-569), the prompt yields
     the first token and the next n_new - 1 steps are timed: tokens/s =
     (n_new - 1) / seconds. The timed steps run as one captured HIP graph;
-    the same steps issued one call at a time are reported beside it."""
+    the same steps issued one call at a time are reported beside it. The
+    prompt runs as one batched prefill (tn_llama_prefill), timed on its own
+    as the reference's bench times its prefill phase
+    (tests/bench/bench_llama_cpp.py:484-523): prefill tokens/s = prompt
+    tokens / seconds, at the 256-token prompt and at 128 tokens."""
     from torchnative_amd.decoder import LlamaConfig, Q4Llama
 
     cfg = LlamaConfig()
@@ -278,12 +282,34 @@ def bench_e2e(tn, L, prompt_len=256, n_new=128, seed=5, graph=True):
 
     def run_prompt():
         model.start(prompt)
-        for _ in range(prompt_len):
-            model.step(st)
+        model.prefill(prompt_len, st)
         L.check(lib.tn_stream_synchronize(st))
+
+    def time_prefill(n, reps=7):
+        model.start(prompt[:n])
+        model.prefill(n, st)  # warm: the GEMM workspace, first-touch
+        L.check(lib.tn_stream_synchronize(st))
+        ts = []
+        for _ in range(reps):
+            model.start(prompt[:n])
+            L.check(lib.tn_stream_synchronize(st))
+            t0 = time.perf_counter()
+            model.prefill(n, st)
+            L.check(lib.tn_stream_synchronize(st))
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
 
     graph_s = tokens = warm_tokens = None
     try:
+        prefill_s = {n: time_prefill(n) for n in (128, prompt_len)}
+        # the stepwise prompt's first tokens, beside the batched prompt's
+        model.start(prompt)
+        for _ in range(prompt_len):
+            model.step(st)
+        for _ in range(15):
+            model.step(st)
+        L.check(lib.tn_stream_synchronize(st))
+        stepwise_tokens = model.generated(prompt_len, 16)
         if graph:
             run_prompt()
             g = model.capture(n_new - 1, st)
@@ -313,6 +339,12 @@ def bench_e2e(tn, L, prompt_len=256, n_new=128, seed=5, graph=True):
     tps = (n_new - 1) / timed_s
     return {"tokens_per_s": tps, "ms_per_token": timed_s * 1e3 / (n_new - 1), "graph": graph,
             "eager_tokens_per_s": (n_new - 1) / eager_s, "prompt_tokens": prompt_len, "new_tokens": n_new,
+            "prefill": {"tokens_per_s": prompt_len / prefill_s[prompt_len], "ms": prefill_s[prompt_len] * 1e3,
+                        "tokens_per_s_128": 128 / prefill_s[128], "ms_128": prefill_s[128] * 1e3,
+                        "method": "tn_llama_prefill, host wall clock around a synchronised call, median of 7",
+                        "reference_published": {"tokens_per_s": {"128": 220.6, "512": 210.3},
+                                                "hardware": "Apple M1 CPU, 4 threads, SmolLM2-135M q4_0"}},
+            "first_tokens_stepwise_prompt": stepwise_tokens,
             "q4_weight_bytes_per_token": weight_bytes,
             "weight_stream_gbs": weight_bytes * tps / 1e9,
             "same_tokens_graph_eager_warm": (tokens == eager_tokens == warm_tokens) if graph else None,

@@ -416,6 +416,21 @@ tn_status tn_llama_capture(void* stream, const tn_llama* model, int64_t steps, v
 tn_status tn_graph_launch(void* stream, void* graph);
 tn_status tn_graph_destroy(void* graph);
 
+/* The prompt in one batched pass (the reference's prefill: one
+ * LlamaForCausalLM.forward over the prompt, timed on its own in
+ * tests/bench/bench_llama_cpp.py:484-523): the model's first `tokens`
+ * prompt tokens run through every layer at once -- RMSNorm rows, the q4_0
+ * linears as GEMMs (M = tokens), RoPE, the K/V rows into the caches at
+ * positions 0 .. tokens-1, the causal f32 SDPA prefill, the SiLU-gated MLP
+ * and the residual adds -- then the last position's logits, their argmax
+ * and the state's advance exactly as tn_llama_step ends, so tn_llama_step
+ * continues at position `tokens`. 1 <= tokens <= prompt_len <= cap. `work`
+ * holds tn_llama_prefill_work_floats(model, tokens) floats; the model's
+ * own work buffer is used too. The q4 GEMM allocates its stream workspace
+ * on a first call (not capturable then). */
+int64_t tn_llama_prefill_work_floats(const tn_llama* model, int64_t tokens);
+tn_status tn_llama_prefill(void* stream, const tn_llama* model, int64_t tokens, float* work);
+
 #ifdef __cplusplus
 }
 #endif

@@ -170,3 +170,68 @@ def test_decoder_composition_with_zeroed_projections(tn, cap, which):
             x = OD.rmsnorm(top["embed"][int(toks[pos])], top["norm"], GQA3.eps)
             closed = O.q4_0_linear(x.reshape(1, -1), lm, GQA3.vocab)[0].astype(np.float64)
             assert np.array_equal(closed, l32)
+
+
+# The prompt in one batched pass (tn_llama_prefill: the q4_0 GEMM over the
+# prompt's rows, the causal f32 prefill attention), then decode steps from
+# there: the last prompt position's logits and the later steps' against the
+# same oracle run as the step-by-step test above, on both attention paths of
+# the steps that follow.
+@pytest.mark.parametrize("cap", [384, 600])
+def test_config5_batched_prefill_then_steps_against_the_oracle(tn, c5, cap):
+    from torchnative_amd.decoder import Q4Llama
+
+    cfg, layers, top, toks, r32, r64 = c5
+    model = Q4Llama(cfg, seed=SEED, cap=cap, weights=(lambda i: layers[i], top))
+    model.start(toks)  # teacher-forced: the sequence is the prompt; the first 256 run batched
+    T = 256
+    model.prefill(T)
+    assert model.position() == T  # the state advanced past the batched positions
+    assert np.array_equal(model.tokens.numpy()[:T + 1], toks[:T + 1])
+    worst = 0.0
+
+    def check(pos):
+        nonlocal worst
+        got = model.logits.numpy().astype(np.float64)
+        l32, l64 = r32[pos].astype(np.float64), r64[pos]
+        tol = O.sdpa_tolerance(l32, l64, "float32")
+        w = float(np.max(np.abs(got - l32) / tol))
+        worst = max(worst, w)
+        assert w <= 1.0, f"cap {cap} position {pos}: {w:.3g}x the bound"
+        top2 = np.sort(l32)[-2:]
+        if top2[1] - top2[0] > 2 * float(np.max(tol)):
+            assert int(model.state.numpy()[3]) == OD.argmax(l32), f"cap {cap} position {pos}: greedy token"
+
+    check(T - 1)  # the prefill's own logits
+    for pos in range(T, N_TOK):
+        model.step()
+        if pos in r32:
+            check(pos)
+    print(f"c5 prefill: cap {cap}: worst {worst:.3f} of the bound", flush=True)
+
+
+@pytest.mark.parametrize("n_prompt", [1, 5, 64, 150])
+def test_prefill_generates_the_oracles_greedy_tokens(tn, n_prompt):
+    """A small model: prefill a prompt of n tokens and generate 12 more with
+    the steps; every generated token is the oracle's greedy token wherever
+    the oracle's top two logits are further apart than twice the bound."""
+    from torchnative_amd.decoder import Q4Llama
+
+    rng = np.random.default_rng(n_prompt)
+    prompt = [int(t) for t in rng.integers(0, NREP3.vocab, n_prompt)]
+    n_new = 12
+    model = Q4Llama(NREP3, seed=13, cap=200)
+    got = model.generate(prompt, n_new, prefill=True)
+    r32 = OD.Decoder(NREP3, 13, 200, np.float32)
+    r64 = OD.Decoder(NREP3, 13, 200, np.float64)
+    seq = list(prompt)
+    for pos in range(n_prompt + n_new - 1):
+        l32 = r32.step(seq[pos], pos).astype(np.float64)
+        l64 = r64.step(seq[pos], pos)
+        if pos + 1 >= n_prompt:
+            i = pos + 1 - n_prompt
+            tol = O.sdpa_tolerance(l32, l64, "float32")
+            top2 = np.sort(l32)[-2:]
+            if top2[1] - top2[0] > 2 * float(np.max(tol)):
+                assert got[i] == OD.argmax(l32), f"prompt {n_prompt}: new token {i}"
+            seq.append(got[i])

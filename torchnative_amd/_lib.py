@@ -113,6 +113,8 @@ SIGNATURES = {
     "tn_llama_work_floats": (_I64, [ctypes.POINTER(Llama)]),
     "tn_llama_step": (_I, [_P, ctypes.POINTER(Llama)]),
     "tn_llama_capture": (_I, [_P, ctypes.POINTER(Llama), _I64, ctypes.POINTER(_P)]),
+    "tn_llama_prefill_work_floats": (_I64, [ctypes.POINTER(Llama), _I64]),
+    "tn_llama_prefill": (_I, [_P, ctypes.POINTER(Llama), _I64, _P]),
     "tn_graph_launch": (_I, [_P, _P]),
     "tn_graph_destroy": (_I, [_P]),
 }

@@ -441,6 +441,98 @@ __global__ void k_kv_append(const float* __restrict__ k, const float* __restrict
     vc[dst] = v[src];
 }
 
+// ---- the prompt in one batched pass (tn_llama_prefill) ----
+
+// Token t of the prompt: its embedding row into h[t], its input id into
+// tokens[t], and the cosine and sine of position pos0 + t's RoPE angles
+// (cosf/sinf of pos * inv_freq[j], k_rope's arithmetic) into rope[t].
+__global__ __launch_bounds__(256) void k_prefill_begin(const int32_t* __restrict__ prompt, int T, int pos0,
+                                                       const float* __restrict__ table, int64_t vocab, int dim,
+                                                       float* __restrict__ h, int32_t* __restrict__ tokens,
+                                                       const float* __restrict__ inv_freq, int half,
+                                                       float2* __restrict__ rope) {
+    const int t = blockIdx.x;
+    const int32_t id = prompt[t];
+    for (int c = threadIdx.x; c < dim; c += 256)
+        h[(int64_t)t * dim + c] = (id >= 0 && id < vocab) ? table[(int64_t)id * dim + c] : NAN;
+    if (threadIdx.x < half) {
+        const float f = (float)(pos0 + t) * inv_freq[threadIdx.x];
+        rope[(int64_t)t * half + threadIdx.x] = make_float2(cosf(f), sinf(f));
+    }
+    if (threadIdx.x == 0) tokens[pos0 + t] = id;
+}
+
+// The prompt's projected rows qkv [T][hq + 2 hkv][d] split for the batched
+// attention and the caches: q heads rotated into q [hq][T][d], k heads
+// rotated into kt [hkv][T][d] and the k cache at positions pos0 + t, v heads
+// copied into vt [hkv][T][d] and the v cache. d/2 threads per (token, head),
+// each a rotated pair (j, j + d/2): k_rope's arithmetic on the prefill's
+// cos/sin table, bit for bit.
+__global__ void k_prefill_qkv(const float* __restrict__ qkv, int T, int hq, int hkv, int d,
+                              const float2* __restrict__ rope, float* __restrict__ q, float* __restrict__ kt,
+                              float* __restrict__ vt, float* __restrict__ kc, float* __restrict__ vc, int cap,
+                              int pos0) {
+    const int t = blockIdx.x, hd = blockIdx.y, i = threadIdx.x, half = d / 2;
+    const float* src = qkv + ((int64_t)t * (hq + 2 * hkv) + hd) * d;
+    const float x1 = src[i], x2 = src[i + half];
+    if (hd < hq + hkv) {
+        const float2 cs = rope[(int64_t)t * half + i];
+        const float r1 = x1 * cs.x + (-x2) * cs.y;
+        const float r2 = x2 * cs.x + x1 * cs.y;
+        if (hd < hq) {
+            float* dst = q + ((int64_t)hd * T + t) * d;
+            dst[i] = r1;
+            dst[i + half] = r2;
+        } else {
+            const int kh = hd - hq;
+            float* dst = kt + ((int64_t)kh * T + t) * d;
+            dst[i] = r1;
+            dst[i + half] = r2;
+            if (pos0 + t < cap) {
+                float* c = kc + ((int64_t)kh * cap + pos0 + t) * d;
+                c[i] = r1;
+                c[i + half] = r2;
+            }
+        }
+    } else {
+        const int vh = hd - hq - hkv;
+        float* dst = vt + ((int64_t)vh * T + t) * d;
+        dst[i] = x1;
+        dst[i + half] = x2;
+        if (pos0 + t < cap) {
+            float* c = vc + ((int64_t)vh * cap + pos0 + t) * d;
+            c[i] = x1;
+            c[i + half] = x2;
+        }
+    }
+}
+
+// The batched attention's output [heads][T][d] back to token rows [T][heads d]
+// for the o projection.
+__global__ void k_heads_to_rows(const float* __restrict__ a, int T, int heads, int d, float* __restrict__ rows) {
+    const int t = blockIdx.x, h = blockIdx.y;
+    for (int c = threadIdx.x; c < d; c += blockDim.x)
+        rows[((int64_t)t * heads + h) * d + c] = a[((int64_t)h * T + t) * d + c];
+}
+
+// silu(gate) * up for token rows gu [T][2I] (gate | up) into act [T][I]:
+// k_silu_mul's arithmetic, which the decode step's SiLU prologue reproduces.
+__global__ __launch_bounds__(256) void k_silu_mul_rows(const float* __restrict__ gu, int64_t T, int I,
+                                                       float* __restrict__ act) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= T * I) return;
+    const int64_t t = idx / I, j = idx - t * I;
+    const float g = gu[t * 2 * I + j];
+    act[idx] = (g / (1.0f + expf(-g))) * gu[t * 2 * I + I + j];
+}
+
+// the decode state before the prompt's last position: position T - 1 is the
+// one being processed, so the lm_head's advance moves to T
+__global__ void k_prefill_state(int32_t* state, int last) {
+    state[0] = last;
+    state[1] = last + 1;
+}
+
 }  // namespace
 
 // scratch layout of a decode step, in floats
@@ -691,6 +783,123 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
     // a row the GEMV does not hold (linear_decode refuses it by name): the
     // logits, then k_argmax
     TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, fin, m->lm_head.qs, m->lm_head.d, m->vocab, nullptr, m->logits));
+    if (m->vocab % 4 == 0 && reinterpret_cast<uintptr_t>(m->logits) % 16 == 0)
+        hipLaunchKernelGGL((k_argmax<true, true>), dim3(1), dim3(ARGMAX_THREADS), 0, st, m->logits, (int)m->vocab,
+                           nullptr, m->state, m->tokens, m->prompt, (int)m->prompt_len, (int)m->cap);
+    else
+        hipLaunchKernelGGL((k_argmax<true, false>), dim3(1), dim3(ARGMAX_THREADS), 0, st, m->logits, (int)m->vocab,
+                           nullptr, m->state, m->tokens, m->prompt, (int)m->prompt_len, (int)m->cap);
+    TN_LAUNCHED();
+    return TN_OK;
+}
+
+// The prompt's first T tokens in one batched pass per layer (the reference's
+// prefill: LlamaForCausalLM.forward over the prompt, bench_llama_cpp.py:484-523):
+//   h = embed[prompt[0..T)]; per layer: x = rmsnorm(h, ln1); qkv = x W_qkv^T
+//   (the q4_0 GEMM, M = T); rope q, k; k, v to the caches; a = causal SDPA
+//   over the T positions (the f32 prefill); h += a W_o^T; x = rmsnorm(h, ln2);
+//   gu = x W_gate_up^T; h += (silu(gate) * up) W_down^T;
+// then the last position's logits and argmax and the state's advance as a
+// decode step ends (linear_decode_argmax), so decode steps continue at T.
+// Every q4 linear row is the decode GEMV's row bit for bit (the reference's
+// batched == one-row property); the attention's summation order is the
+// prefill kernel's.
+struct PrefillWork {
+    int64_t h, x, qkv, q, kt, vt, att, rows, o, gu, act, rope, total;
+};
+static PrefillWork prefill_work(const tn_llama* m, int64_t T) {
+    PrefillWork w;
+    const int64_t H = m->hidden, D = m->head_dim, Hq = m->n_heads, Hkv = m->n_kv_heads, I = m->inter;
+    int64_t o = 0;
+    auto take = [&](int64_t n) {
+        const int64_t at = o;
+        o += (n + 3) & ~(int64_t)3;  // 16-byte aligned pieces
+        return at;
+    };
+    w.h = take(T * H);
+    w.x = take(T * H);
+    w.qkv = take(T * (Hq + 2 * Hkv) * D);
+    w.q = take(T * Hq * D);
+    w.kt = take(T * Hkv * D);
+    w.vt = take(T * Hkv * D);
+    w.att = take(T * Hq * D);
+    w.rows = take(T * Hq * D);
+    w.o = take(T * H);
+    w.gu = take(T * 2 * I);
+    w.act = take(T * I);
+    w.rope = take(T * D);  // T * D/2 float2
+    w.total = o;
+    return w;
+}
+
+int64_t tn_llama_prefill_work_floats(const tn_llama* model, int64_t tokens) {
+    if (!model || tokens < 1) return 0;
+    return prefill_work(model, tokens).total;
+}
+
+tn_status tn_llama_prefill(void* stream, const tn_llama* m, int64_t T, float* work) {
+    tn_status s = check_model(m);
+    if (s != TN_OK) return s;
+    if (!work) return fail(TN_EVALUE, "tn_llama_prefill: null work buffer");
+    if (T < 1 || T > m->prompt_len || T > m->cap)
+        return fail(TN_EINVAL, "tn_llama_prefill: need 1 <= tokens <= prompt_len <= cap");
+    if (m->head_dim % 2 != 0 || m->head_dim > 1024)
+        return fail(TN_ENOTIMPL, "tn_llama_prefill: head_dim must be even and at most 1024");
+    hipStream_t st = (hipStream_t)stream;
+    const PrefillWork w = prefill_work(m, T);
+    const int64_t H = m->hidden, D = m->head_dim, Hq = m->n_heads, Hkv = m->n_kv_heads, I = m->inter;
+    const int64_t nqkv = (Hq + 2 * Hkv) * D;
+    if (T * std::max(nqkv, 2 * I) > INT32_MAX) return fail(TN_EVALUE, "tn_llama_prefill: prompt too long");
+    float* h = work + w.h;
+    float* x = work + w.x;
+    float* o = work + w.o;
+    float2* rope = reinterpret_cast<float2*>(work + w.rope);
+    hipLaunchKernelGGL(k_prefill_begin, dim3((unsigned)T), dim3(256), 0, st, m->prompt, (int)T, 0, m->embed,
+                       m->vocab, (int)H, h, m->tokens, m->inv_freq, (int)(D / 2), rope);
+    TN_LAUNCHED();
+    for (int64_t l = 0; l < m->n_layers; l++) {
+        const tn_llama_layer& L = m->layers[l];
+        TN_TRY(tn_rmsnorm(stream, h, T, H, L.ln1, m->eps, x));
+        TN_TRY(tn_q4_0_linear(stream, x, TN_F32, T, H, L.qkv.qs, L.qkv.d, nqkv, nullptr, work + w.qkv, TN_F32));
+        hipLaunchKernelGGL(k_prefill_qkv, dim3((unsigned)T, (unsigned)(Hq + 2 * Hkv)), dim3((unsigned)(D / 2)), 0, st,
+                           work + w.qkv, (int)T, (int)Hq, (int)Hkv, (int)D, rope, work + w.q, work + w.kt,
+                           work + w.vt, L.k_cache, L.v_cache, (int)m->cap, 0);
+        TN_LAUNCHED();
+        TN_TRY(tn_sdpa_fwd(stream, TN_F32, work + w.q, work + w.kt, work + w.vt, 1, Hq, Hkv, T, T, D, nullptr, 0,
+                           nullptr, 1, std::nan(""), work + w.att, nullptr));
+        hipLaunchKernelGGL(k_heads_to_rows, dim3((unsigned)T, (unsigned)Hq), dim3((unsigned)std::min<int64_t>(D, 256)),
+                           0, st, work + w.att, (int)T, (int)Hq, (int)D, work + w.rows);
+        TN_LAUNCHED();
+        TN_TRY(tn_q4_0_linear(stream, work + w.rows, TN_F32, T, Hq * D, L.o.qs, L.o.d, H, nullptr, o, TN_F32));
+        TN_TRY(tn_add(stream, h, o, T * H, h));
+        TN_TRY(tn_rmsnorm(stream, h, T, H, L.ln2, m->eps, x));
+        TN_TRY(tn_q4_0_linear(stream, x, TN_F32, T, H, L.gate_up.qs, L.gate_up.d, 2 * I, nullptr, work + w.gu,
+                              TN_F32));
+        hipLaunchKernelGGL(k_silu_mul_rows, dim3((unsigned)cdiv(T * I, 256)), dim3(256), 0, st, work + w.gu, T, (int)I,
+                           work + w.act);
+        TN_LAUNCHED();
+        TN_TRY(tn_q4_0_linear(stream, work + w.act, TN_F32, T, I, L.down.qs, L.down.d, H, nullptr, o, TN_F32));
+        TN_TRY(tn_add(stream, h, o, T * H, h));
+    }
+    // the last position as a decode step ends it: the logits, their argmax
+    // and the advance to position T (the prompt's token there, else the argmax)
+    hipLaunchKernelGGL(k_prefill_state, dim3(1), dim3(1), 0, st, m->state, (int)(T - 1));
+    TN_LAUNCHED();
+    const LlamaWork lw = llama_work(m);
+    GemvPro fin;
+    fin.eps = (float)m->eps;
+    fin.w = m->norm;
+    fin.arg_v = m->work + lw.arg_v;
+    fin.arg_i = reinterpret_cast<int32_t*>(m->work + lw.arg_i);
+    fin.state = m->state;
+    fin.tokens = m->tokens;
+    fin.prompt = m->prompt;
+    fin.prompt_len = (int)m->prompt_len;
+    fin.cap = (int)m->cap;
+    const float* hl = h + (T - 1) * H;
+    s = linear_decode_argmax(st, hl, H, fin, m->lm_head.qs, m->lm_head.d, m->vocab, m->logits);
+    if (s != TN_ENOTIMPL) return s;
+    TN_TRY(linear_decode(st, hl, H, PRO_RMSNORM, fin, m->lm_head.qs, m->lm_head.d, m->vocab, nullptr, m->logits));
     if (m->vocab % 4 == 0 && reinterpret_cast<uintptr_t>(m->logits) % 16 == 0)
         hipLaunchKernelGGL((k_argmax<true, true>), dim3(1), dim3(ARGMAX_THREADS), 0, st, m->logits, (int)m->vocab,
                            nullptr, m->state, m->tokens, m->prompt, (int)m->prompt_len, (int)m->cap);

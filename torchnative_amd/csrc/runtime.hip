@@ -188,7 +188,7 @@ const char* tn_ops(void) {
            "torch._C._quantized_to,torch._C._quantized_blob,"
            "aten._scaled_dot_product_flash_attention_for_cpu.default,sdpa_decode,"
            "aten.embedding.default,rms_norm,rotary_embedding,silu_mul,aten.add.Tensor,aten.argmax.default,"
-           "kv_append,q4_0_linear_decode,llama_decode_step";
+           "kv_append,q4_0_linear_decode,llama_decode_step,llama_prefill";
 }
 
 tn_status tn_probe(char* buf, size_t len) {

@@ -11,9 +11,12 @@ adds and the argmax. The step keeps its position and token on the device,
 so the prompt and the generated tokens run as one sequence of identical
 steps that `capture` can record as a HIP graph.
 
-The prompt is processed one token per step. The q4_0 linear of a row does
-not depend on how many rows are batched with it, so this gives the
-reference's prefill values up to the attention's summation order.
+A prompt runs either one token per step, or in one batched pass per layer
+(`prefill`, `tn_llama_prefill`: the q4_0 linears as GEMMs over the prompt's
+rows and the causal f32 prefill attention), after which the steps continue.
+The q4_0 linear of a row does not depend on how many rows are batched with
+it, so both give the reference's prefill values up to the attention's
+summation order.
 """
 
 from __future__ import annotations
@@ -144,6 +147,8 @@ class Q4Llama:
         self.work = Tensor((int(lib().tn_llama_work_floats(ctypes.byref(m))),), "float32", "hip")
         m.work = self.work.data_ptr()
         self._keep = keep
+        self._prefill_work = None
+        self._prefill_tokens = 0
 
     # --- running -----------------------------------------------------------------------
     def start(self, prompt_ids) -> None:
@@ -163,6 +168,17 @@ class Q4Llama:
     def step(self, stream=None) -> None:
         check(lib().tn_llama_step(stream if stream is not None else current_stream(), ctypes.byref(self._desc)))
 
+    def prefill(self, tokens=None, stream=None) -> None:
+        """Run the loaded prompt's first `tokens` (all of it by default) in one
+        batched pass; the next step() continues at position `tokens`."""
+        t = int(self._desc.prompt_len if tokens is None else tokens)
+        if self._prefill_work is None or self._prefill_tokens < t:
+            n = int(lib().tn_llama_prefill_work_floats(ctypes.byref(self._desc), t))
+            self._prefill_work = Tensor((n,), "float32", "hip")
+            self._prefill_tokens = t
+        check(lib().tn_llama_prefill(stream if stream is not None else current_stream(), ctypes.byref(self._desc), t,
+                                     self._prefill_work.data_ptr()))
+
     def capture(self, steps: int, stream) -> "Graph":
         """Record `steps` consecutive steps as one HIP graph on `stream` (a
         created stream). The graph reads the step state from the device, so
@@ -178,15 +194,21 @@ class Q4Llama:
         """The n_new tokens after an n_prompt-token prompt."""
         return [int(t) for t in self.tokens.numpy()[n_prompt:n_prompt + n_new]]
 
-    def generate(self, prompt_ids, max_new_tokens: int, stream=None, graph: bool = False) -> list:
-        """Greedy decoding: the prompt's last step yields the first new token,
-        each further step one more (max_new_tokens - 1 steps after the prompt)."""
+    def generate(self, prompt_ids, max_new_tokens: int, stream=None, graph: bool = False,
+                 prefill: bool = False) -> list:
+        """Greedy decoding: the prompt's last position yields the first new
+        token, each further step one more (max_new_tokens - 1 steps after the
+        prompt). prefill: the prompt in one batched pass instead of a step
+        per token."""
         n = len(prompt_ids)
         if n + max_new_tokens - 1 > self.cap:
             raise ValueError(f"{n} prompt + {max_new_tokens} new tokens do not fit a cache of {self.cap}")
         self.start(prompt_ids)
-        for _ in range(n):
-            self.step(stream)
+        if prefill:
+            self.prefill(n, stream)
+        else:
+            for _ in range(n):
+                self.step(stream)
         rest = max_new_tokens - 1
         if rest > 0:
             if graph:
