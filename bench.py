@@ -136,6 +136,42 @@ def bench_sdpa(tn, L, dtype, steps, warmup, B=1, Hq=9, Hkv=3, S=2048, D=64, seed
                          "traffic": None}}
 
 
+def bench_sdpa_masked(tn, L, steps, warmup, B=1, Hq=9, Hkv=3, S=2048, D=64, pad=64, seed=2):
+    """Config 2's shape (bf16, causal, GQA) with a bool padding mask
+    [B, 1, 1, S] that hides the last `pad` keys, as a padded batch passes
+    to F.scaled_dot_product_attention; masked calls take the split-row
+    kernel (k_flash16). flops = 4 D Hq over the (query, key) pairs both the
+    causal rule and the mask let through."""
+    rng = np.random.default_rng(seed)
+    q = tn.tensor(rng.standard_normal((B, Hq, S, D)).astype(np.float32), dtype="bfloat16", device="hip")
+    k = tn.tensor(rng.standard_normal((B, Hkv, S, D)).astype(np.float32), dtype="bfloat16", device="hip")
+    v = tn.tensor(rng.standard_normal((B, Hkv, S, D)).astype(np.float32), dtype="bfloat16", device="hip")
+    keep = np.ones((B, 1, 1, S), np.bool_)
+    keep[..., S - pad:] = False
+    mask = tn.tensor(keep, device="hip")
+    strides = (ctypes.c_int64 * 4)(S, 0, 0, 1)  # element strides over (B, Hq, L, S): broadcast heads and rows
+    out = tn.empty((B, Hq, S, D), "bfloat16", "hip")
+    lse = tn.empty((B, Hq, S), "float32", "hip")
+    lib = L.lib()
+
+    def step():
+        st = lib.tn_sdpa_fwd(None, L.TN_BF16, q.data_ptr(), k.data_ptr(), v.data_ptr(), B, Hq, Hkv, S, S, D,
+                             mask.data_ptr(), L.TN_BOOL, strides, 1, float("nan"), out.data_ptr(), lse.data_ptr())
+        if st:
+            L.check(st)
+
+    ms, kern_ms = Timer(tn).run(step, steps, warmup)
+    valid = S - pad
+    # row i attends keys 0 .. min(i, valid - 1)
+    pairs = sum(min(i, valid - 1) + 1 for i in range(S))
+    flops = 4.0 * D * Hq * B * pairs
+    ach = flops / (kern_ms * 1e-3) / 1e12
+    return {"ms_per_step": ms, "kernel_ms": kern_ms, "flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
+            "mask": f"bool [B,1,1,S], last {pad} keys hidden", "kernel": "k_flash16",
+            "roofline": {"bound": "mfma", "achieved": ach, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": ach / BF16_PEAK_TFLOPS, "traffic": None}}
+
+
 def bench_gemv(tn, L, steps, warmup, copies=1024, fmt="q4_0"):
     # q4_k needs K % 256 == 0: its leg uses K = 768 (C1's 576 rounded up)
     n, k = 1536, (768 if fmt == "q4_k" else 576)
@@ -545,7 +581,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c3,c4,c5,q8c1,q8c3,q4kc1,q4kc3)")
+    ap.add_argument("--only", default="", help="comma list of parts to run (c1,c2,c2f32,c2mask,c3,c4,c5,q8c1,q8c3,q4kc1,q4kc3)")
     ap.add_argument("--no-graph", action="store_true",
                     help="c5: time the decode steps as separate launches only (no HIP graph)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -573,6 +609,9 @@ def main():
     if want("c2f32"):
         print("bench: c2 SDPA prefill fp32", file=sys.stderr, flush=True)
         parts["c2_sdpa_prefill_fp32"] = bench_sdpa(tn, L, "float32", args.steps, args.warmup)
+    if want("c2mask"):
+        print("bench: c2 SDPA prefill bf16 with a bool padding mask", file=sys.stderr, flush=True)
+        parts["c2_sdpa_prefill_bf16_padding_mask"] = bench_sdpa_masked(tn, L, args.steps, args.warmup)
     if want("c3"):
         print("bench: c3 q4_0 GEMM", file=sys.stderr, flush=True)
         parts["c3_q4_gemm"] = bench_gemm(tn, L, args.steps, args.warmup)

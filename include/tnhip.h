@@ -205,6 +205,28 @@ tn_status tn_q4_k_dequantize(void* stream, const uint8_t* w, int64_t n, int64_t 
 tn_status tn_q4_k_linear(void* stream, const void* x, int x_dtype, int64_t m, int64_t k,
                          const uint8_t* w, int64_t n, const float* bias, void* y, int y_dtype);
 
+/* ---- dense formats f32 / f16 / bf16: the exactness control ----
+ * `_quantize(t, "f32" | "f16" | "bf16")` stores the weight element by element
+ * (candle k_quants.rs:2778-2910; block size 1) and `_quantized_linear` on such
+ * a weight is a plain matmul on the weight widened to f32 (QMatMul::from_arc,
+ * candle quantized/mod.rs:836-852), which must be bit-identical to the dense
+ * linear (quant.rs:273-279). dtype / w_dtype is TN_F32, TN_F16 or TN_BF16;
+ * anything else is refused with TN_ENOTIMPL.
+ *   quantize: out[i] = x[i] (f32), half's round-to-nearest-even f16 / bf16
+ *     narrowing (NaN keeps its high payload bits and is quieted);
+ *   dequantize: half's exact widening to f32 (a NaN comes back quieted);
+ *   linear: y[m, n] = chain(m, n) (+ bias[n], added once after the chain, as
+ *     the addmm of nn.Linear's bias branch, aten.rs:9686-9700), where
+ *     chain = 0, then fma(x[m, k], widen(w[n, k]), chain) for k = 0 .. K-1 in
+ *     order: one fixed rounding sequence, equal for every m and every launch.
+ *     x f32 [m, k], w [n, k] in w_dtype, bias nullable f32 [n], y f32 [m, n].
+ *     The same function is the dense `F.linear` (bootstrap.py:13352-13357)
+ *     with w_dtype TN_F32. */
+tn_status tn_dense_quantize(void* stream, const float* x, int64_t count, int dtype, void* out);
+tn_status tn_dense_dequantize(void* stream, const void* w, int dtype, int64_t count, float* out);
+tn_status tn_dense_linear(void* stream, const float* x, int64_t m, int64_t k, const void* w, int w_dtype,
+                          int64_t n, const float* bias, float* y);
+
 /* ---- scaled dot-product attention ----
  * `aten._scaled_dot_product_flash_attention_for_cpu(q, k, v, dropout_p=0.,
  * is_causal=False, *, attn_mask=None, scale=None) -> (out, logsumexp)`

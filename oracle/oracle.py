@@ -23,7 +23,7 @@ __all__ = [
     "q4_k_quantize", "q4_k_dequantize", "q8_k_quantize", "vec_dot_q4_k_q8_k", "q4_k_linear", "q4_k_parts",
     "q8_k_parts", "exact_linear_q4_k", "accumulation_k_q4_k", "synth_q4_k_weight", "gamma", "accumulation_k",
     "linear_bound", "sdpa_closed_form", "sdpa_det", "q8_0_ties", "signed_max_ties",
-    "synth_q4_0_weight", "sdpa_tolerance",
+    "synth_q4_0_weight", "sdpa_tolerance", "dense_linear",
 ]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -77,6 +77,8 @@ def lib():
     L.tnref_vec_dot_q4_k_q8_k.restype = ctypes.c_float
     L.tnref_vec_dot_q4_k_q8_k.argtypes = [I64, P, P]
     L.tnref_q4_k_linear.argtypes = [I64, I64, I64, P, P, P, P, I]
+    L.tnref_dense_linear.restype = None
+    L.tnref_dense_linear.argtypes = [I64, I64, I64, P, P, P, P]
     for name in ("tnref_sdpa_f32", "tnref_sdpa_f64"):
         fn = getattr(L, name)
         fn.restype = I
@@ -217,6 +219,21 @@ def q4_0_linear(x, w_blob, n, bias=None, threads=1) -> np.ndarray:
 def q8_0_linear(x, w_blob, n, bias=None, threads=1) -> np.ndarray:
     """The same with a Q8_0 weight blob (34-byte blocks, K:738-757)."""
     return _linear(lib().tnref_q8_0_linear, Q8_0_BYTES, x, w_blob, n, bias, threads)
+
+
+def dense_linear(x, w, bias=None) -> np.ndarray:
+    """x [..., K] . w[N, K]^T (+ bias) in float32, each output the sequential
+    fmaf chain over k that tn_dense_linear declares (the reference's own
+    matmul order, the gemm crate's, is not restated)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    k = x.shape[-1]
+    n = w.shape[0]
+    assert w.shape == (n, k)
+    y = np.empty(x.shape[:-1] + (n,), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    lib().tnref_dense_linear(x.size // k, k, n, _p(x), _p(w), _p(b), _p(y))
+    return y
 
 
 def q4_k_linear(x, w_blob, n, bias=None, threads=1) -> np.ndarray:

@@ -294,6 +294,16 @@ int tnref_q8_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uin
     return q_linear(m, k, n, x, w, 34, tnref_vec_dot_q8_0_q8_0, bias, y, threads);
 }
 
+void tnref_dense_linear(int64_t m, int64_t k, int64_t n, const float* x, const float* w, const float* bias,
+                        float* y) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            float acc = 0.0f;
+            for (int64_t t = 0; t < k; ++t) acc = fmaf(x[i * k + t], w[j * k + t], acc);
+            y[i * n + j] = bias ? acc + bias[j] : acc;
+        }
+}
+
 /* ------------------------------------------------------------------------ */
 /* Q4_K weights with Q8_K activations                                        */
 /* ------------------------------------------------------------------------ */

@@ -45,6 +45,14 @@ float tnref_vec_dot_q4_0_q8_0(int64_t k, const uint8_t* w_row, const uint8_t* xq
  * threads <= 0 means one thread. Returns 0, or -1 on a bad shape. */
 int tnref_q4_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w_blob,
                       const float* bias, float* y, int threads);
+/* The dense control formats' linear (quant.rs:273-279: an f32/f16/bf16
+ * "quantised" weight is widened up front and takes a plain matmul, candle
+ * quantized/mod.rs:836-852). The reference's matmul order is the gemm crate's
+ * and is not restated; this is the order the HIP library declares for
+ * tn_dense_linear: y[m,n] = chain (+ bias[n]), chain = 0 then
+ * fmaf(x[m,k], w[n,k], chain) for k = 0..K-1. w is f32 (already widened). */
+void tnref_dense_linear(int64_t m, int64_t k, int64_t n, const float* x, const float* w, const float* bias,
+                        float* y);
 /* Q8_0 weights: K:738-757 (vec_dot_unopt) per output, the same driver. */
 float tnref_vec_dot_q8_0_q8_0(int64_t k, const uint8_t* w_row, const uint8_t* xq_row);
 int tnref_q8_0_linear(int64_t m, int64_t k, int64_t n, const float* x, const uint8_t* w_blob,

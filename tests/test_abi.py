@@ -136,7 +136,11 @@ def test_python_mirror_refuses_host_operands_instead_of_falling_back():
         tn._quantized_from_blob(b"\0" * 36, (1, 64), "q8_0")
     with pytest.raises(NotImplementedError, match="'q5_k' is not implemented on the hip device"):
         tn._quantize(x, "q5_k")
-    assert tn._quantized_formats() == ["q4_0", "q8_0", "q4_k"]
+    assert tn._quantized_formats() == ["f32", "f16", "bf16", "q4_0", "q8_0", "q4_k"]
+    with pytest.raises(ValueError, match="needs 256 bytes; got 128"):
+        tn._quantized_from_blob(b"\0" * 128, (2, 32), "f32")
+    qf = tn._quantized_from_blob(b"\0" * 128, (2, 32), "f16")  # host blob: 2 bytes per element, no compute
+    assert tn._quantized_nbytes(qf) == 128 and tn._quantized_blob(qf) == b"\0" * 128
     q = tn._quantized_from_blob(b"\0" * 36, (1, 64), "q4_0")  # stays on the host: no compute
     assert tn._quantized_blob(q) == b"\0" * 36 and tn._quantized_nbytes(q) == 36
     with pytest.raises(NotImplementedError, match="hip device"):
@@ -157,6 +161,20 @@ def test_bf16_host_conversion_is_round_to_nearest_even():
     x = np.concatenate([rng.standard_normal(10000).astype(np.float32),
                         np.array([1.00390625, 1.005859375, np.inf, -np.inf, 0.0, -0.0], np.float32)])
     assert np.array_equal(bf16_bits_from_f32(x), O.bf16_from_f32(x))
+
+
+def test_dense_format_refusals(L):
+    from torchnative_amd import _lib
+
+    # the dense formats are f32 / f16 / bf16 only; checked before any launch
+    assert L.tn_dense_quantize(None, None, 8, _lib.TN_F64, None) == _lib.TN_ENOTIMPL
+    assert "dense formats are f32, f16 and bf16" in _lib.last_error()
+    assert L.tn_dense_dequantize(None, None, 99, 8, None) == _lib.TN_ENOTIMPL
+    st = L.tn_dense_linear(None, None, 2, 0, None, _lib.TN_F32, 4, None, None)
+    assert st == _lib.TN_EINVAL and "mat1 and mat2 shapes cannot be multiplied ([2, 0]" in _lib.last_error()
+    assert L.tn_dense_linear(None, None, 2, 8, None, _lib.TN_F16, 4, None, None) == _lib.TN_EVALUE
+    assert "null pointer" in _lib.last_error()
+    assert L.tn_dense_linear(None, None, 0, 8, None, _lib.TN_BF16, 4, None, None) == _lib.TN_OK  # nothing to do
 
 
 def test_fused_decode_linear_refusals(L):

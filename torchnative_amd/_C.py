@@ -28,17 +28,32 @@ _LAYOUT = {
     "q8_0": (32, 34, 32, "tn_q8_0"),
     "q4_k": (256, 144, 144, "tn_q4_k"),  # one plane: the super-blocks, nibbles repacked (include/tnhip.h)
 }
-_FORMATS = tuple(_LAYOUT)
+# dense formats (block size 1, candle k_quants.rs:2778-2910) -> (stored dtype, C ABI code, bytes per element)
+_DENSE = {
+    "f32": ("float32", _lib.TN_F32, 4),
+    "f16": ("float16", _lib.TN_F16, 2),
+    "bf16": ("bfloat16", _lib.TN_BF16, 2),
+}
+_FORMATS = tuple(_DENSE) + tuple(_LAYOUT)
 _REFERENCE_FORMATS = ("f32", "f16", "bf16", "q4_0", "q4_1", "q5_0", "q5_1", "q8_0", "q8_1",
                       "q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "q8_k")
 SDPA_OP = "aten._scaled_dot_product_flash_attention_for_cpu.default"
 
 
+def _block(fmt):
+    """(elements per block, GGML bytes per block) of a format."""
+    if fmt in _DENSE:
+        return 1, _DENSE[fmt][2]
+    return _LAYOUT[fmt][:2]
+
+
 class QTensor:
     """A block-quantised weight [N, K] (the reference's `Repr::Quantized`,
     tensor.rs:970). On "hip" it is two device planes (the code bytes of every
-    block and the f16 scales, include/tnhip.h); on "cpu" it is the GGML blob
-    itself. The dtype tag is float32, as the reference's is (quant.rs:167)."""
+    block and the f16 scales, include/tnhip.h), or for the dense formats
+    f32/f16/bf16 one dense device tensor of that dtype; on "cpu" it is the
+    GGML blob itself. The dtype tag is float32, as the reference's is
+    (quant.rs:167)."""
 
     dtype = "float32"
 
@@ -60,7 +75,11 @@ class QTensor:
 
     @property
     def nblocks(self) -> int:
-        return math.prod(self.shape) // _LAYOUT[self.format][0]
+        return math.prod(self.shape) // _block(self.format)[0]
+
+    @property
+    def dense(self) -> bool:
+        return self.format in _DENSE
 
     def _fn(self, op):
         return getattr(lib(), f"{_LAYOUT[self.format][3]}_{op}")
@@ -110,14 +129,15 @@ def _format_check(op, fmt):
             "vec_dot and no weight format names it as a VecDotType, so a weight stored this way has no matmul. "
             "Use q8_0."
         )
-    if fmt not in _LAYOUT:
+    if fmt not in _LAYOUT and fmt not in _DENSE:
         raise NotImplementedError(
             f"{op}: format {fmt!r} is not implemented on the hip device ({', '.join(_FORMATS)} are)")
 
 
 def _quantize(t: Tensor, fmt: str) -> QTensor:
-    """`_C._quantize(t, format)` (quant.rs:124-172): BlockQ4_0::from_float or
-    BlockQ8_0::from_float on the device."""
+    """`_C._quantize(t, format)` (quant.rs:124-172): BlockQ4_0 / BlockQ8_0 /
+    BlockQ4K::from_float on the device, or for f32/f16/bf16 the element-wise
+    store (a copy, or half's round-to-nearest-even narrowing)."""
     op = "torch._C._quantize"
     _format_check(op, fmt)
     _require_hip(op, t)
@@ -125,6 +145,12 @@ def _quantize(t: Tensor, fmt: str) -> QTensor:
         raise NotImplementedError(f"{op}: a 0-d tensor cannot be quantised")
     if t.dtype != "float32":
         raise NotImplementedError(f"{op}: the hip quantiser takes float32, got {t.dtype}")
+    if fmt in _DENSE:
+        n, k = _shape2(t.shape, fmt)
+        stored, code, _ = _DENSE[fmt]
+        w = Tensor((n, k), stored, "hip")
+        check(lib().tn_dense_quantize(current_stream(), t.data_ptr(), n * k, code, w.data_ptr()))
+        return QTensor((n, k), fmt, "hip", qs=w)
     blk = _LAYOUT[fmt][0]
     if t.shape[-1] % blk:
         raise NotImplementedError(
@@ -142,7 +168,7 @@ def _quantized_from_blob(data: bytes, shape, fmt: str, device="cpu") -> QTensor:
     """`_C._quantized_from_blob(bytes, shape, format)` (quant.rs:230-262)."""
     op = "torch._C._quantized_from_blob"
     _format_check(op, fmt)
-    blk, size = _LAYOUT[fmt][:2]
+    blk, size = _block(fmt)
     numel = math.prod(shape)
     want = numel // blk * size
     if numel % blk or len(data) != want:
@@ -164,6 +190,13 @@ def _quantized_to(t: QTensor, device) -> QTensor:
     if dev == t.device:
         return t
     n, k = t.shape
+    if t.dense:
+        if dev == "hip":
+            w = Tensor((n, k), _DENSE[t.format][0], "hip")
+            src = np.frombuffer(t._blob, dtype=np.uint8)
+            check(lib().tn_memcpy_h2d(w.data_ptr(), src.ctypes.data, src.nbytes, current_stream()))
+            return QTensor(t.shape, t.format, "hip", qs=w)
+        return QTensor(t.shape, t.format, "cpu", blob=t._qs.bits().tobytes())
     if dev == "hip":
         blob = Tensor.from_numpy(np.frombuffer(t._blob, dtype=np.uint8), device="hip")
         qs, d = _planes(n, k, t.format)
@@ -177,6 +210,8 @@ def _quantized_blob(t: QTensor) -> bytes:
     """`_C._quantized_blob(t)` (quant.rs:213-221): the raw GGML bytes."""
     if t.device == "cpu":
         return t._blob
+    if t.dense:
+        return t._qs.bits().tobytes()
     n, k = t.shape
     blob = Tensor((t.nblocks * _LAYOUT[t.format][1],), "uint8", "hip")
     check(t._fn("to_blob")(current_stream(), *t._planes(), n, k, blob.data_ptr()))
@@ -189,7 +224,7 @@ def _quantized_format(t: QTensor) -> str:
 
 def _quantized_nbytes(t: QTensor) -> int:
     """What the weight costs (quant.rs:197-211): the GGML storage size."""
-    return t.nblocks * _LAYOUT[t.format][1]
+    return t.nblocks * _block(t.format)[1]
 
 
 def _dequantize(t: QTensor) -> Tensor:
@@ -198,6 +233,10 @@ def _dequantize(t: QTensor) -> Tensor:
     _require_hip(op, t)
     n, k = t.shape
     out = Tensor((n, k), "float32", "hip")
+    if t.dense:
+        check(lib().tn_dense_dequantize(current_stream(), t._qs.data_ptr(), _DENSE[t.format][1], n * k,
+                                        out.data_ptr()))
+        return out
     check(t._fn("dequantize")(current_stream(), *t._planes(), n, k, out.data_ptr()))
     return out
 
@@ -236,10 +275,48 @@ def _quantized_linear(input: Tensor, weight: QTensor, bias: Tensor | None = None
         _require_hip(op, bias)
     m = input.numel // in_features
     odt = out_dtype or "float32"
+    if weight.dense:
+        # QMatMul::from_arc widens f32/f16/bf16 up front and takes a plain
+        # matmul (candle quantized/mod.rs:836-852): the dense linear itself
+        if input.dtype != "float32" or odt != "float32":
+            raise NotImplementedError(
+                f"{op}: a {weight.format} weight is the dense control path, float32 in and out "
+                f"(got torch.{input.dtype} in, torch.{odt} out)")
+        out = Tensor(input.shape[:-1] + (out_features,), "float32", "hip")
+        check(lib().tn_dense_linear(current_stream(), input.data_ptr(), m, in_features, weight._qs.data_ptr(),
+                                    _DENSE[weight.format][1], out_features,
+                                    bias.data_ptr() if bias is not None else None, out.data_ptr()))
+        return out
     out = Tensor(input.shape[:-1] + (out_features,), odt, "hip")
     check(weight._fn("linear")(current_stream(), input.data_ptr(), _dt(input.dtype), m, in_features,
                                *weight._planes(), out_features,
                                bias.data_ptr() if bias is not None else None, out.data_ptr(), _dt(odt)))
+    return out
+
+
+def linear(input: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+    """`F.linear(input, weight, bias)` for float32 operands on the hip device
+    (bootstrap.py:13352-13357 -> aten.linear; the bias branch is addmm,
+    aten.rs:9686-9700): input @ weight.T, each output one sequential fma chain
+    over in_features (include/tnhip.h, tn_dense_linear), then + bias. The
+    `_quantized_linear` of an f32 "quantised" weight is this same call."""
+    op = "aten.linear.default"
+    _require_hip(op, input, weight, bias)
+    for name, t in (("input", input), ("weight", weight), ("bias", bias)):
+        if t is not None and t.dtype != "float32":
+            raise NotImplementedError(f"{op}: the hip linear takes float32, got torch.{t.dtype} for {name}")
+    if weight.dim() != 2:
+        raise RuntimeError(f"{op}: weight must be 2-d [out_features, in_features], got {list(weight.shape)}")
+    out_features, in_features = weight.shape
+    if input.dim() == 0 or input.shape[-1] != in_features:
+        raise RuntimeError(
+            f"{op}: mat1 and mat2 shapes cannot be multiplied ({list(input.shape)} and {in_features}x{out_features})")
+    if bias is not None and bias.shape != (out_features,):
+        raise RuntimeError(f"{op}: bias shape {list(bias.shape)} does not match out_features {out_features}")
+    out = Tensor(input.shape[:-1] + (out_features,), "float32", "hip")
+    check(lib().tn_dense_linear(current_stream(), input.data_ptr(), input.numel // in_features, in_features,
+                                weight.data_ptr(), _lib.TN_F32, out_features,
+                                bias.data_ptr() if bias is not None else None, out.data_ptr()))
     return out
 
 

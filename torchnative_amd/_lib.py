@@ -99,6 +99,9 @@ SIGNATURES = {
     "tn_q4_k_quantize": (_I, [_P, _P, _I64, _I64, _P]),
     "tn_q4_k_dequantize": (_I, [_P, _P, _I64, _I64, _P]),
     "tn_q4_k_linear": (_I, [_P, _P, _I, _I64, _I64, _P, _I64, _P, _P, _I]),
+    "tn_dense_quantize": (_I, [_P, _P, _I64, _I, _P]),
+    "tn_dense_dequantize": (_I, [_P, _P, _I, _I64, _P]),
+    "tn_dense_linear": (_I, [_P, _P, _I64, _I64, _P, _I, _I64, _P, _P]),
     "tn_q4_0_linear_decode": (_I, [_P, _P, _I64, _I, _P, _D, _P, _P, _I64, _P, _P]),
     "tn_sdpa_fwd": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I, _P, _I, _D, _P, _P]),
     "tn_sdpa_decode": (_I, [_P, _I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _D, _P, _P]),

@@ -13,7 +13,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libtnhip.so")
-SOURCES = ["runtime.hip", "qlinear.hip", "qk.hip", "sdpa.hip", "flash64.hip", "decode.hip"]
+SOURCES = ["runtime.hip", "qlinear.hip", "qk.hip", "sdpa.hip", "flash64.hip", "decode.hip", "dense.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: the q4 recurrence and the SDPA softmax are written with the

@@ -185,6 +185,8 @@ const char* tn_ops(void) {
     return "torch._C._quantize(q4_0),torch._C._dequantize(q4_0),torch._C._quantized_linear(q4_0),"
            "torch._C._quantize(q8_0),torch._C._dequantize(q8_0),torch._C._quantized_linear(q8_0),"
            "torch._C._quantize(q4_k),torch._C._dequantize(q4_k),torch._C._quantized_linear(q4_k),"
+           "torch._C._quantize(f32|f16|bf16),torch._C._dequantize(f32|f16|bf16),"
+           "torch._C._quantized_linear(f32|f16|bf16),aten.linear.default,"
            "torch._C._quantized_to,torch._C._quantized_blob,"
            "aten._scaled_dot_product_flash_attention_for_cpu.default,sdpa_decode,"
            "aten.embedding.default,rms_norm,rotary_embedding,silu_mul,aten.add.Tensor,aten.argmax.default,"

@@ -6,7 +6,8 @@ parents list their children by name, a child is rebound with `setattr`, and
 `.to(device)` visits every module so that each moves what it owns. These
 classes give that shape over this package's tensors: `Module` records child
 modules in assignment order, `Linear` holds a float32 weight [out, in] and
-an optional bias, and `ModuleList` numbers its children.
+an optional bias (its forward is the dense F.linear), and `ModuleList`
+numbers its children.
 """
 
 from __future__ import annotations
@@ -78,7 +79,8 @@ class ModuleList(Module):
 
 class Linear(Module):
     """A dense linear layer: y = x W^T + b, W float32 [out_features, in_features].
-    Only the quantised swap computes with it here; its forward is refused."""
+    forward is `F.linear` on the hip device (_C.linear), the dense side of the
+    `format="f32"` exactness control."""
 
     def __init__(self, weight, bias=None, device="hip"):
         super().__init__()
@@ -100,7 +102,8 @@ class Linear(Module):
         return self
 
     def forward(self, x):
-        raise NotImplementedError("Linear.forward: a dense float32 linear is not a kernel of this backend; "
-                                  "quantize_() the model first")
+        from . import _C
+
+        return _C.linear(x, self.weight, self.bias)
 
     __call__ = forward

@@ -22,7 +22,8 @@ from .tensor import Tensor
 
 class QuantizedLinear:
     """A linear layer over a block-quantised weight [out_features, in_features]
-    (q4_0, q8_0 or q4_k): forward is `_quantized_linear(x, qweight, bias)`."""
+    (q4_0, q8_0 or q4_k, or the dense control formats f32/f16/bf16): forward
+    is `_quantized_linear(x, qweight, bias)`."""
 
     def __init__(self, qweight: "_C.QTensor", bias: Tensor | None = None):
         self.qweight = qweight
