@@ -30,8 +30,9 @@
 // XOR-swizzled ring, lane l owning query l & 31; P = exp2(S*scale*log2e - m)
 // narrowed RNE; O^T += V^T . P^T with V^T read column-wise by
 // ds_read_b64_tr_b16. The reference point m of a row moves only when it
-// must: the probabilities are computed against the current m, and only if
-// the row has none yet or a lane's sum of its sixteen probabilities exceeds
+// must: a row's first tile sets it to that tile's maximum before any
+// exponential; after that the probabilities are computed against the
+// current m, and only if a lane's sum of its sixteen probabilities exceeds
 // 2^10 (so no probability is larger) is the tile's maximum taken, m moved to
 // it, the accumulators rescaled and the probabilities recomputed. That is
 // the same softmax, and it drops the row maximum from the common path.
@@ -195,6 +196,20 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
                 if (key >= S || (causal && key > qi)) v[r] = -INFINITY;
             }
         }
+        // A row with no reference point yet (this key group's first tile of
+        // it) takes the tile's maximum before any exponential, so that its
+        // probabilities are computed once. Rows that have one keep it.
+        if (__any(m == -INFINITY)) {
+            float a = max3f(v[0], v[1], v[2]);
+            a = max3f(a, v[3], v[4]);
+            a = max3f(a, v[5], v[6]);
+            float bm = max3f(v[8], v[9], v[10]);
+            bm = max3f(bm, v[11], v[12]);
+            bm = max3f(bm, v[13], v[14]);
+            const float mx = xor32_max(max3f(max3f(a, v[7], v[15]), bm, bm)) * scl;
+            // o and l are still 0 for such a row: nothing to rescale
+            if (m == -INFINITY) m = mx;
+        }
         // probabilities against the current reference point
         float p[16], ps = 0.0f;
         {
@@ -204,9 +219,9 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
 #pragma unroll
             for (int r = 0; r < 16; r += 4) ps = ps + ((p[r] + p[r + 1]) + (p[r + 2] + p[r + 3]));
         }
-        // the row has no reference point yet, or a probability may exceed 2^10
-        // (or one overflowed): move the reference to the tile's maximum
-        if (__any(m == -INFINITY || !(ps <= FA_SUM_MAX))) {
+        // a probability may exceed 2^10 (or one overflowed): move the
+        // reference to the tile's maximum
+        if (__any(!(ps <= FA_SUM_MAX))) {
             float a = max3f(v[0], v[1], v[2]);
             a = max3f(a, v[3], v[4]);
             a = max3f(a, v[5], v[6]);
