@@ -26,7 +26,8 @@
 // leave for their softmax one after another.
 //
 // Per tile and wave (as k_flash16 in sdpa.hip): S^T = K . Q^T on
-// v_mfma_f32_32x32x16 with Q^T in registers and K rows from the
+// v_mfma_f32_32x32x16 with Q^T in registers (read once from the block's
+// query rows, staged in LDS by one load per 16-byte chunk) and K rows from the
 // XOR-swizzled ring, lane l owning query l & 31; P = exp2(S*scale*log2e - m)
 // narrowed RNE; O^T += V^T . P^T with V^T read column-wise by
 // ds_read_b64_tr_b16. The reference point m of a row moves only when it
@@ -69,6 +70,7 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
     __shared__ float2 s_ml[NW][32];
     __shared__ float s_lf[NW][32];  // each key group's l scaled to the row's reference point
     __shared__ float s_mu[2][32];   // the row's reference point, per query half
+    __shared__ __align__(16) uint16_t sQ[FA_BQ * D];  // the block's query rows, chunks swizzled as K's
     auto stK = [&](auto sc) -> uint16_t* {
         if constexpr (decltype(sc)::value == 0) return sK0; else return sK1;
     };
@@ -101,14 +103,20 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
 
     using E = El<F16>;
     using V8 = typename E::v8;
-    // Q^T operand: lane l holds q[qw0 + (l&31)][16c + 8*(l>>5) .. +7]
-    V8 qf[D / 16];
-#pragma unroll
-    for (int c = 0; c < D / 16; c++) {
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (qi < L) v = *reinterpret_cast<const uint4*>(qp + (int64_t)qi * D + 16 * c + 8 * hh);
-        qf[c] = __builtin_bit_cast(V8, v);
+    // The block's 64 query rows come into LDS once (8 KB, rows past L read
+    // as 0), one 1 KB LDS-DMA load for each of waves 0-7, ahead of the first
+    // stage's K and V: each of the eight key groups of a query half needs
+    // the same rows, and the CU's vector memory path takes a workgroup's
+    // first loads one instruction after another.
+    if (w < FA_BQ * CPR / 64) {
+        const int p = 64 * w + lane;
+        const int row = p / CPR;
+        const buf_rsrc rq = make_rsrc(qp + (int64_t)q0 * D, (uint32_t)(L - q0) * (uint32_t)(D * 2));
+        lds_direct16(rq, (uint32_t)(row * D + swz(row, p % CPR) * 8) * 2u, sQ + 64 * w * 8);
     }
+    // Q^T operand: lane l holds q[qw0 + (l&31)][16c + 8*(l>>5) .. +7], read
+    // from sQ after the first stage's barrier
+    V8 qf[D / 16];
 
     // this lane's byte offset in a stage for its i-th 16-byte load (LDS chunk
     // position p = tid + NT*i holds logical chunk swz(row, p % CPR) of row p / CPR)
@@ -146,6 +154,14 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     issue(I0{}, 0);  // nst >= 1
+    wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < D / 16; c++) {
+        const int row = 32 * qh + lq;
+        qf[c] = *reinterpret_cast<const V8*>(sQ + row * D + swz(row, 2 * c + hh) * 8);
+    }
 
     auto step = [&](auto sc, int st) __attribute__((always_inline)) {
         wait_vmcnt<0>();  // the only loads in flight are this stage's
