@@ -360,6 +360,10 @@ tn_status tn_kv_append(void* stream, const float* k, const float* v, int64_t m, 
  *            TN_PRO_SILU     x [2k] = gate | up -> tn_silu_mul(gate, up)
  *   then y [n] = tn_q4_0_linear of that row (no bias),
  *   then, if resid is non-null, y = tn_add(resid [n], y).
+ * TN_PRO_RMSNORM_SILU is the MLP's first half instead: x [k] ->
+ * tn_rmsnorm(x, prologue_w, eps); the weight holds [gate; up], 2n rows; the
+ * 2n outputs g | u of tn_q4_0_linear give y [n] = tn_silu_mul(g, u) (resid
+ * must be null), so the down projection's input leaves the GEMV finished.
  * The reference runs these as separate ops (LlamaRMSNorm, the SiLU-gated
  * MLP and the residual adds of modeling_llama.py around
  * `_quantized_linear`, quant.rs:286-369); the fusion saves the launches and
@@ -368,6 +372,7 @@ tn_status tn_kv_append(void* stream, const float* k, const float* v, int64_t m, 
 #define TN_PRO_NONE 0
 #define TN_PRO_RMSNORM 1
 #define TN_PRO_SILU 2
+#define TN_PRO_RMSNORM_SILU 3
 tn_status tn_q4_0_linear_decode(void* stream, const float* x, int64_t k, int prologue, const float* prologue_w,
                                 double eps, const uint8_t* qs, const uint16_t* d, int64_t n, const float* resid,
                                 float* y);
@@ -384,7 +389,8 @@ tn_status tn_q4_0_linear_decode(void* stream, const float* x, int64_t k, int pro
  *   h = embed[token]; per layer: x = rmsnorm(h, ln1); qkv = x W_qkv^T;
  *   rope(q, k at pos); append k, v; a = attention(q, cache[0..pos]);
  *   h += a W_o^T; x = rmsnorm(h, ln2); gu = x W_gate_up^T;
- *   h += (silu(gate) * up) W_down^T; then logits = rmsnorm(h, norm) W_lm^T,
+ *   h += (silu(gate) * up) W_down^T (the SiLU in the gate_up launch, as
+ *   TN_PRO_RMSNORM_SILU); then logits = rmsnorm(h, norm) W_lm^T,
  *   next = argmax(logits).
  * The projections are stacked row-wise (q|k|v and gate|up): each output
  * row of the q4 linear is computed on its own, so stacking changes no bit.

@@ -213,6 +213,34 @@ def test_fused_decode_linear_equals_the_separate_ops(tn, k, n):
     assert np.array_equal(got.numpy(), ref.numpy())
 
 
+@pytest.mark.parametrize("k,n", [(576, 1536), (1536, 576), (64, 3), (2304, 70), (128, 256)])
+def test_fused_rmsnorm_silu_linear_equals_the_separate_ops(tn, k, n):
+    """TN_PRO_RMSNORM_SILU (the decode step's gate_up launch) against
+    tn_rmsnorm, tn_q4_0_linear over the stacked [gate; up] weight (2n rows)
+    and tn_silu_mul of its two halves: bit for bit. A residual is refused."""
+    from torchnative_amd import _C
+
+    L = _lib()
+    f = L.lib()
+    rng = np.random.default_rng(k * 5 + n)
+    w = _dev(tn, (rng.standard_normal((2 * n, k)) * 0.05).astype(np.float32))
+    q = _C._quantize(w, "q4_0")
+    qs, d = q._qs.data_ptr(), q._d.data_ptr()
+    x = _dev(tn, (rng.standard_normal(k) * 2).astype(np.float32))
+    g = _dev(tn, rng.standard_normal(k).astype(np.float32))
+    t = tn.empty((k,), "float32", "hip")
+    gu = tn.empty((2 * n,), "float32", "hip")
+    ref, got = tn.empty((n,), "float32", "hip"), tn.empty((n,), "float32", "hip")
+    L.check(f.tn_rmsnorm(None, x.data_ptr(), 1, k, g.data_ptr(), 1e-5, t.data_ptr()))
+    L.check(f.tn_q4_0_linear(None, t.data_ptr(), L.TN_F32, 1, k, qs, d, 2 * n, None, gu.data_ptr(), L.TN_F32))
+    L.check(f.tn_silu_mul(None, gu.data_ptr(), gu.data_ptr() + 4 * n, n, ref.data_ptr()))
+    L.check(f.tn_q4_0_linear_decode(None, x.data_ptr(), k, L.TN_PRO_RMSNORM_SILU, g.data_ptr(), 1e-5, qs, d, n,
+                                    None, got.data_ptr()))
+    assert np.array_equal(got.numpy(), ref.numpy())
+    assert f.tn_q4_0_linear_decode(None, x.data_ptr(), k, L.TN_PRO_RMSNORM_SILU, g.data_ptr(), 1e-5, qs, d, n,
+                                   got.data_ptr(), got.data_ptr()) == L.TN_EINVAL
+
+
 SMALL = OD.LlamaConfig(n_layers=2, hidden=128, n_heads=2, n_kv_heads=1, head_dim=64, inter=256, vocab=512)
 SMALL128 = OD.LlamaConfig(n_layers=2, hidden=256, n_heads=2, n_kv_heads=1, head_dim=128, inter=256, vocab=512)
 

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(HERE, "libtnhip.so")
 
 TN_OK, TN_EINVAL, TN_ENOTIMPL, TN_EHIP, TN_EVALUE = 0, 1, 2, 3, 4
 TN_F32, TN_BF16, TN_F16, TN_F64, TN_BOOL = 0, 1, 2, 3, 4
-TN_PRO_NONE, TN_PRO_RMSNORM, TN_PRO_SILU = 0, 1, 2
+TN_PRO_NONE, TN_PRO_RMSNORM, TN_PRO_SILU, TN_PRO_RMSNORM_SILU = 0, 1, 2, 3
 
 # every symbol include/tnhip.h declares, with (restype, argtypes)
 _P, _I64, _I, _D, _SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double, ctypes.c_size_t

@@ -688,8 +688,9 @@ int64_t tn_llama_work_floats(const tn_llama* model) {
 //   qkv = Q4(rmsnorm(h, ln1))                    linear_decode, RMSNorm prologue
 //   rope q, k; append k, v; split attention      k_step_attn -> partials
 //   h = h + Q4(merge(partials))                  linear_decode, PRO_COMBINE, residual
-//   gu = Q4(rmsnorm(h, ln2))                     linear_decode, RMSNorm prologue
-//   h = h + Q4(silu(gate) * up)                  linear_decode, SiLU prologue
+//   g = silu(gate) * up, gate_up = Q4(rmsnorm(h, ln2))
+//                                                linear_decode, RMSNorm prologue, SiLU epilogue
+//   h = h + Q4(g)                                linear_decode, residual
 // A longer cache replaces the middle two by k_rope_append, the split-KV decode
 // attention with its combine, and the o projection on its output.
 // Then logits = Q4(rmsnorm(h, norm)) with per-workgroup argmax partials, and
@@ -714,8 +715,9 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
     int32_t* pos = m->state;      // [0]: position of this token
     int32_t* len = m->state + 1;  // [1]: KV length after appending it
     const double nan = std::nan("");
-    GemvPro none, ln1, ln2, fin, comb;
-    ln1.eps = ln2.eps = fin.eps = eps;
+    GemvPro none, ln1, ln2g, fin, comb;
+    ln1.eps = ln2g.eps = fin.eps = eps;
+    ln2g.glu = 1;
     fin.w = m->norm;
     // short caches: the fused split attention, merged in the o projection
     const int nrep = (int)(Hq / Hkv);
@@ -735,7 +737,7 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
     for (int64_t l = 0; l < m->n_layers; l++) {
         const tn_llama_layer& L = m->layers[l];
         ln1.w = L.ln1;
-        ln2.w = L.ln2;
+        ln2g.w = L.ln2;
         TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, ln1, L.qkv.qs, L.qkv.d, nqkv, nullptr, qkv));
         if (fused) {
             const dim3 grid((unsigned)nsplit_step, (unsigned)Hkv);
@@ -767,8 +769,9 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
                                  attn, nullptr, part_o, part_ml));
             TN_TRY(linear_decode(st, attn, Hq * D, PRO_NONE, none, L.o.qs, L.o.d, H, h, h));
         }
-        TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, ln2, L.gate_up.qs, L.gate_up.d, 2 * I, nullptr, gu));
-        TN_TRY(linear_decode(st, gu, I, PRO_SILU, none, L.down.qs, L.down.d, H, h, h));
+        // silu(gate) * up in the gate_up GEMV's epilogue, once, into gu[0, I)
+        TN_TRY(linear_decode(st, h, H, PRO_RMSNORM, ln2g, L.gate_up.qs, L.gate_up.d, I, nullptr, gu));
+        TN_TRY(linear_decode(st, gu, I, PRO_NONE, none, L.down.qs, L.down.d, H, h, h));
     }
     // the logits with their argmax partials, then the argmax and the state's advance
     fin.arg_v = m->work + w.arg_v;

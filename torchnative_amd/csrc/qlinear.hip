@@ -357,7 +357,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_argmax_parts(const float* __re
 
 // Epilogue ARG (MR == 1, f32 y; linear_decode_argmax): each workgroup's best
 // output of y to po.arg_v/arg_i[workgroup], for k_argmax_parts.
-template <int FMT, int MR, typename XT, int PRO, bool ARG = false>
+// Epilogue GLU (MR == 1, f32 y, no bias or residual): the weight is
+// [gate; up], 2N rows, and y[n] = silu(gate_n) * up_n over the N outputs
+// (tn_silu_mul of the two halves, its arithmetic): a tile holds gate rows
+// row0 .. row0+rows-1 and the matching up rows, and the thread that sums
+// output n's gate row sums its up row too.
+template <int FMT, int MR, typename XT, int PRO, bool ARG = false, bool GLU = false>
 __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x, int K, int nb,
                                                      const uint8_t* __restrict__ qs,
                                                      const uint16_t* __restrict__ dw, int N, int rows,
@@ -365,6 +370,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                                                      int y_bf16, const GemvPro po) {
     static_assert(PRO == PRO_NONE || (MR == 1 && sizeof(XT) == 4), "prologues take one f32 row");
     static_assert(!ARG || MR == 1, "the argmax epilogue takes one row");
+    static_assert(!GLU || (MR == 1 && !ARG), "the SiLU epilogue takes one row");
     constexpr int HOLD = PRO == PRO_COMBINE ? 1 : GEMV_HOLD;
     constexpr int ITEMS = Fmt<FMT>::GEMV_ITEMS, NV = Fmt<FMT>::CODE_BYTES / 16;
     extern __shared__ __align__(16) char smem[];
@@ -372,7 +378,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
     int* xq = reinterpret_cast<int*>(smem);               // [MR][K/4] packed int8 codes
     float* dxs = reinterpret_cast<float*>(xq + MR * (K / 4));  // [MR][nb]
     int* sxs = reinterpret_cast<int*>(dxs + MR * nb);     // [MR][nb]
-    // [2][rows][MR][nbp]: term rows padded to 16 bytes for the float4 reads of phase 3
+    // [2][rows (GLU: 2 rows)][MR][nbp]: term rows padded to 16 bytes for the float4 reads of phase 3
     const int nbp = (nb + 3) & ~3;
     float* terms = reinterpret_cast<float*>(smem + ((MR * K + 8 * MR * nb + 15) & ~15));
     const int tid = threadIdx.x;
@@ -383,16 +389,19 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
     // (a third, two tiles ahead, measured slower: fewer resident waves)
     uint4 wv[ITEMS][NV], wn[ITEMS][NV];
     uint16_t dv[ITEMS], dn[ITEMS];
+    constexpr int RW = GLU ? 2 : 1;  // weight rows per output
     auto gload = [&](int tile, uint4 (*wr)[NV], uint16_t* dr) {
         const int64_t row0 = (int64_t)tile * rows;
         const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
-        const int total = nrows * nb;
+        const int total = RW * nrows * nb;
         const uint4* qbase = reinterpret_cast<const uint4*>(qs) + row0 * nb * NV;
         const uint16_t* dbase = dw + row0 * nb;
 #pragma unroll
         for (int it = 0; it < ITEMS; it++) {
-            const int g = tid + it * GEMV_THREADS;
+            int g = tid + it * GEMV_THREADS;
             if (g < total) {
+                // GLU: items past the tile's gate rows are its up rows, N rows on
+                if (GLU && g >= nrows * nb) g += (N - nrows) * nb;
                 // streamed once: a non-temporal load keeps it from evicting x and the terms
 #pragma unroll
                 for (int v = 0; v < NV; v++) {
@@ -403,25 +412,32 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
             }
         }
     };
-    // the first tile's weight loads (and this thread's residual and bias for
-    // it) are in flight during the activation work
     int tile = (int)blockIdx.x;
     float pre_add = 0.0f;
-    if (tile < ntiles) {
-        gload(tile, wv, dv);
-        const int64_t row0 = (int64_t)tile * rows;
-        const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
-        if (tid < nrows * MR) {
-            const int r = tid / MR, mr = tid - r * MR;
-            if (bias) pre_add = bias[row0 + r];
-            if (resid) pre_add = resid[(int64_t)mr * N + row0 + r];  // resid and bias are not combined
+    // the first tile's weight loads (and this thread's residual and bias for
+    // it), in flight during the activation work
+    auto first_loads = [&]() {
+        if (tile < ntiles) {
+            gload(tile, wv, dv);
+            const int64_t row0 = (int64_t)tile * rows;
+            const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
+            if (tid < nrows * MR) {
+                const int r = tid / MR, mr = tid - r * MR;
+                if (bias) pre_add = bias[row0 + r];
+                if (resid) pre_add = resid[(int64_t)mr * N + row0 + r];  // resid and bias are not combined
+            }
         }
-    }
+    };
 
     // phase 1: Q8_0 of the MR activation rows (after the prologue)
     {
         const int g8 = tid & 7, slot = tid >> 3;
         const int nblk = MR * nb, npass = (nblk + 31) / 32;
+        // a row that fits the registers is loaded before the weights, whose
+        // loads would otherwise stand in front of it in the memory pipeline
+        // (the merge of the attention partials, PRO_COMBINE, is left behind
+        // them: it computes as it loads)
+        const bool early = PRO != PRO_COMBINE && npass <= HOLD;
         float4 xv[HOLD], av[HOLD];  // the row, and the prologue's second operand
         int ns = 0;
         if constexpr (PRO == PRO_COMBINE) {
@@ -483,11 +499,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                 }
             }
         };
+        if (early) load_passes(0);
+        first_loads();
         float r = 0.0f;
         if constexpr (PRO == PRO_RMSNORM) {
             float ss = 0.0f;
             for (int p0 = 0; p0 < npass; p0 += HOLD) {
-                load_passes(p0);
+                if (!early) load_passes(p0);
 #pragma unroll
                 for (int u = 0; u < HOLD; u++) {
                     if ((p0 + u) * 32 + slot < nblk) {
@@ -502,8 +520,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
         }
         int8_t* xb = reinterpret_cast<int8_t*>(xq);
         for (int p0 = 0; p0 < npass; p0 += HOLD) {
-            // the RMSNorm pass already holds a row of up to HOLD passes
-            if (PRO != PRO_RMSNORM || npass > HOLD) load_passes(p0);
+            // a row of up to HOLD passes is already held
+            if (!early) load_passes(p0);
 #pragma unroll
             for (int u = 0; u < HOLD; u++) {
                 const int blk = (p0 + u) * 32 + slot;
@@ -551,8 +569,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
         if (next < ntiles) gload(next, wn, dn);
         const int64_t row0 = (int64_t)tile * rows;
         const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
-        const int total = nrows * nb;
-        float* tb = terms + buf * rows * MR * nbp;
+        const int total = RW * nrows * nb;
+        float* tb = terms + buf * RW * rows * MR * nbp;
 #pragma unroll
         for (int it = 0; it < ITEMS; it++) {
             const int g = tid + it * GEMV_THREADS;
@@ -575,12 +593,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
         }
         __syncthreads();
         // each output's terms in block order, read 16 at a time
-        for (int o = tid; o < nrows * MR; o += GEMV_THREADS) {
-            const int r = o / MR, mr = o - r * MR;
-            const int64_t n = row0 + r;
-            float add = pre_add;
-            if (tile != (int)blockIdx.x || o != tid) add = bias ? bias[n] : resid ? resid[(int64_t)mr * N + n] : 0.0f;
-            const float* tr = tb + (r * MR + mr) * nbp;
+        // one row's terms in block order
+        auto ordered_sum = [&](const float* tr) {
             float acc = 0.0f;
             int b = 0;
             for (; b + 16 <= nb; b += 16) {
@@ -603,6 +617,19 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                 acc = acc + t4.w;
             }
             for (; b < nb; b++) acc = acc + tr[b];
+            return acc;
+        };
+        for (int o = tid; o < nrows * MR; o += GEMV_THREADS) {
+            const int r = o / MR, mr = o - r * MR;
+            const int64_t n = row0 + r;
+            float add = pre_add;
+            if (tile != (int)blockIdx.x || o != tid) add = bias ? bias[n] : resid ? resid[(int64_t)mr * N + n] : 0.0f;
+            float acc = ordered_sum(tb + (r * MR + mr) * nbp);
+            if constexpr (GLU) {
+                // silu(gate) * up, tn_silu_mul's arithmetic
+                const float up = ordered_sum(tb + (nrows + r) * nbp);
+                acc = (acc / (1.0f + expf(-acc))) * up;
+            }
             if (bias || resid) acc = acc + add;
             if constexpr (ARG) {
                 if (arg_before(acc, (int)n, best_v, best_i)) {
@@ -1212,7 +1239,7 @@ tn_status check_weight(const char* op, const char* fmt, int64_t n, int64_t k) {
     return TN_OK;
 }
 
-template <int FMT, int MR, typename XT, int PRO = PRO_NONE, bool ARG = false>
+template <int FMT, int MR, typename XT, int PRO = PRO_NONE, bool ARG = false, bool GLU = false>
 tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, const uint16_t* dw, int N,
                       const float* bias, void* y, int y_bf16, const float* resid = nullptr,
                       const GemvPro& po = GemvPro(), unsigned* grid_out = nullptr) {
@@ -1220,7 +1247,8 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     constexpr int ITEMS = Fmt<FMT>::GEMV_ITEMS;
     // rows per tile: as many as ITEMS items per thread allow, but no more
     // than it takes to give every CU a tile of a small matrix
-    int rows = (GEMV_THREADS * ITEMS) / nb;
+    constexpr int RW = GLU ? 2 : 1;  // weight rows per output (GLU: gate and up)
+    int rows = (GEMV_THREADS * ITEMS) / (RW * nb);
     const int spread = (int)cdiv(N, 256);
     if (rows > spread) rows = spread;
     if (rows < 1) rows = 1;
@@ -1229,7 +1257,7 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     if (bias && resid) return fail(TN_EINVAL, "quantised GEMV: bias and residual together are not supported");
     const int nbp = (nb + 3) & ~3;
     auto lds_of = [&](int r) {
-        return (((size_t)MR * K + (size_t)MR * nb * 8 + 15) & ~(size_t)15) + 2 * (size_t)r * MR * nbp * 4;
+        return (((size_t)MR * K + (size_t)MR * nb * 8 + 15) & ~(size_t)15) + 2 * (size_t)RW * r * MR * nbp * 4;
     };
     size_t lds = lds_of(rows);
     while (rows > 1 && lds > 64 * 1024) {
@@ -1238,18 +1266,19 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     }
     if (lds > 64 * 1024) return TN_ENOTIMPL;  // caller falls through to the GEMM path
     // (row, block) items must fit ITEMS per thread
-    if ((int64_t)rows * nb > GEMV_THREADS * ITEMS) return TN_ENOTIMPL;
+    if ((int64_t)RW * rows * nb > GEMV_THREADS * ITEMS) return TN_ENOTIMPL;
+    if (GLU && (bias || resid)) return fail(TN_EINVAL, "quantised GEMV: the SiLU epilogue takes no bias or residual");
     const int64_t ntiles = cdiv(N, rows);
     // persistent: exactly as many workgroups as the device holds at once (a
     // workgroup that had to wait for a slot would start its whole share of
     // tiles late)
     int resident = 0;
-    tn_status s = resident_workgroups(reinterpret_cast<const void*>(&k_gemv<FMT, MR, XT, PRO, ARG>), GEMV_THREADS,
+    tn_status s = resident_workgroups(reinterpret_cast<const void*>(&k_gemv<FMT, MR, XT, PRO, ARG, GLU>), GEMV_THREADS,
                                       lds, &resident);
     if (s != TN_OK) return s;
     unsigned grid = (unsigned)(ntiles < resident ? ntiles : resident);
     if (ARG && grid > (unsigned)GEMV_ARG_MAX_PARTS) grid = (unsigned)GEMV_ARG_MAX_PARTS;
-    hipLaunchKernelGGL((k_gemv<FMT, MR, XT, PRO, ARG>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N,
+    hipLaunchKernelGGL((k_gemv<FMT, MR, XT, PRO, ARG, GLU>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N,
                        rows, bias, resid, y, y_bf16, po);
     TN_LAUNCHED();
     if (grid_out) *grid_out = grid;
@@ -1409,7 +1438,11 @@ tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, cons
     if (n == 0) return TN_OK;
     switch (pro) {
         case PRO_RMSNORM:
-            s = launch_gemv<FMT_Q4_0, 1, float, PRO_RMSNORM>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po);
+            if (po.glu)
+                s = launch_gemv<FMT_Q4_0, 1, float, PRO_RMSNORM, false, true>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0,
+                                                                             resid, po);
+            else
+                s = launch_gemv<FMT_Q4_0, 1, float, PRO_RMSNORM>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po);
             break;
         case PRO_SILU: s = launch_gemv<FMT_Q4_0, 1, float, PRO_SILU>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po); break;
         case PRO_COMBINE:
@@ -1483,11 +1516,14 @@ tn_status tn_q4_0_linear_decode(void* stream, const float* x, int64_t k, int pro
                                 double eps, const uint8_t* qs, const uint16_t* d, int64_t n, const float* resid,
                                 float* y) {
     const char* op = "q4_0_linear_decode";
-    if (prologue != TN_PRO_NONE && prologue != TN_PRO_RMSNORM && prologue != TN_PRO_SILU)
+    if (prologue != TN_PRO_NONE && prologue != TN_PRO_RMSNORM && prologue != TN_PRO_SILU &&
+        prologue != TN_PRO_RMSNORM_SILU)
         return fail(TN_EINVAL, std::string(op) + ": unknown prologue");
     if (k <= 0 || n < 0) return fail(TN_EINVAL, std::string(op) + ": bad sizes");
+    const bool glu = prologue == TN_PRO_RMSNORM_SILU;
+    if (glu && resid) return fail(TN_EINVAL, std::string(op) + ": the SiLU epilogue takes no residual");
     if (n == 0) return TN_OK;
-    if (!x || !qs || !d || !y || (prologue == TN_PRO_RMSNORM && !prologue_w))
+    if (!x || !qs || !d || !y || ((prologue == TN_PRO_RMSNORM || glu) && !prologue_w))
         return fail(TN_EVALUE, std::string(op) + ": null pointer");
     // y is written while other workgroups still read x
     const char* xb = reinterpret_cast<const char*>(x);
@@ -1500,7 +1536,8 @@ tn_status tn_q4_0_linear_decode(void* stream, const float* x, int64_t k, int pro
     GemvPro po;
     po.w = prologue_w;
     po.eps = (float)eps;
-    return linear_decode((hipStream_t)stream, x, k, prologue, po, qs, d, n, resid, y);
+    po.glu = glu ? 1 : 0;
+    return linear_decode((hipStream_t)stream, x, k, glu ? PRO_RMSNORM : prologue, po, qs, d, n, resid, y);
 }
 
 tn_status tn_q4_0_linear(void* stream, const void* x, int x_dtype, int64_t m, int64_t k, const uint8_t* qs,

@@ -279,6 +279,9 @@ constexpr int STEP_MAX_SPLITS = 16;
 struct GemvPro {
     const float* w = nullptr;  // PRO_RMSNORM weight [K]
     float eps = 0.0f;
+    // PRO_RMSNORM with the SiLU epilogue: the weight is [gate; up] (2n rows)
+    // and y[i] = silu(gate_i) * up_i, n outputs (linear_decode)
+    int glu = 0;
     // PRO_COMBINE: partials [heads][nsplit][head_dim] and (m, l) [heads][nsplit]
     // in log2 units over splits of STEP_SPLIT keys; the KV length is
     // min(*len, cap)
@@ -305,8 +308,10 @@ constexpr int GEMV_ARG_MAX_PARTS = 2048;
 // One f32 row through a q4_0 linear (qlinear.hip), y[n] = Q8_0(pro(x)) . W^T
 // (+ resid[n]): pro is a LinearPrologue (PRO_RMSNORM scales by po.w with
 // po.eps; PRO_SILU reads x as [gate | up], 2k floats; PRO_COMBINE ignores x
-// and merges po's attention partials). Bit-identical to the separate ops in
-// sequence. y may alias resid, not x. k <= LINEAR_DECODE_MAX_K.
+// and merges po's attention partials). With PRO_RMSNORM and po.glu the
+// weight is [gate; up], 2n rows, and y[i] = silu(gate_i) * up_i (no resid).
+// Bit-identical to the separate ops in sequence. y may alias resid, not x.
+// k <= LINEAR_DECODE_MAX_K.
 constexpr int64_t LINEAR_DECODE_MAX_K = 24576;  // 768 blocks: one per (row, block) item of the workgroup
 tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, const GemvPro& po, const uint8_t* qs,
                         const uint16_t* d, int64_t n, const float* resid, float* y);
