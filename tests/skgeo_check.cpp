@@ -3,8 +3,9 @@
 // unit range exactly as k_fa_f32 does and checks that: the ranges are
 // non-empty and cover every unit once; a block covered whole is written by
 // one workgroup; a cut block's partials sit in distinct slots, which the
-// merge's arithmetic (wg_at, lo) finds again, in workgroup order; and no
-// workgroup cuts more than its first and last block. Prints "ok <shapes>" or
+// merge's arithmetic (wg_at, lo) finds again, in workgroup order; no
+// workgroup cuts more than its first and last block; and the XCD numbering of
+// the workgroups (xcd_order) is a bijection. Prints "ok <shapes>" or
 // the first failure.
 #define __host__
 #define __device__
@@ -33,6 +34,16 @@ static int check(int64_t BH, int L, int S, int causal, int BQ, int BK, int slots
     std::map<int64_t, int> whole;
     std::vector<int> seen(geo.T, 0);
     if (geo.lo(0) != 0 || geo.lo(geo.G) != geo.T) return 1;
+    {
+        // xcd_order is a bijection of 0 .. G-1, and the workgroups one XCD
+        // takes (b = x, x + 8, ...) get consecutive range numbers
+        std::vector<int> hit(geo.G, 0);
+        for (int64_t b = 0; b < geo.G; b++) {
+            const int64_t g = geo.xcd_order(b);
+            if (g < 0 || g >= geo.G || hit[g]++) return 12;
+            if (b >= 8 && g != geo.xcd_order(b - 8) + 1) return 13;
+        }
+    }
     for (int64_t g = 0; g < geo.G; g++) {
         const int64_t u_lo = geo.lo(g), u_hi = geo.lo(g + 1);
         if (u_hi <= u_lo) return 2;  // an empty range

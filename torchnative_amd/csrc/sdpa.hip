@@ -710,7 +710,8 @@ __global__ __launch_bounds__(PF_THREADS) void k_fa_f32(const float* __restrict__
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int lq = lane & 15, g = lane >> 4;
-    const int64_t gw = blockIdx.x;
+    // consecutive ranges on one XCD: a head's K and V fetched into one or two L2s
+    const int64_t gw = geo.xcd_order(blockIdx.x);
     const int64_t u_hi = geo.lo(gw + 1);
 
     // query block qt of (batch, head) bh, key tiles t_begin .. t_end-1;
@@ -902,6 +903,10 @@ __global__ __launch_bounds__(PF_THREADS) void k_fa_f32(const float* __restrict__
         // order and returns the counter to zero for the next launch. No
         // fence is needed: only the partials cross workgroups, and they never
         // sit in a non-coherent cache.
+        // A slot's O is kept in register order: store k = 4e + r of wave w is
+        // 1 KB at float (w * 4 DS + k) * 256, lane by lane, so every write-
+        // through store covers whole lines (row-major rows took 16-byte
+        // pieces at a 64-byte stride, which memory saw as partial writes).
         constexpr uint32_t SC1 = 16;  // cache policy: device scope
         typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
         typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -910,13 +915,14 @@ __global__ __launch_bounds__(PF_THREADS) void k_fa_f32(const float* __restrict__
 #if __HIP_DEVICE_COMPILE__
         {
             const uint32_t prow = (uint32_t)(slot * BQ + w * 16 + lq);
+            const uint32_t wbase = (uint32_t)slot * (uint32_t)(BQ * D) + (uint32_t)(w * 4 * DS) * 256u + 4u * lane;
 #pragma unroll
             for (int e = 0; e < DS; e++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const u32x4_t v = {__float_as_uint(o[e][0][r]), __float_as_uint(o[e][1][r]),
                                        __float_as_uint(o[e][2][r]), __float_as_uint(o[e][3][r])};
-                    __builtin_amdgcn_raw_buffer_store_b128(v, ro, (prow * D + 64 * e + 16 * g + 4 * r) * 4u, 0, SC1);
+                    __builtin_amdgcn_raw_buffer_store_b128(v, ro, (wbase + (uint32_t)(4 * e + r) * 256u) * 4u, 0, SC1);
                 }
             if (g == 0) {
                 const u32x2_t v = {__float_as_uint(m), __float_as_uint(l)};
@@ -938,21 +944,25 @@ __global__ __launch_bounds__(PF_THREADS) void k_fa_f32(const float* __restrict__
         const int64_t s_lo = 2 * g_lo + (geo.lo(g_lo) < u0 ? 1 : 0);
         const int np = (int)(g_hi - g_lo + 1);
 #if __HIP_DEVICE_COMPILE__
-        constexpr int TPR = D / 4;  // threads per row, four columns each
-        constexpr int CMAX = 8;     // partials whose loads are in flight together
-        const int c4 = (tid % TPR) * 4;
-        for (int rr = tid / TPR; rr < BQ; rr += PF_THREADS / TPR) {
+        constexpr int CMAX = 8;  // partials whose loads are in flight together
+        // item it is float 4 it of a slot in register order: four columns of
+        // one row, consecutive threads reading consecutive 16 bytes
+        for (int it = tid; it < BQ * D / 4; it += PF_THREADS) {
+            const int ln = it & 63, k = (it >> 6) % (4 * DS), wv = (it >> 6) / (4 * DS);
+            const int rr = 16 * wv + (ln & 15);
+            const int c4 = 64 * (k >> 2) + 16 * (ln >> 4) + 4 * (k & 3);
             const int qrow = qt * BQ + rr;
-            if (qrow >= L) break;
+            if (qrow >= L) continue;
             auto prow_of = [&](int i) { return (uint32_t)((i == 0 ? s_lo : 2 * (g_lo + i)) * BQ + rr); };
+            auto slot_of = [&](int i) { return (uint32_t)(i == 0 ? s_lo : 2 * (g_lo + i)); };
             typedef float f32x2_t __attribute__((ext_vector_type(2)));
             typedef float f32x4_t __attribute__((ext_vector_type(4)));
             auto ld_ml = [&](int i) {
                 return __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rm, prow_of(i) * 8u, 0, SC1));
             };
             auto ld_o = [&](int i) {
-                return __builtin_bit_cast(f32x4_t,
-                                          __builtin_amdgcn_raw_buffer_load_b128(ro, (prow_of(i) * D + c4) * 4u, 0, SC1));
+                return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       ro, (slot_of(i) * (uint32_t)(BQ * D) + 4u * it) * 4u, 0, SC1));
             };
             f32x2_t mlv[CMAX];
             f32x4_t pv[CMAX];

@@ -29,6 +29,14 @@ struct SkGeo {
         return (int64_t)c * m * (m + 1) / 2 + ((int64_t)qt - m) * NS;
     }
     __host__ __device__ int64_t lo(int64_t g) const { return g * T / G; }
+    // The range number of hardware workgroup b. Workgroups are dealt to the
+    // eight XCDs in turn (b to XCD b % 8); XCD x takes the consecutive
+    // numbers x*(G/8) + min(x, G%8) onwards, so that the ranges of one head
+    // stay on one or two XCDs' L2s. A bijection of 0 .. G-1.
+    __host__ __device__ int64_t xcd_order(int64_t b) const {
+        const int64_t x = b % 8, qx = G / 8, rx = G % 8;
+        return x * qx + (x < rx ? x : rx) + b / 8;
+    }
     __host__ __device__ int64_t wg_of(int64_t u) const { return ((u + 1) * G + T - 1) / T - 1; }
     // the query block (bh, qt) that holds unit u, and u's tile in it
     __host__ __device__ void locate(int64_t u, int64_t& bh, int& qt, int& t) const {
