@@ -729,6 +729,7 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
     comb.len = len;
     comb.nsplit = (int)nsplit_step;
     comb.head_dim = (int)D;
+    while ((1 << comb.head_shift) < comb.head_dim) comb.head_shift++;  // the fused path's D is 64 or 128
     comb.cap = (int)m->cap;
     const float sl2 = (float)(1.0 / std::sqrt((double)D)) * STEP_LOG2E;
     hipLaunchKernelGGL(k_step_begin, dim3((unsigned)cdiv(H, 256)), dim3(256), 0, st, m->state, m->embed, m->vocab,

@@ -217,6 +217,7 @@ constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_MAX_M = 4;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ inline int dot_block(uint4 w, const int* __restrict__ xw) {
     // xw: the 32 int8 codes of the block as 8 dwords, natural element order.
@@ -264,6 +265,7 @@ __device__ inline int dot_block_q8(const uint4& w0, const uint4& w1, const int* 
 // Epilogue: y = acc (+ bias, or + resid: never both); y may alias resid (each
 // output's thread reads its residual before writing it), never x. x must be 16-byte aligned.
 constexpr int GEMV_HOLD = 4;  // passes of 32 blocks held in registers (K <= 4096 per row at once)
+constexpr int GEMV_ONE = 0, GEMV_STREAM = 1, GEMV_PASSES = 2;  // k_gemv's SHAPE
 
 // The best (value, index) over a workgroup of GEMV_THREADS threads, in
 // thread 0 (arg_before's order: any pairing gives the same winner).
@@ -362,7 +364,22 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_argmax_parts(const float* __re
 // (tn_silu_mul of the two halves, its arithmetic): a tile holds gate rows
 // row0 .. row0+rows-1 and the matching up rows, and the thread that sums
 // output n's gate row sums its up row too.
-template <int FMT, int MR, typename XT, int PRO, bool ARG = false, bool GLU = false>
+// SHAPE (launch_gemv picks):
+//   GEMV_ONE     the activation rows fit the registers (MR * nb <= 32 * HOLD
+//                blocks) and every workgroup has one row tile: the rows are
+//                loaded once, ahead of the weights, in straight-line code,
+//                and every weight load is unconditional, so the compiler's
+//                waits for the rows do not also wait for the weights (the
+//                decode step's GEMVs, latency-bound)
+//   GEMV_STREAM  rows held, several tiles per workgroup with the next tile's
+//                loads in flight (a streamed weight, bandwidth-bound; these
+//                loads stay conditional: the unconditional form takes ten
+//                more VGPRs, which costs a wave per SIMD here)
+//   GEMV_PASSES  rows too long to hold, loaded in passes (twice with the
+//                RMSNorm prologue), several tiles per workgroup
+// Separate instantiations rather than branches: in one kernel the compiler
+// joins the paths, and the waits on one path then count the other's loads.
+template <int FMT, int MR, typename XT, int PRO, bool ARG = false, bool GLU = false, int SHAPE = GEMV_ONE>
 __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x, int K, int nb,
                                                      const uint8_t* __restrict__ qs,
                                                      const uint16_t* __restrict__ dw, int N, int rows,
@@ -373,6 +390,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
     static_assert(!GLU || (MR == 1 && !ARG), "the SiLU epilogue takes one row");
     constexpr int HOLD = PRO == PRO_COMBINE ? 1 : GEMV_HOLD;
     constexpr int ITEMS = Fmt<FMT>::GEMV_ITEMS, NV = Fmt<FMT>::CODE_BYTES / 16;
+    constexpr bool HELD = SHAPE != GEMV_PASSES, ONE = SHAPE == GEMV_ONE;
     extern __shared__ __align__(16) char smem[];
     __shared__ float red[4];
     int* xq = reinterpret_cast<int*>(smem);               // [MR][K/4] packed int8 codes
@@ -382,6 +400,15 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
     const int nbp = (nb + 3) & ~3;
     float* terms = reinterpret_cast<float*>(smem + ((MR * K + 8 * MR * nb + 15) & ~15));
     const int tid = threadIdx.x;
+    // PRO_COMBINE: the weight items start at the first wave that merges no
+    // block of the row (wave 3 at K = 576), so that the merging waves issue
+    // only their partial loads and wait on nothing else (a wave's loads
+    // complete in order)
+    int wt = tid;
+    if constexpr (PRO == PRO_COMBINE) {
+        const int busy = 8 * (nb < 32 ? nb : 32);  // threads with a block in phase 1 (MR == 1)
+        wt = (tid + GEMV_THREADS - (((busy + 63) & ~63) & (GEMV_THREADS - 1))) & (GEMV_THREADS - 1);
+    }
 
     const int ntiles = (N + rows - 1) / rows;
     const int tstride = (int)gridDim.x;
@@ -390,35 +417,84 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
     uint4 wv[ITEMS][NV], wn[ITEMS][NV];
     uint16_t dv[ITEMS], dn[ITEMS];
     constexpr int RW = GLU ? 2 : 1;  // weight rows per output
+    // GEMV_ONE: the weight loads are unconditional buffer loads, one
+    // descriptor per plane over the tile's span; an item past the tile reads
+    // at an offset past the descriptor, which returns zero without a memory
+    // access. Otherwise they are plain loads of the items that exist.
+    constexpr uint32_t OOB = 0x80000000u;  // past every descriptor here (spans < 2^31 bytes)
+    constexpr int NT = 2;                  // cache policy: non-temporal, the weights are streamed once
     auto gload = [&](int tile, uint4 (*wr)[NV], uint16_t* dr) {
         const int64_t row0 = (int64_t)tile * rows;
         const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
         const int total = RW * nrows * nb;
-        const uint4* qbase = reinterpret_cast<const uint4*>(qs) + row0 * nb * NV;
-        const uint16_t* dbase = dw + row0 * nb;
+        if constexpr (ONE) {
+            // GLU: the tile's up rows sit N rows after its gate rows
+            const uint32_t span = (uint32_t)((GLU ? N + nrows : nrows) * nb);
+            const buf_rsrc rq = make_rsrc(qs + row0 * nb * (16 * NV), span * (16u * NV));
+            const buf_rsrc rd = make_rsrc(dw + row0 * nb, span * 2u);
 #pragma unroll
-        for (int it = 0; it < ITEMS; it++) {
-            int g = tid + it * GEMV_THREADS;
-            if (g < total) {
-                // GLU: items past the tile's gate rows are its up rows, N rows on
-                if (GLU && g >= nrows * nb) g += (N - nrows) * nb;
-                // streamed once: a non-temporal load keeps it from evicting x and the terms
+            for (int it = 0; it < ITEMS; it++) {
+                const int g0 = wt + it * GEMV_THREADS;
+                const int g = (GLU && g0 >= nrows * nb) ? g0 + (N - nrows) * nb : g0;
+                const bool on = g0 < total;
+                const uint32_t qo = on ? (uint32_t)g * (16u * NV) : OOB, dof = on ? (uint32_t)g * 2u : OOB;
+#if __HIP_DEVICE_COMPILE__
 #pragma unroll
-                for (int v = 0; v < NV; v++) {
-                    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(qbase + g * NV + v));
-                    wr[it][v] = make_uint4(t[0], t[1], t[2], t[3]);
+                for (int v = 0; v < NV; v++)
+                    wr[it][v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 16 * v, NT));
+                dr[it] = __builtin_amdgcn_raw_buffer_load_b16(rd, dof, 0, 0);
+#else
+                (void)rq, (void)rd, (void)qo, (void)dof;
+#endif
+            }
+        } else {
+            const uint4* qbase = reinterpret_cast<const uint4*>(qs) + row0 * nb * NV;
+            const uint16_t* dbase = dw + row0 * nb;
+#pragma unroll
+            for (int it = 0; it < ITEMS; it++) {
+                int g = wt + it * GEMV_THREADS;
+                if (g < total) {
+                    // GLU: items past the tile's gate rows are its up rows, N rows on
+                    if (GLU && g >= nrows * nb) g += (N - nrows) * nb;
+                    // streamed once: a non-temporal load keeps it from evicting x and the terms
+#pragma unroll
+                    for (int v = 0; v < NV; v++) {
+                        const u32x4 t =
+                            __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(qbase + g * NV + v));
+                        wr[it][v] = make_uint4(t[0], t[1], t[2], t[3]);
+                    }
+                    dr[it] = dbase[g];
                 }
-                dr[it] = dbase[g];
             }
         }
     };
     int tile = (int)blockIdx.x;
     float pre_add = 0.0f;
-    // the first tile's weight loads (and this thread's residual and bias for
-    // it), in flight during the activation work
+    // the first tile's weight loads (and this thread's residual or bias for
+    // it), in flight during the activation work; unconditional as gload's
+    // (the grid never exceeds the tile count, so the first tile exists)
+    // the bias or residual of this thread's first output of tile t (output
+    // o = tid), an unconditional buffer load: resid and bias are not
+    // combined, and with neither the descriptor is empty
+    [[maybe_unused]] auto load_add = [&](int t) -> float {
+        const int64_t row0 = (int64_t)t * rows;
+        const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
+        const int r = tid / MR, mr = tid - r * MR;
+        const float* src = bias ? bias : resid;
+        const buf_rsrc rb = make_rsrc(src, src ? (uint32_t)((bias ? 1 : MR) * N) * 4u : 0u);
+        const uint32_t off = tid < nrows * MR ? (uint32_t)((bias ? 0 : (int64_t)mr * N) + row0 + r) * 4u : OOB;
+#if __HIP_DEVICE_COMPILE__
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0));
+#else
+        (void)rb, (void)off;
+        return 0.0f;
+#endif
+    };
     auto first_loads = [&]() {
-        if (tile < ntiles) {
-            gload(tile, wv, dv);
+        gload(tile, wv, dv);
+        if constexpr (ONE) {
+            pre_add = load_add(tile);
+        } else {
             const int64_t row0 = (int64_t)tile * rows;
             const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
             if (tid < nrows * MR) {
@@ -435,9 +511,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
         const int nblk = MR * nb, npass = (nblk + 31) / 32;
         // a row that fits the registers is loaded before the weights, whose
         // loads would otherwise stand in front of it in the memory pipeline
-        // (the merge of the attention partials, PRO_COMBINE, is left behind
-        // them: it computes as it loads)
-        const bool early = PRO != PRO_COMBINE && npass <= HOLD;
+        // (the merge of the attention partials, PRO_COMBINE, after them: its
+        // waves hold no weight items)
+        (void)npass;
         float4 xv[HOLD], av[HOLD];  // the row, and the prologue's second operand
         int ns = 0;
         if constexpr (PRO == PRO_COMBINE) {
@@ -446,47 +522,80 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
             ns = (len + STEP_SPLIT - 1) / STEP_SPLIT;
             ns = ns < po.nsplit ? ns : po.nsplit;
         }
+        // PRO_COMBINE: row block blk merged over the splits. Every split's
+        // (m, l) and O piece is in flight at once, read before the length is
+        // known (splits past it are not used). The loads are unconditional --
+        // a split index past the launch's count reads the last split's row
+        // again, a block past the row's reads its last block, and neither is
+        // used -- so the compiler counts the loads in flight exactly.
+        auto merge_block = [&](int blk) -> float4 {
+            const int bc = blk < nblk ? blk : nblk - 1;
+            const int o32 = bc * QK + 4 * g8;  // MR == 1: the element offset in the row
+            const int h = o32 >> po.head_shift, d = o32 & ((1 << po.head_shift) - 1);
+            // one descriptor per plane: a lane's (head, column) is its vector
+            // offset and a split's row the scalar one
+            const uint32_t rows = (uint32_t)(K >> po.head_shift) * (uint32_t)po.nsplit;
+            const buf_rsrc rml = make_rsrc(po.part_ml, rows * 8u);
+            const buf_rsrc ro = make_rsrc(po.part_o, rows * (uint32_t)po.head_dim * 4u);
+            const uint32_t vml = (uint32_t)(h * po.nsplit) * 8u;
+            const uint32_t vo = ((uint32_t)(h * po.nsplit) * (uint32_t)po.head_dim + (uint32_t)d) * 4u;
+            u32x2 mlr[STEP_MAX_SPLITS] = {};
+            u32x4 orr[STEP_MAX_SPLITS] = {};
+#if __HIP_DEVICE_COMPILE__
+#pragma unroll
+            for (int sp = 0; sp < STEP_MAX_SPLITS; sp++) {
+                const uint32_t spc = (uint32_t)(sp < po.nsplit ? sp : po.nsplit - 1);
+                mlr[sp] = __builtin_amdgcn_raw_buffer_load_b64(rml, vml, spc * 8u, 0);
+            }
+#pragma unroll
+            for (int sp = 0; sp < STEP_MAX_SPLITS; sp++) {
+                const uint32_t spc = (uint32_t)(sp < po.nsplit ? sp : po.nsplit - 1);
+                orr[sp] = __builtin_amdgcn_raw_buffer_load_b128(ro, vo, spc * (uint32_t)po.head_dim * 4u, 0);
+            }
+#else
+            (void)rml, (void)ro, (void)vml, (void)vo;
+#endif
+            // every load issued before any result is used
+            __builtin_amdgcn_sched_barrier(0);
+            float2 ml[STEP_MAX_SPLITS];
+            float4 o4[STEP_MAX_SPLITS];
+#pragma unroll
+            for (int sp = 0; sp < STEP_MAX_SPLITS; sp++) {
+                ml[sp] = make_float2(__uint_as_float(mlr[sp][0]), __uint_as_float(mlr[sp][1]));
+                o4[sp] = make_float4(__uint_as_float(orr[sp][0]), __uint_as_float(orr[sp][1]),
+                                     __uint_as_float(orr[sp][2]), __uint_as_float(orr[sp][3]));
+            }
+            float mm = -INFINITY;
+#pragma unroll
+            for (int sp = 0; sp < STEP_MAX_SPLITS; sp++)
+                if (sp < ns) mm = fmaxf(mm, ml[sp].x);
+            const float mu = (mm == -INFINITY) ? 0.0f : mm;
+            float tl = 0.0f;
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int sp = 0; sp < STEP_MAX_SPLITS; sp++) {
+                if (sp < ns) {
+                    const float f = exp2f(ml[sp].x - mu);
+                    tl = tl + ml[sp].y * f;
+                    acc.x = acc.x + o4[sp].x * f;
+                    acc.y = acc.y + o4[sp].y * f;
+                    acc.z = acc.z + o4[sp].z * f;
+                    acc.w = acc.w + o4[sp].w * f;
+                }
+            }
+            return make_float4(acc.x / tl, acc.y / tl, acc.z / tl, acc.w / tl);
+        };
         auto load_passes = [&](int p0) {
 #pragma unroll
             for (int u = 0; u < HOLD; u++) {
                 const int blk = (p0 + u) * 32 + slot;
-                if (blk < nblk) {
+                if constexpr (PRO == PRO_COMBINE) {
+                    // waves with no block of the row skip it
+                    if (__builtin_amdgcn_readfirstlane(blk) < nblk) xv[u] = merge_block(blk);
+                } else if (blk < nblk) {
                     const int mr = blk / nb, b = blk - mr * nb;
                     const int64_t off = (int64_t)mr * K + b * QK + 4 * g8;
-                    if constexpr (PRO == PRO_COMBINE) {
-                        // every split's (m, l) and O piece in flight at once, read
-                        // before the length is known; splits past it are not used
-                        const int h = (int)(off / po.head_dim), d = (int)(off - (int64_t)h * po.head_dim);
-                        float2 ml[STEP_MAX_SPLITS];
-                        float4 o4[STEP_MAX_SPLITS];
-#pragma unroll
-                        for (int sp = 0; sp < STEP_MAX_SPLITS; sp++) {
-                            if (sp < po.nsplit) {
-                                const int64_t prow = (int64_t)h * po.nsplit + sp;
-                                ml[sp] = po.part_ml[prow];
-                                o4[sp] = *reinterpret_cast<const float4*>(po.part_o + prow * po.head_dim + d);
-                            }
-                        }
-                        float mm = -INFINITY;
-#pragma unroll
-                        for (int sp = 0; sp < STEP_MAX_SPLITS; sp++)
-                            if (sp < ns) mm = fmaxf(mm, ml[sp].x);
-                        const float mu = (mm == -INFINITY) ? 0.0f : mm;
-                        float tl = 0.0f;
-                        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                        for (int sp = 0; sp < STEP_MAX_SPLITS; sp++) {
-                            if (sp < ns) {
-                                const float f = exp2f(ml[sp].x - mu);
-                                tl = tl + ml[sp].y * f;
-                                acc.x = acc.x + o4[sp].x * f;
-                                acc.y = acc.y + o4[sp].y * f;
-                                acc.z = acc.z + o4[sp].z * f;
-                                acc.w = acc.w + o4[sp].w * f;
-                            }
-                        }
-                        xv[u] = make_float4(acc.x / tl, acc.y / tl, acc.z / tl, acc.w / tl);
-                    } else if constexpr (sizeof(XT) == 4) {
+                    if constexpr (sizeof(XT) == 4) {
                         xv[u] = *reinterpret_cast<const float4*>(x + off);
                     } else {
                         const uint2 h = *reinterpret_cast<const uint2*>(x + off);
@@ -499,29 +608,27 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                 }
             }
         };
-        if (early) load_passes(0);
-        first_loads();
-        float r = 0.0f;
-        if constexpr (PRO == PRO_RMSNORM) {
-            float ss = 0.0f;
-            for (int p0 = 0; p0 < npass; p0 += HOLD) {
-                if (!early) load_passes(p0);
+        if constexpr (PRO == PRO_COMBINE) {
+            first_loads();
+            if constexpr (HELD) load_passes(0);
+        } else {
+            if constexpr (HELD) load_passes(0);
+            first_loads();
+        }
+        // thread t's squares in order (k_rmsnorm's), over the passes held in xv
+        auto ss_pass = [&](int p0, float& ss) {
 #pragma unroll
-                for (int u = 0; u < HOLD; u++) {
-                    if ((p0 + u) * 32 + slot < nblk) {
-                        ss = ss + xv[u].x * xv[u].x;
-                        ss = ss + xv[u].y * xv[u].y;
-                        ss = ss + xv[u].z * xv[u].z;
-                        ss = ss + xv[u].w * xv[u].w;
-                    }
+            for (int u = 0; u < HOLD; u++) {
+                if ((p0 + u) * 32 + slot < nblk) {
+                    ss = ss + xv[u].x * xv[u].x;
+                    ss = ss + xv[u].y * xv[u].y;
+                    ss = ss + xv[u].z * xv[u].z;
+                    ss = ss + xv[u].w * xv[u].w;
                 }
             }
-            r = rms_scale(block_sum256(ss, red), K, po.eps);
-        }
+        };
         int8_t* xb = reinterpret_cast<int8_t*>(xq);
-        for (int p0 = 0; p0 < npass; p0 += HOLD) {
-            // a row of up to HOLD passes is already held
-            if (!early) load_passes(p0);
+        auto q8_pass = [&](int p0, float r) {
 #pragma unroll
             for (int u = 0; u < HOLD; u++) {
                 const int blk = (p0 + u) * 32 + slot;
@@ -555,6 +662,31 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                     }
                 }
             }
+        };
+        if constexpr (HELD) {
+            // the held row in straight-line code: the waits for the row count
+            // only the loads issued after it
+            float r = 0.0f;
+            if constexpr (PRO == PRO_RMSNORM) {
+                float ss = 0.0f;
+                ss_pass(0, ss);
+                r = rms_scale(block_sum256(ss, red), K, po.eps);
+            }
+            q8_pass(0, r);
+        } else {
+            float r = 0.0f;
+            if constexpr (PRO == PRO_RMSNORM) {
+                float ss = 0.0f;
+                for (int p0 = 0; p0 < npass; p0 += HOLD) {
+                    load_passes(p0);
+                    ss_pass(p0, ss);
+                }
+                r = rms_scale(block_sum256(ss, red), K, po.eps);
+            }
+            for (int p0 = 0; p0 < npass; p0 += HOLD) {
+                load_passes(p0);
+                q8_pass(p0, r);
+            }
         }
     }
     __syncthreads();
@@ -565,15 +697,17 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
     float best_v = -INFINITY;  // ARG: this thread's best output so far
     int best_i = INT32_MAX;    // loses every tie against a real output
     for (int buf = 0; tile < ntiles; tile += tstride, buf ^= 1) {
-        const int next = tile + tstride;
-        if (next < ntiles) gload(next, wn, dn);
+        // GEMV_ONE: this is the workgroup's only tile
+        if constexpr (!ONE) {
+            if (tile + tstride < ntiles) gload(tile + tstride, wn, dn);
+        }
         const int64_t row0 = (int64_t)tile * rows;
         const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
         const int total = RW * nrows * nb;
         float* tb = terms + buf * RW * rows * MR * nbp;
 #pragma unroll
         for (int it = 0; it < ITEMS; it++) {
-            const int g = tid + it * GEMV_THREADS;
+            const int g = wt + it * GEMV_THREADS;
             if (g < total) {
                 const int r = g / nb, b = g - r * nb;
                 const float dwf = f16_bits_hw(dv[it]);
@@ -619,11 +753,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
             for (; b < nb; b++) acc = acc + tr[b];
             return acc;
         };
-        for (int o = tid; o < nrows * MR; o += GEMV_THREADS) {
+        auto out_row = [&](int o, float add) {
             const int r = o / MR, mr = o - r * MR;
             const int64_t n = row0 + r;
-            float add = pre_add;
-            if (tile != (int)blockIdx.x || o != tid) add = bias ? bias[n] : resid ? resid[(int64_t)mr * N + n] : 0.0f;
             float acc = ordered_sum(tb + (r * MR + mr) * nbp);
             if constexpr (GLU) {
                 // silu(gate) * up, tn_silu_mul's arithmetic
@@ -641,7 +773,27 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                 reinterpret_cast<uint16_t*>(y)[(int64_t)mr * N + n] = bf16_from_f32(acc);
             else
                 reinterpret_cast<float*>(y)[(int64_t)mr * N + n] = acc;
+        };
+        if constexpr (ONE) {
+            // the thread's first output outside the loop: its add was loaded
+            // unconditionally, before the weights, and its wait counts them out
+            if (tid < nrows * MR) out_row(tid, pre_add);
+            for (int o = tid + GEMV_THREADS; o < nrows * MR; o += GEMV_THREADS) {
+                const int r = o / MR, mr = o - r * MR;
+                const int64_t n = row0 + r;
+                out_row(o, bias ? bias[n] : resid ? resid[(int64_t)mr * N + n] : 0.0f);
+            }
+        } else {
+            for (int o = tid; o < nrows * MR; o += GEMV_THREADS) {
+                const int r = o / MR, mr = o - r * MR;
+                const int64_t n = row0 + r;
+                float add = pre_add;
+                if (tile != (int)blockIdx.x || o != tid)
+                    add = bias ? bias[n] : resid ? resid[(int64_t)mr * N + n] : 0.0f;
+                out_row(o, add);
+            }
         }
+        if constexpr (ONE) break;  // the launch gives every workgroup one tile
 #pragma unroll
         for (int it = 0; it < ITEMS; it++) {
 #pragma unroll
@@ -1271,15 +1423,36 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     const int64_t ntiles = cdiv(N, rows);
     // persistent: exactly as many workgroups as the device holds at once (a
     // workgroup that had to wait for a slot would start its whole share of
-    // tiles late)
-    int resident = 0;
-    tn_status s = resident_workgroups(reinterpret_cast<const void*>(&k_gemv<FMT, MR, XT, PRO, ARG, GLU>), GEMV_THREADS,
-                                      lds, &resident);
+    // tiles late). SHAPE: the activation rows held in registers (k_gemv's
+    // HOLD passes of 32 blocks), and GEMV_ONE when the resident workgroups
+    // cover the tiles and its buffer descriptors (a tile's weight span, GLU:
+    // N + rows rows; the bias or residual rows) stay below 2^31 bytes
+    const bool held = MR * nb <= 32 * (PRO == PRO_COMBINE ? 1 : GEMV_HOLD);
+    const bool spans = (int64_t)(GLU ? N + rows : rows) * nb * Fmt<FMT>::CODE_BYTES < (int64_t(1) << 31) &&
+                       (int64_t)MR * N * 4 < (int64_t(1) << 31);
+    auto kern_of = [](int shape) -> const void* {
+        return shape == GEMV_ONE      ? reinterpret_cast<const void*>(&k_gemv<FMT, MR, XT, PRO, ARG, GLU, GEMV_ONE>)
+               : shape == GEMV_STREAM ? reinterpret_cast<const void*>(&k_gemv<FMT, MR, XT, PRO, ARG, GLU, GEMV_STREAM>)
+                                      : reinterpret_cast<const void*>(&k_gemv<FMT, MR, XT, PRO, ARG, GLU, GEMV_PASSES>);
+    };
+    const int64_t cap = ARG ? GEMV_ARG_MAX_PARTS : INT32_MAX;
+    int shape = held ? GEMV_ONE : GEMV_PASSES, resident = 0;
+    tn_status s = resident_workgroups(kern_of(shape), GEMV_THREADS, lds, &resident);
     if (s != TN_OK) return s;
+    if (shape == GEMV_ONE && (ntiles > resident || ntiles > cap || !spans)) {
+        shape = GEMV_STREAM;
+        s = resident_workgroups(kern_of(shape), GEMV_THREADS, lds, &resident);
+        if (s != TN_OK) return s;
+    }
     unsigned grid = (unsigned)(ntiles < resident ? ntiles : resident);
-    if (ARG && grid > (unsigned)GEMV_ARG_MAX_PARTS) grid = (unsigned)GEMV_ARG_MAX_PARTS;
-    hipLaunchKernelGGL((k_gemv<FMT, MR, XT, PRO, ARG, GLU>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, dw, N,
-                       rows, bias, resid, y, y_bf16, po);
+    if (grid > (unsigned)cap) grid = (unsigned)cap;
+#define TN_GEMV(SH)                                                                                                   \
+    hipLaunchKernelGGL((k_gemv<FMT, MR, XT, PRO, ARG, GLU, SH>), dim3(grid), dim3(GEMV_THREADS), lds, st, x, K, nb, qs, \
+                       dw, N, rows, bias, resid, y, y_bf16, po)
+    if (shape == GEMV_ONE) TN_GEMV(GEMV_ONE);
+    else if (shape == GEMV_STREAM) TN_GEMV(GEMV_STREAM);
+    else TN_GEMV(GEMV_PASSES);
+#undef TN_GEMV
     TN_LAUNCHED();
     if (grid_out) *grid_out = grid;
     return TN_OK;
@@ -1446,7 +1619,8 @@ tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, cons
             break;
         case PRO_SILU: s = launch_gemv<FMT_Q4_0, 1, float, PRO_SILU>(st, x, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po); break;
         case PRO_COMBINE:
-            if (po.head_dim < 4 || po.head_dim % 4 != 0 || k % po.head_dim != 0 || po.nsplit < 1 ||
+            // head_dim a power of two (the merge addresses by shifts), at least a 4-column piece
+            if (po.head_dim < 4 || po.head_dim != (1 << po.head_shift) || k % po.head_dim != 0 || po.nsplit < 1 ||
                 po.nsplit > STEP_MAX_SPLITS || !po.part_o || !po.part_ml || !po.len)
                 return fail(TN_EINVAL, "linear_decode: bad attention partials");
             s = launch_gemv<FMT_Q4_0, 1, float, PRO_COMBINE>(st, po.part_o, (int)k, qs, d, (int)n, nullptr, y, 0, resid, po);

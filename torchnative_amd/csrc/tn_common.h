@@ -289,6 +289,7 @@ struct GemvPro {
     const float2* part_ml = nullptr;
     const int32_t* len = nullptr;
     int nsplit = 0, head_dim = 0, cap = 0;
+    int head_shift = 0;  // log2(head_dim): head_dim is a power of two
     // argmax epilogue (linear_decode_argmax): every workgroup's best (value,
     // index) of y goes to arg_v/arg_i[workgroup] (GEMV_ARG_MAX_PARTS
     // entries); a one-workgroup launch then reduces them and advances the
