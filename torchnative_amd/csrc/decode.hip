@@ -132,7 +132,10 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
     constexpr int SLOTS = 256 / TPK;       // rows per load instruction of the workgroup
     constexpr int U = STEP_SPLIT / SLOTS;  // rows per lane
     static_assert(U * SLOTS == STEP_SPLIT && (TPK == 16 || TPK == 32), "shape");
-    __shared__ __align__(16) float sq[NR][D];
+    // the rotated query heads [NR][D], then two words per thread where idle
+    // threads store (the rotation has no branch for the compiler to sink the
+    // query loads into, behind the cache rows)
+    __shared__ __align__(16) float sq[NR * D + 2 * 256];
     __shared__ __align__(16) float snew[2][D];  // the new key (rotated) and value
     __shared__ float smax[NR][4], ssum[NR][4];
     __shared__ float4 so[4][NR][TPK];
@@ -140,46 +143,47 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
     const int c = tid % TPK, kl = tid / TPK;
     const int sp = blockIdx.x, kvh = blockIdx.y;
     const int k0 = sp * STEP_SPLIT;
-    // the split's rows below cap go out before the position is known (rows at
-    // or past the position are replaced or masked below), so the cache reads
-    // and the read of the position overlap
-    const float4* kp = reinterpret_cast<const float4*>(kc + (int64_t)kvh * cap * D);
-    const float4* vp = reinterpret_cast<const float4*>(vc + (int64_t)kvh * cap * D);
+    // Every load is an unconditional buffer load (an idle lane's offset lies
+    // past its descriptor and reads zero), so the compiler counts the loads
+    // in flight exactly. The rotation's operands go first -- thread i <
+    // NR * D/2 rotates pair i of the query heads, thread i < D/2 also pair i
+    // of the new key -- then the split's K and V rows below cap, before the
+    // position is known (rows at or past it are replaced or masked where
+    // they are used), so that the rotation waits only for its own operands
+    // while the cache rows are in flight.
+    constexpr int half = D / 2;
+    constexpr int QP = (NR * half + 255) / 256;  // query pairs per thread
+    const buf_rsrc rq = make_rsrc(qkv + (int64_t)kvh * NR * D, (uint32_t)(NR * D * 4));
+    const buf_rsrc rkn = make_rsrc(qkv + (int64_t)(hq + kvh) * D, (uint32_t)(D * 4));
+    const buf_rsrc rvn = make_rsrc(qkv + (int64_t)(hq + hkv + kvh) * D, (uint32_t)(D * 4));
+    const buf_rsrc rrope = make_rsrc(rope, (uint32_t)(half * 8));
+    float qx1[QP], qx2[QP];
+    float2 qcs[QP];
+#pragma unroll
+    for (int i = 0; i < QP; i++) {
+        const int pi = tid + 256 * i;
+        const int hh = pi / half, j = pi - hh * half;
+        const bool on = pi < NR * half;
+        qx1[i] = buf_load_f(rq, on ? (uint32_t)(hh * D + j) * 4u : BUF_OOB);
+        qx2[i] = buf_load_f(rq, on ? (uint32_t)(hh * D + j + half) * 4u : BUF_OOB);
+        qcs[i] = buf_load_f2(rrope, on ? (uint32_t)j * 8u : BUF_OOB);
+    }
+    const bool kon = tid < half;
+    const float kx1 = buf_load_f(rkn, kon ? (uint32_t)tid * 4u : BUF_OOB);
+    const float kx2 = buf_load_f(rkn, kon ? (uint32_t)(tid + half) * 4u : BUF_OOB);
+    const float kvv1 = buf_load_f(rvn, kon ? (uint32_t)tid * 4u : BUF_OOB);
+    const float kvv2 = buf_load_f(rvn, kon ? (uint32_t)(tid + half) * 4u : BUF_OOB);
+    const float2 kcs = buf_load_f2(rrope, kon ? (uint32_t)tid * 8u : BUF_OOB);
+    const buf_rsrc rk = make_rsrc(kc + (int64_t)kvh * cap * D, (uint32_t)cap * (uint32_t)(D * 4));
+    const buf_rsrc rv = make_rsrc(vc + (int64_t)kvh * cap * D, (uint32_t)cap * (uint32_t)(D * 4));
     const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 kr[U], vr[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const int t = k0 + u * SLOTS + kl;
-        kr[u] = t < cap ? kp[(int64_t)t * TPK + c] : zero;
-        vr[u] = t < cap ? vp[(int64_t)t * TPK + c] : zero;
-    }
-    // the rotation's operands too: thread i < NR * D/2 rotates pair i of the
-    // query heads, thread i < D/2 also pair i of the new key
-    constexpr int half = D / 2;
-    constexpr int QP = (NR * half + 255) / 256;  // query pairs per thread
-    float qx1[QP], qx2[QP], kx1 = 0.f, kx2 = 0.f, kvv1 = 0.f, kvv2 = 0.f;
-    float2 qcs[QP], kcs = make_float2(1.f, 0.f);
-#pragma unroll
-    for (int i = 0; i < QP; i++) {
-        const int pi = tid + 256 * i;
-        qx1[i] = qx2[i] = 0.0f;
-        qcs[i] = make_float2(1.f, 0.f);
-        if (pi < NR * half) {
-            const int hh = pi / half, j = pi - hh * half;
-            const float* xr = qkv + (int64_t)(kvh * NR + hh) * D;
-            qx1[i] = xr[j];
-            qx2[i] = xr[j + half];
-            qcs[i] = rope[j];
-        }
-    }
-    if (tid < half) {
-        const float* xk = qkv + (int64_t)(hq + kvh) * D;
-        const float* xv = qkv + (int64_t)(hq + hkv + kvh) * D;
-        kx1 = xk[tid];
-        kx2 = xk[tid + half];
-        kvv1 = xv[tid];
-        kvv2 = xv[tid + half];
-        kcs = rope[tid];
+        const uint32_t off = t < cap ? (uint32_t)(t * D + 4 * c) * 4u : BUF_OOB;
+        kr[u] = buf_load_f4(rk, off);
+        vr[u] = buf_load_f4(rv, off);
     }
     const int pos = state[0];
     const int len = pos < 0 ? 0 : (pos + 1 < cap ? pos + 1 : cap);
@@ -187,26 +191,16 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
     const int ncached = pos < len ? pos : len;  // rows taken from the caches
     const bool fresh = pos >= k0 && pos < k0 + STEP_SPLIT && pos < len;
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-        // rows past the cached ones hold stale or unwritten values: zero them
-        // (a NaN there would survive a zero probability)
-        if (k0 + u * SLOTS + kl >= ncached) {
-            kr[u] = zero;
-            vr[u] = zero;
-        }
-    }
-#pragma unroll
     for (int i = 0; i < QP; i++) {
         const int pi = tid + 256 * i;
-        if (pi < NR * half) {
-            const int hh = pi / half, j = pi - hh * half;
-            const float cs = qcs[i].x, sn = qcs[i].y;
-            const float x1 = qx1[i], x2 = qx2[i];
-            sq[hh][j] = x1 * cs + (-x2) * sn;
-            sq[hh][j + half] = x2 * cs + x1 * sn;
-        }
+        const int hh = pi / half, j = pi - hh * half;
+        const bool on = pi < NR * half;
+        const float cs = qcs[i].x, sn = qcs[i].y;
+        const float x1 = qx1[i], x2 = qx2[i];
+        sq[on ? hh * D + j : NR * D + 2 * tid] = x1 * cs + (-x2) * sn;
+        sq[on ? hh * D + j + half : NR * D + 2 * tid + 1] = x2 * cs + x1 * sn;
     }
-    if (fresh && tid < half) {
+    if (fresh && kon) {
         const float cs = kcs.x, sn = kcs.y;
         const float x1 = kx1, x2 = kx2;
         const float y1 = x1 * cs + (-x2) * sn, y2 = x2 * cs + x1 * sn;
@@ -223,18 +217,23 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
         vd[tid + half] = v2;
     }
     __syncthreads();
-    if (fresh) {
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (k0 + u * SLOTS + kl == pos) {
-                kr[u] = reinterpret_cast<const float4*>(snew[0])[c];
-                vr[u] = reinterpret_cast<const float4*>(snew[1])[c];
-            }
+    for (int u = 0; u < U; u++) {
+        // the new row from LDS; rows past the cached ones hold stale or
+        // unwritten values: zero them (a NaN there would survive a zero
+        // probability)
+        const int t = k0 + u * SLOTS + kl;
+        if (fresh && t == pos) {
+            kr[u] = reinterpret_cast<const float4*>(snew[0])[c];
+            vr[u] = reinterpret_cast<const float4*>(snew[1])[c];
+        } else if (t >= ncached) {
+            kr[u] = zero;
+            vr[u] = zero;
         }
     }
     float4 qv[NR];
 #pragma unroll
-    for (int hh = 0; hh < NR; hh++) qv[hh] = reinterpret_cast<const float4*>(sq[hh])[c];
+    for (int hh = 0; hh < NR; hh++) qv[hh] = reinterpret_cast<const float4*>(sq + hh * D)[c];
 
     // scores (log2 units), then the split's max per head
     float sc[NR][U];

@@ -101,6 +101,43 @@ __device__ inline buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
 #endif
 }
 
+// Unconditional loads through a descriptor: an offset at or past its end
+// reads zero without a memory access, so a kernel can issue the same loads
+// on every path and the compiler counts the loads in flight exactly (a load
+// behind a branch makes every later wait on an older load a full wait).
+template <int AUX = 0>  // cache policy bits
+__device__ inline float4 buf_load_f4(buf_rsrc r, uint32_t off) {
+#if __HIP_DEVICE_COMPILE__
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const u4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+#else
+    (void)r, (void)off;
+    return float4{};
+#endif
+}
+template <int AUX = 0>  // cache policy bits
+__device__ inline float2 buf_load_f2(buf_rsrc r, uint32_t off) {
+#if __HIP_DEVICE_COMPILE__
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    const u2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, AUX);
+    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+#else
+    (void)r, (void)off;
+    return float2{};
+#endif
+}
+template <int AUX = 0>  // cache policy bits
+__device__ inline float buf_load_f(buf_rsrc r, uint32_t off) {
+#if __HIP_DEVICE_COMPILE__
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX));
+#else
+    (void)r, (void)off;
+    return 0.0f;
+#endif
+}
+constexpr uint32_t BUF_OOB = 0x80000000u;  // an offset past every descriptor of under 2^31 bytes
+
 // ---- reduced floats (exact, identical on host and device) ---------------
 
 // f32 -> f16 round-to-nearest-even with subnormals and overflow to inf: the
