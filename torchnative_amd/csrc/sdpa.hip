@@ -1556,22 +1556,29 @@ __global__ __launch_bounds__(D) void k_decode_sk_combine(const float* __restrict
         w_lo = ((u0 + 1) * W + T - 1) / T - 1;
         w_hi = ((u0 + n) * W + T - 1) / T - 1;
     }
-    // batches of CB partials, every load of a batch in flight at once; the
-    // running sums are rescaled when a batch raises the maximum
+    // batches of CB partials, every load of a batch in flight at once, as
+    // unconditional buffer loads (a slot past the segment's last wave reads
+    // zero: no memory access, and the compiler counts the loads exactly);
+    // the running sums are rescaled when a batch raises the maximum. The
+    // first batch (all of them at C4's shapes) is outside the loop, so its
+    // waits count only its own loads.
     constexpr int CB = 32;
-    for (int64_t w0 = w_lo; w0 <= w_hi; w0 += CB) {
+    const buf_rsrc rml = make_rsrc(part_ml, 0x7fffffffu), ro = make_rsrc(part_o, 0x7fffffffu);
+    auto batch = [&](int64_t w0) __attribute__((always_inline)) {
         float2 ml[CB];
         float ov[CB];
 #pragma unroll
         for (int i = 0; i < CB; i++) {
-            ml[i] = make_float2(-INFINITY, 0.0f);
-            ov[i] = 0.0f;
-            if (w0 + i <= w_hi) {
-                const int64_t sl = (slot0 + w0 + i) * NR + hh;
-                ml[i] = part_ml[sl];
-                ov[i] = part_o[sl * D + d];
-            }
+            const int64_t sl = (slot0 + w0 + i) * NR + hh;
+            const bool on = w0 + i <= w_hi;
+            ml[i] = buf_load_f2(rml, on ? (uint32_t)(sl * 8) : BUF_OOB);
+            ov[i] = buf_load_f(ro, on ? (uint32_t)((sl * D + d) * 4) : BUF_OOB);
         }
+        __builtin_amdgcn_sched_barrier(0);  // every load issued before any result is used
+        // absent partials read (0, 0): their m is taken as -inf
+#pragma unroll
+        for (int i = 0; i < CB; i++)
+            if (w0 + i > w_hi) ml[i].x = -INFINITY;
         float bm = mm;
 #pragma unroll
         for (int i = 0; i < CB; i++) bm = fmaxf(bm, ml[i].x);
@@ -1583,12 +1590,14 @@ __global__ __launch_bounds__(D) void k_decode_sk_combine(const float* __restrict
         }
 #pragma unroll
         for (int i = 0; i < CB; i++) {
-            const float f = exp2f(ml[i].x - mu);  // 0 for the padding entries
+            const float f = exp2f(ml[i].x - mu);  // 0 for the absent entries
             tl = tl + ml[i].y * f;
             acc = acc + ov[i] * f;
         }
         mm = bm;
-    }
+    };
+    if (w_lo <= w_hi) batch(w_lo);
+    for (int64_t w0 = w_lo + CB; w0 <= w_hi; w0 += CB) batch(w0);
     const float mu = (mm == -INFINITY) ? 0.0f : mm;
     if constexpr (std::is_same<OT, _Float16>::value)
         reinterpret_cast<uint16_t*>(out)[((int64_t)b * Hq + h) * D + d] = f16_from_f32(acc / tl);
