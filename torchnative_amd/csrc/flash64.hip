@@ -179,12 +179,18 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
         f32x16 acc;
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+        // the tile's K fragments all read before the products: interleaved
+        // with them by the compiler, two reads at a time, the LDS latency was
+        // exposed twice per tile (the same for V below)
+        V8 ka[D / 16];
 #pragma unroll
         for (int c = 0; c < D / 16; c++) {
             const int row = kr + lq;
-            const V8 ka = *reinterpret_cast<const V8*>(tK + row * D + swz(row, 2 * c + hh) * 8);
-            acc = E::mfma(ka, qf[c], acc);
+            ka[c] = *reinterpret_cast<const V8*>(tK + row * D + swz(row, 2 * c + hh) * 8);
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < D / 16; c++) acc = E::mfma(ka[c], qf[c], acc);
         // The scores are read by VALU next. A VALU read of a 16-pass XDL
         // result needs 18 wait states; they are spelled out, tied to the
         // accumulator, so that no read is scheduled above them (the
@@ -266,6 +272,7 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
             pf[j] = __builtin_bit_cast(
                 V8, make_uint4(E::pack_p(p[8 * j], p[8 * j + 1]), E::pack_p(p[8 * j + 2], p[8 * j + 3]),
                                E::pack_p(p[8 * j + 4], p[8 * j + 5]), E::pack_p(p[8 * j + 6], p[8 * j + 7])));
+        V8 vf[D / 32][2];
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
@@ -275,8 +282,13 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
                 const int col = 32 * dt + dcol;
                 const uint2 lo = lds_read_tr16(tV + r0 * D + swz(r0, col >> 3) * 8 + (col & 7));
                 const uint2 hi = lds_read_tr16(tV + r1 * D + swz(r1, col >> 3) * 8 + (col & 7));
-                o[dt] = E::mfma(__builtin_bit_cast(V8, make_uint4(lo.x, lo.y, hi.x, hi.y)), pf[j], o[dt]);
+                vf[dt][j] = __builtin_bit_cast(V8, make_uint4(lo.x, lo.y, hi.x, hi.y));
             }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) o[dt] = E::mfma(vf[dt][j], pf[j], o[dt]);
     };
     // the ring unrolled so that every stage index is a constant
     for (int st = 0; st < nst; st += 2) {
