@@ -381,21 +381,29 @@ __global__ __launch_bounds__(QG_THREADS) void k_gemv_qk(const XT* __restrict__ x
     __syncthreads();
 
     // phases 2 and 3, persistent over row tiles with the next tile's bytes in flight
+    // The super-block loads are unconditional buffer loads over the tile's
+    // bytes (a thread past the tile, or a tile past the last, reads at an
+    // offset past the descriptor: zero, no memory access), so the compiler
+    // counts the loads in flight exactly and the waits for this tile's item
+    // leave the next tile's in flight. Behind a branch, every wait on the
+    // current item also waited for the whole prefetch.
     uint4 wv[9], wn[9];
     auto gload = [&](int tile, uint4* dst) {
-        const int64_t row0 = (int64_t)tile * rows;
-        const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
-        if (tid < nrows * nsb) {
-            const uint4* src = reinterpret_cast<const uint4*>(w + (row0 * nsb + tid) * QK4K_BYTES);
+        const bool live = tile < ntiles;
+        const int64_t row0 = live ? (int64_t)tile * rows : 0;
+        const int nrows = live ? (int)((N - row0) < rows ? (N - row0) : rows) : 0;
+        const buf_rsrc rw = make_rsrc(w + row0 * nsb * QK4K_BYTES, (uint32_t)(nrows * nsb) * QK4K_BYTES);
+        const uint32_t off = tid < nrows * nsb ? (uint32_t)tid * QK4K_BYTES : BUF_OOB;
 #pragma unroll
-            for (int i = 0; i < 9; i++) dst[i] = src[i];
+        for (int i = 0; i < 9; i++) {
+            const float4 f = buf_load_f4(rw, off + 16u * i);
+            dst[i] = make_uint4(__float_as_uint(f.x), __float_as_uint(f.y), __float_as_uint(f.z), __float_as_uint(f.w));
         }
     };
     int tile = (int)blockIdx.x;
-    if (tile < ntiles) gload(tile, wv);
+    gload(tile, wv);  // the grid never exceeds the tile count
     for (int buf = 0; tile < ntiles; tile += (int)gridDim.x, buf ^= 1) {
-        const int next = tile + (int)gridDim.x;
-        if (next < ntiles) gload(next, wn);
+        gload(tile + (int)gridDim.x, wn);
         const int64_t row0 = (int64_t)tile * rows;
         const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
         float* tb = terms + (size_t)buf * rows * MR * nsb * QG_TERMS;
