@@ -491,10 +491,11 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
 #endif
     };
     auto first_loads = [&]() {
-        gload(tile, wv, dv);
         if constexpr (ONE) {
+            gload(tile, wv, dv);
             pre_add = load_add(tile);
-        } else {
+        } else if (tile < ntiles) {  // always true; the branch keeps this shape at 64 VGPRs (66 without)
+            gload(tile, wv, dv);
             const int64_t row0 = (int64_t)tile * rows;
             const int nrows = (int)((N - row0) < rows ? (N - row0) : rows);
             if (tid < nrows * MR) {
