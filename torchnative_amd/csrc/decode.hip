@@ -136,7 +136,9 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
     // threads store (the rotation has no branch for the compiler to sink the
     // query loads into, behind the cache rows)
     __shared__ __align__(16) float sq[NR * D + 2 * 256];
-    __shared__ __align__(16) float snew[2][D];  // the new key (rotated) and value
+    // the new key (rotated) and value [2][D], then four words per thread where
+    // the other threads store (as sq's padding)
+    __shared__ __align__(16) float snew[2 * D + 4 * 256];
     __shared__ float smax[NR][4], ssum[NR][4];
     __shared__ float4 so[4][NR][TPK];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -150,7 +152,10 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
     // of the new key -- then the split's K and V rows below cap, before the
     // position is known (rows at or past it are replaced or masked where
     // they are used), so that the rotation waits only for its own operands
-    // while the cache rows are in flight.
+    // while the cache rows are in flight. A split past the length runs
+    // through with every row masked (its partial is never merged): an early
+    // exit there let the compiler sink every load below the position's
+    // read, so that all of them waited for it.
     constexpr int half = D / 2;
     constexpr int QP = (NR * half + 255) / 256;  // query pairs per thread
     const buf_rsrc rq = make_rsrc(qkv + (int64_t)kvh * NR * D, (uint32_t)(NR * D * 4));
@@ -185,9 +190,9 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
         kr[u] = buf_load_f4(rk, off);
         vr[u] = buf_load_f4(rv, off);
     }
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the rotation waits for its operands
     const int pos = state[0];
     const int len = pos < 0 ? 0 : (pos + 1 < cap ? pos + 1 : cap);
-    if (k0 >= len) return;  // uniform over the workgroup
     const int ncached = pos < len ? pos : len;  // rows taken from the caches
     const bool fresh = pos >= k0 && pos < k0 + STEP_SPLIT && pos < len;
 #pragma unroll
@@ -200,15 +205,16 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
         sq[on ? hh * D + j : NR * D + 2 * tid] = x1 * cs + (-x2) * sn;
         sq[on ? hh * D + j + half : NR * D + 2 * tid + 1] = x2 * cs + x1 * sn;
     }
+    // the new key's rotation in every split, without a branch (only the
+    // fresh split reads it back; behind a branch its loads were sunk there,
+    // after the cache rows)
+    const float ny1 = kx1 * kcs.x + (-kx2) * kcs.y, ny2 = kx2 * kcs.x + kx1 * kcs.y;
+    snew[kon ? tid : 2 * D + 4 * tid] = ny1;
+    snew[kon ? tid + half : 2 * D + 4 * tid + 1] = ny2;
+    snew[kon ? D + tid : 2 * D + 4 * tid + 2] = kvv1;
+    snew[kon ? D + tid + half : 2 * D + 4 * tid + 3] = kvv2;
     if (fresh && kon) {
-        const float cs = kcs.x, sn = kcs.y;
-        const float x1 = kx1, x2 = kx2;
-        const float y1 = x1 * cs + (-x2) * sn, y2 = x2 * cs + x1 * sn;
-        const float v1 = kvv1, v2 = kvv2;
-        snew[0][tid] = y1;
-        snew[0][tid + half] = y2;
-        snew[1][tid] = v1;
-        snew[1][tid + half] = v2;
+        const float y1 = ny1, y2 = ny2, v1 = kvv1, v2 = kvv2;
         float* kd = kc + ((int64_t)kvh * cap + pos) * D;
         float* vd = vc + ((int64_t)kvh * cap + pos) * D;
         kd[tid] = y1;
@@ -224,8 +230,8 @@ __global__ __launch_bounds__(256) void k_step_attn(const float* __restrict__ qkv
         // probability)
         const int t = k0 + u * SLOTS + kl;
         if (fresh && t == pos) {
-            kr[u] = reinterpret_cast<const float4*>(snew[0])[c];
-            vr[u] = reinterpret_cast<const float4*>(snew[1])[c];
+            kr[u] = reinterpret_cast<const float4*>(snew)[c];
+            vr[u] = reinterpret_cast<const float4*>(snew + D)[c];
         } else if (t >= ncached) {
             kr[u] = zero;
             vr[u] = zero;
