@@ -261,7 +261,7 @@ __device__ inline int dot_block_q8(const uint4& w0, const uint4& w1, const int* 
 //   PRO_RMSNORM  x -> w * (x * r), r = 1/sqrt(sum(x^2)/K + eps)
 //   PRO_SILU     x holds [gate | up] (2K floats) -> gate/(1 + exp(-gate)) * up
 //   PRO_COMBINE  the row is the attention output h * D + d, merged from the
-//                split partials: sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)
+//                split partials: sum_s O_s 2^(m_s - M) * (1 / sum_s l_s 2^(m_s - M))
 // Epilogue: y = acc (+ bias, or + resid: never both); y may alias resid (each
 // output's thread reads its residual before writing it), never x. x must be 16-byte aligned.
 constexpr int GEMV_HOLD = 4;  // passes of 32 blocks held in registers (K <= 4096 per row at once)
@@ -573,10 +573,14 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
             const float mu = (mm == -INFINITY) ? 0.0f : mm;
             float tl = 0.0f;
             float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            // One wave issues this whole merge, so its instruction count is
+            // its time: the hardware exp2 (a factor below 2^-126 becomes 0,
+            // where the library's would keep a subnormal), and one
+            // reciprocal of the sum for the four columns.
 #pragma unroll
             for (int sp = 0; sp < STEP_MAX_SPLITS; sp++) {
                 if (sp < ns) {
-                    const float f = exp2f(ml[sp].x - mu);
+                    const float f = __builtin_amdgcn_exp2f(ml[sp].x - mu);
                     tl = tl + ml[sp].y * f;
                     acc.x = acc.x + o4[sp].x * f;
                     acc.y = acc.y + o4[sp].y * f;
@@ -584,7 +588,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(const XT* __restrict__ x,
                     acc.w = acc.w + o4[sp].w * f;
                 }
             }
-            return make_float4(acc.x / tl, acc.y / tl, acc.z / tl, acc.w / tl);
+            const float inv = 1.0f / tl;
+            return make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
         };
         auto load_passes = [&](int p0) {
 #pragma unroll
