@@ -6,7 +6,8 @@
 // merge's arithmetic (wg_at, lo) finds again, in workgroup order; no
 // workgroup cuts more than its first and last block; and the XCD numbering of
 // the workgroups (xcd_order) is a bijection. Prints "ok <shapes>" or
-// the first failure.
+// the first failure. It also checks floordiv_nn, the division these walks
+// and the decode attention's partition use, against the integer quotient.
 #define __host__
 #define __device__
 #include <cstdio>
@@ -99,8 +100,36 @@ static int check(int64_t BH, int L, int S, int causal, int BQ, int BK, int slots
     return 0;
 }
 
+// floordiv_nn against the integer quotient: near multiples of t (where the
+// f64 quotient rounds to the next integer), at the ends of the range the
+// kernels use (products below 2^42), and on a pseudo-random sweep
+static int check_div() {
+    const int64_t ts[] = {1, 2, 3, 7, 255, 256, 1023, 1024, 2047, 2048, 65535, 1000003, 2147483647LL};
+    for (int64_t t : ts)
+        for (int64_t k : {0LL, 1LL, 2LL, 1000LL, (1LL << 20) + 7, (1LL << 31) - 1, (1LL << 42) / t})
+            for (int64_t d = -2; d <= 2; d++) {
+                const int64_t x = k * t + d;
+                if (x < 0) continue;
+                if (tn::floordiv_nn(x, t) != x / t) return 1;
+            }
+    uint64_t r = 0x9e3779b97f4a7c15ULL;
+    for (int i = 0; i < 2000000; i++) {
+        r ^= r << 13;
+        r ^= r >> 7;
+        r ^= r << 17;
+        const int64_t x = (int64_t)(r >> 22), t = (int64_t)((r & 0x7fffffff) | 1) >> (r % 31);
+        if (t < 1) continue;
+        if (tn::floordiv_nn(x, t) != x / t) return 1;
+    }
+    return 0;
+}
+
 int main() {
     int n = 0;
+    if (check_div()) {
+        std::printf("fail: floordiv_nn\n");
+        return 1;
+    }
     const int Ls[] = {1, 5, 127, 128, 129, 300, 1000, 2048, 4096};
     const int Ss[] = {1, 63, 64, 65, 200, 1000, 2048, 4096};
     const int64_t BHs[] = {1, 2, 9, 32, 64};

@@ -1271,7 +1271,7 @@ void k_decode_sk_bf16(const uint16_t* __restrict__ Qg, const uint16_t* __restric
     const int64_t W = min((int64_t)gridDim.x * (blockDim.x >> 6), (int64_t)T);
     const int wv = (int)blockIdx.x * (int)(blockDim.x >> 6) + rfl((int)threadIdx.x >> 6);
     if (wv >= W) return;  // uniform over the wave
-    const int u_lo = rfl((int)((int64_t)wv * T / W)), u_hi = rfl((int)((int64_t)(wv + 1) * T / W));
+    const int u_lo = rfl((int)floordiv_nn((int64_t)wv * T, W)), u_hi = rfl((int)floordiv_nn((int64_t)(wv + 1) * T, W));
 
     // walking state, uniform over the wave: the segment (b, sg) holding unit u
     int b, sg, n, len, seg0;
@@ -1543,18 +1543,27 @@ __global__ __launch_bounds__(D) void k_decode_sk_combine(const float* __restrict
     const int groups = nrep / NR, G = Hkv * groups;
     const int kvh = h / nrep, hr = h % nrep, grp = hr / NR, hh = hr % NR;
     const int sg = kvh * groups + grp;
-    int len = lens[b];
+    // the sequence's length and the two prefix sums, all three loads in one
+    // round trip (as scalar loads the compiler waited for each in turn)
+    const buf_rsrc rlen = make_rsrc(lens, (uint32_t)B * 4u), rpre = make_rsrc(pref, (uint32_t)(B + 1) * 4u);
+    const float f_len = buf_load_f(rlen, (uint32_t)b * 4u);
+    const float f_pb = buf_load_f(rpre, (uint32_t)b * 4u);
+    const float f_pT = buf_load_f(rpre, (uint32_t)B * 4u);
+    __builtin_amdgcn_sched_barrier(0);
+    int len = __builtin_amdgcn_readfirstlane(__float_as_int(f_len));
     len = len < 0 ? 0 : (len > max_len ? max_len : len);
     const int n = (len + SK_UNIT - 1) / SK_UNIT;
-    const int64_t T = pref[B];
-    const int64_t u0 = pref[b] + (int64_t)sg * n;  // the kernel's int sums, widened here
+    const int64_t T = __builtin_amdgcn_readfirstlane(__float_as_int(f_pT));
+    // the kernel's int sums, widened here
+    const int64_t u0 = __builtin_amdgcn_readfirstlane(__float_as_int(f_pb)) + (int64_t)sg * n;
     W = W < T ? W : T;
     const int64_t slot0 = (int64_t)b * G + sg;
     float mm = -INFINITY, tl = 0.0f, acc = 0.0f;
     int64_t w_lo = 0, w_hi = -1;
     if (n > 0) {
-        w_lo = ((u0 + 1) * W + T - 1) / T - 1;
-        w_hi = ((u0 + n) * W + T - 1) / T - 1;
+        // wave of unit u: ceil((u + 1) W / T) - 1 = floor(((u + 1) W - 1) / T)
+        w_lo = floordiv_nn((u0 + 1) * W - 1, T);
+        w_hi = floordiv_nn((u0 + n) * W - 1, T);
     }
     // batches of CB partials, every load of a batch in flight at once, as
     // unconditional buffer loads (a slot past the segment's last wave reads

@@ -18,6 +18,16 @@
 
 namespace tn {
 
+// floor(x / t) for 0 <= x < 2^53 and t > 0: the quotient from f64 (exact
+// operands, so it is off by at most one) corrected in integers. On the GPU a
+// 64-bit integer division is a long instruction sequence; this is a few.
+__host__ __device__ inline int64_t floordiv_nn(int64_t x, int64_t t) {
+    int64_t q = (int64_t)((double)x / (double)t);
+    if (q * t > x) q--;
+    else if ((q + 1) * t <= x) q++;
+    return q;
+}
+
 struct SkGeo {
     int nqb, NS, c, causal;  // query blocks, key tiles of S, key tiles per query block (PF_BQ / BK)
     int64_t Tbh, T, G;       // units per (batch, head), all units, workgroups (G <= T)
@@ -28,7 +38,7 @@ struct SkGeo {
         const int64_t m = qt < NS / c ? qt : NS / c;  // blocks below qt whose tiles stop before S
         return (int64_t)c * m * (m + 1) / 2 + ((int64_t)qt - m) * NS;
     }
-    __host__ __device__ int64_t lo(int64_t g) const { return g * T / G; }
+    __host__ __device__ int64_t lo(int64_t g) const { return floordiv_nn(g * T, G); }
     // The range number of hardware workgroup b. Workgroups are dealt to the
     // eight XCDs in turn (b to XCD b % 8); XCD x takes the consecutive
     // numbers x*(G/8) + min(x, G%8) onwards, so that the ranges of one head
@@ -37,10 +47,11 @@ struct SkGeo {
         const int64_t x = b % 8, qx = G / 8, rx = G % 8;
         return x * qx + (x < rx ? x : rx) + b / 8;
     }
-    __host__ __device__ int64_t wg_of(int64_t u) const { return ((u + 1) * G + T - 1) / T - 1; }
+    // ceil((u + 1) G / T) - 1
+    __host__ __device__ int64_t wg_of(int64_t u) const { return floordiv_nn((u + 1) * G - 1, T); }
     // the query block (bh, qt) that holds unit u, and u's tile in it
     __host__ __device__ void locate(int64_t u, int64_t& bh, int& qt, int& t) const {
-        bh = u / Tbh;
+        bh = floordiv_nn(u, Tbh);
         const int64_t r = u - bh * Tbh;
         int a = 0, b = nqb;  // the largest qt with P(qt) <= r (every block has a tile)
         while (b - a > 1) {
