@@ -67,9 +67,7 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
     // other and emits no blanket vmcnt(0) in front of it
     __shared__ __align__(16) uint16_t sK0[STAGE], sK1[STAGE];
     __shared__ __align__(16) uint16_t sV0[STAGE], sV1[STAGE];
-    __shared__ float2 s_ml[NW][32];
-    __shared__ float s_lf[NW][32];  // each key group's l scaled to the row's reference point
-    __shared__ float s_mu[2][32];   // the row's reference point, per query half
+    __shared__ float2 s_ml[NW][32];  // each wave's (m, l) per query row
     __shared__ __align__(16) uint16_t sQ[FA_BQ * D];  // the block's query rows, chunks swizzled as K's
     auto stK = [&](auto sc) -> uint16_t* {
         if constexpr (decltype(sc)::value == 0) return sK0; else return sK1;
@@ -301,31 +299,25 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
     for (int i = 0; i < D / 32; i++) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(o[i]));
     l = xor32_sum(l);
 
-    // The eight key groups of each query half meet in LDS. First every wave
-    // publishes its (m, l) (s_ml lies outside the ring); after the barrier
-    // each lane takes its query's largest reference point mu over the key
-    // groups, scales its accumulators by 2^(m - mu) and writes them (8 KB per
-    // wave, laid over the ring, whose last reads are behind that barrier) with
-    // its scaled l; then every thread adds four columns of one query over the
-    // key groups, in key-group order, normalises and stores them. Rows hold
-    // 16 float4 columns, XOR-swizzled by the query so that the 32 queries of a
-    // store land in different banks. The scaling is done once per (wave,
-    // lane) instead of once per output column, and the normalisation is one
-    // reciprocal per thread: this end of the workgroup is VALU-bound.
+    // The eight key groups of each query half meet in LDS. Each wave writes
+    // its unscaled accumulators (8 KB) into a slot laid over the ring, with
+    // its (m, l) beside it; then every thread takes one query's largest
+    // reference point mu over the key groups and adds four columns of that
+    // query over the groups in key-group order, each group's columns and l
+    // scaled by 2^(m - mu) as they are read, normalises and stores them.
+    // During the last stage the ring buffer it does not use is free, so the
+    // waves of key groups 0-3 (the oldest, which finish their last tile
+    // first) write there at once; groups 4-7 write over the last stage's
+    // buffer once every wave has passed the barrier after its last reads.
+    // Rows hold 16 float4 columns, XOR-swizzled by the query so that the 32
+    // queries of a store land in different banks.
+    const int lastbuf = (nst - 1) & 1;  // the ring buffer of the last stage
     auto slot_of = [&](int wv) -> float* {
-        const int a = wv >> 2;
-        uint16_t* base = a == 0 ? sK0 : a == 1 ? sK1 : a == 2 ? sV0 : sV1;
+        const int buf = wv < 8 ? lastbuf ^ 1 : lastbuf, a = (wv >> 2) & 1;
+        uint16_t* base = buf == 0 ? (a == 0 ? sK0 : sV0) : (a == 0 ? sK1 : sV1);
         return reinterpret_cast<float*>(base) + (wv & 3) * (32 * D);
     };
-    if (hh == 0) s_ml[w][lq] = make_float2(m, l);
-    __syncthreads();
-    {
-        float mm = -INFINITY;
-#pragma unroll
-        for (int g = 0; g < FA_KG; g++) mm = fmaxf(mm, s_ml[2 * g + qh][lq].x);
-        const float mu = (mm == -INFINITY) ? 0.0f : mm;
-        // a group that saw no key has m = -inf: factor 0 (its o and l are 0)
-        const float f = __builtin_amdgcn_exp2f(m - mu);
+    auto store_o = [&]() __attribute__((always_inline)) {
         float* slot = slot_of(w);
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++)
@@ -334,28 +326,39 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
                 // O^T[d = 32dt + 8g4 + 4hh + e][q = lq]
                 const int c4 = (32 * dt + 8 * g4 + 4 * hh) >> 2;
                 *reinterpret_cast<float4*>(slot + lq * D + ((c4 ^ (lq & 15)) << 2)) =
-                    make_float4(o[dt][4 * g4] * f, o[dt][4 * g4 + 1] * f, o[dt][4 * g4 + 2] * f,
-                                o[dt][4 * g4 + 3] * f);
+                    make_float4(o[dt][4 * g4], o[dt][4 * g4 + 1], o[dt][4 * g4 + 2], o[dt][4 * g4 + 3]);
             }
-        if (hh == 0) s_lf[w][lq] = l * f;
-        if (hh == 0 && kg == 0) s_mu[qh][lq] = mm;
-    }
+    };
+    if (hh == 0) s_ml[w][lq] = make_float2(m, l);
+    if (kg < 4) store_o();
+    __syncthreads();
+    if (kg >= 4) store_o();
     __syncthreads();
     {
         const int q = tid >> 4, c4 = tid & 15;  // query of the workgroup, columns 4*c4 .. 4*c4 + 3
         const int half = q >> 5, ql = q & 31;
         const int qrow = q0 + q;
         if (qrow < L) {
+            float2 mlg[FA_KG];
+            float mm = -INFINITY;
+#pragma unroll
+            for (int g = 0; g < FA_KG; g++) {
+                mlg[g] = s_ml[2 * g + half][ql];
+                mm = fmaxf(mm, mlg[g].x);
+            }
+            const float mu = (mm == -INFINITY) ? 0.0f : mm;
             float tl = 0.0f, a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
             for (int g = 0; g < FA_KG; g++) {
-                tl = tl + s_lf[2 * g + half][ql];
+                // a group that saw no key has m = -inf: factor 0 (its o and l are 0)
+                const float f = __builtin_amdgcn_exp2f(mlg[g].x - mu);
+                tl = tl + mlg[g].y * f;
                 const float4 x = *reinterpret_cast<const float4*>(slot_of(2 * g + half) + ql * D +
                                                                   ((c4 ^ (ql & 15)) << 2));
-                a0 = a0 + x.x;
-                a1 = a1 + x.y;
-                a2 = a2 + x.z;
-                a3 = a3 + x.w;
+                a0 = a0 + x.x * f;
+                a1 = a1 + x.y * f;
+                a2 = a2 + x.z * f;
+                a3 = a3 + x.w * f;
             }
             // the reciprocal (1 ulp) then four products: the bf16/f16 outputs
             // round far coarser than the f32 quotient's last bit
@@ -363,10 +366,7 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
             const int64_t row = (int64_t)bh * L + qrow;
             *reinterpret_cast<uint2*>(Og + row * D + 4 * c4) =
                 make_uint2(E::pack_out_hw(a0 * inv, a1 * inv), E::pack_out_hw(a2 * inv, a3 * inv));
-            if (lse && c4 == 0) {
-                const float mm = s_mu[half][ql];
-                lse[row] = mm == -INFINITY ? NAN : mm * LN2 + logf(tl);
-            }
+            if (lse && c4 == 0) lse[row] = mm == -INFINITY ? NAN : mm * LN2 + logf(tl);
         }
     }
 }
