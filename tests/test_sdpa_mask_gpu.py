@@ -142,3 +142,72 @@ def test_a_mask_that_does_not_broadcast_is_refused(tn):
     mt = tn.tensor(np.zeros((3, 4), np.float32), device="hip")
     with pytest.raises(RuntimeError, match="cannot be broadcast"):
         tn._aten_dispatch(OP, qt, qt, qt, 0.0, False, attn_mask=mt)
+
+
+# A mask that is the same for every query row ([B, 1, 1, S] key padding, or a
+# per-head key bias [B, Hq, 1, S]) runs at head dim 64 on the kernel without
+# split rows, which stages the 256 mask values of each ring stage in LDS;
+# the shapes below give partial stages and tiles (S = 333), GQA, and causal
+# rows on top of the mask.
+@pytest.mark.parametrize("dtype,mask_dtype,mshape,causal", [
+    ("bfloat16", "float32", (2, 1, 1, 333), True),
+    ("bfloat16", "bfloat16", (1, 4, 1, 333), False),
+    ("float16", "float16", (2, 4, 1, 333), True),
+    ("float16", "float32", (1, 1, 1, 333), False),
+])
+def test_key_mask_on_the_kernel_without_split_rows(tn, dtype, mask_dtype, mshape, causal):
+    from test_sdpa_gpu import _check_masked
+
+    rng = np.random.default_rng(sum(mshape) + causal)
+    B, Hq, Hkv, L, S, D = 2, 4, 2, 200, 333, 64
+    q, k, v = (rng.standard_normal(s) for s in ((B, Hq, L, D), (B, Hkv, S, D), (B, Hkv, S, D)))
+    mask = rng.standard_normal(mshape) * 2
+    mask[..., 50:60] = -np.inf  # keys no row may see
+    _check_masked(tn, dtype, q, k, v, mask, mask_dtype, causal)
+
+
+def test_key_padding_in_front_leaves_the_first_causal_rows_empty(tn):
+    """Keys 0-36 masked and causal rows: rows 0-36 see no key, so their
+    outputs and lse are NaN, as the reference's are."""
+    from test_sdpa_gpu import _check_masked
+
+    rng = np.random.default_rng(21)
+    B, Hq, Hkv, L, S, D = 1, 3, 1, 100, 100, 64
+    q, k, v = (rng.standard_normal(s) for s in ((B, Hq, L, D), (B, Hkv, S, D), (B, Hkv, S, D)))
+    mask = np.zeros((1, 1, 1, S))
+    mask[..., :37] = -np.inf
+    _check_masked(tn, "bfloat16", q, k, v, mask, "float32", causal=True,
+                  nan_rows=[(0, h, i) for h in range(Hq) for i in range(37)])
+
+
+def test_bool_key_padding_with_causal_rows_through_the_c_abi(tn):
+    """The bench's masked leg: config 2's shape (bf16, causal, 9/3 heads,
+    S = 2048) with a bool [B, 1, 1, S] mask hiding the last 64 keys, passed
+    by strides to tn_sdpa_fwd, against the oracle with where(mask, 0, -inf)."""
+    import ctypes
+
+    from torchnative_amd import _lib as L
+    from test_sdpa_gpu import _bound, _dev, _narrow
+
+    rng = np.random.default_rng(22)
+    B, Hq, Hkv, S, D = 1, 9, 3, 2048, 64
+    q, k, v = (rng.standard_normal(s) for s in ((B, Hq, S, D), (B, Hkv, S, D), (B, Hkv, S, D)))
+    keep = np.ones((B, 1, 1, S), bool)
+    keep[..., S - 64:] = False
+    qt, kt, vt = (_dev(tn, "bfloat16", a) for a in (q, k, v))
+    mt = tn.tensor(keep, device="hip")
+    out = tn.empty((B, Hq, S, D), "bfloat16", "hip")
+    lse = tn.empty((B, Hq, S), "float32", "hip")
+    strides = (ctypes.c_int64 * 4)(S, 0, 0, 1)
+    L.check(L.lib().tn_sdpa_fwd(None, L.TN_BF16, qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), B, Hq, Hkv, S, S, D,
+                                mt.data_ptr(), L.TN_BOOL, strides, 1, float("nan"), out.data_ptr(),
+                                lse.data_ptr()))
+    qw, kw, vw = (t.numpy().astype(np.float64) for t in (qt, kt, vt))
+    add = np.ascontiguousarray(np.broadcast_to(np.where(keep, 0.0, -np.inf), (B, Hq, S, S)))
+    r32, l32 = O.sdpa(qw, kw, vw, mask=add, is_causal=True, threads=16)
+    r64, l64 = O.sdpa(qw, kw, vw, mask=add, is_causal=True, threads=16, dtype=np.float64)
+    pav = O.sdpa(qw, kw, np.abs(vw), mask=add, is_causal=True, threads=16, dtype=np.float64)[0]
+    got, gl = out.numpy().astype(np.float64), lse.numpy().astype(np.float64)
+    tol = _bound(r32, r64, pav, got=got, kind="bfloat16")
+    assert float(np.max(np.abs(got - _narrow("bfloat16", r32)) / tol)) <= 1.0
+    assert float(np.max(np.abs(gl - l32) / _bound(l32, l64))) <= 1.0

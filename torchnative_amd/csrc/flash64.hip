@@ -68,6 +68,9 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
     __shared__ __align__(16) uint16_t sK0[STAGE], sK1[STAGE];
     __shared__ __align__(16) uint16_t sV0[STAGE], sV1[STAGE];
     __shared__ float2 s_ml[NW][32];  // each wave's (m, l) per query row
+    // a mask that is the same for every query row: the stage's 256 values,
+    // in log2 units, per ring stage
+    __shared__ __align__(16) float sM[MASK ? 2 : 1][MASK ? FA_ROWS : 1];
     __shared__ __align__(16) uint16_t sQ[FA_BQ * D];  // the block's query rows, chunks swizzled as K's
     auto stK = [&](auto sc) -> uint16_t* {
         if constexpr (decltype(sc)::value == 0) return sK0; else return sK1;
@@ -125,8 +128,17 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
         const int row = p / CPR;
         voff[i] = (uint32_t)(row * D + swz(row, p % CPR) * 8) * 2u;
     }
+    // the mask row of this (batch, head); thread t < 256 loads key t of each
+    // stage into mval, and writes it to sM once the stage's loads have landed
+    const int64_t mbase = MASK ? (int64_t)b * mask.sb + (int64_t)h * mask.sh : 0;
+    float mval = 0.0f;
     auto issue = [&](auto sc, int st) __attribute__((always_inline)) {
         const int k0 = st * FA_ROWS;
+        if constexpr (MASK != 0) {
+            const int key = k0 + tid;
+            mval = 0.0f;  // keys past S: masked by the tile's key test
+            if (tid < FA_ROWS && key < S) mval = mask_val<MASK, F16>(mask.p, mbase + (int64_t)key * mask.sk);
+        }
         const uint32_t bytes = (uint32_t)(S - k0) * (uint32_t)(D * 2);  // keys k0 .. S-1; past them read 0
         const buf_rsrc rk = make_rsrc(kp + (int64_t)k0 * D, bytes);
         const buf_rsrc rv = make_rsrc(vp + (int64_t)k0 * D, bytes);
@@ -163,6 +175,10 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
 
     auto step = [&](auto sc, int st) __attribute__((always_inline)) {
         wait_vmcnt<0>();  // the only loads in flight are this stage's
+        // the stage's mask values, in log2 units (the buffer's last reads,
+        // two stages back, are behind the previous barrier)
+        if constexpr (MASK != 0)
+            if (tid < FA_ROWS) sM[decltype(sc)::value][tid] = mval * LOG2E;
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
@@ -199,14 +215,14 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
         for (int r = 0; r < 16; r++) v[r] = acc[r];
         if constexpr (MASK != 0) {
             // scores to log2 units with the mask added: raw*scale*log2e + mask*log2e
-            if (qi < L) {
-                const int64_t mrow = (int64_t)b * mask.sb + (int64_t)h * mask.sh + (int64_t)qi * mask.sl;
+            const float* ms = sM[decltype(sc)::value] + kr + 4 * hh;
 #pragma unroll
-                for (int rq = 0; rq < 4; rq++) {
-                    const f32x4 mv = mask_quad<MASK, F16>(mask, mrow, k0 + 8 * rq + 4 * hh, S);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) v[4 * rq + e] = v[4 * rq + e] * sl2 + mv[e] * LOG2E;
-                }
+            for (int rq = 0; rq < 4; rq++) {
+                const float4 mv = *reinterpret_cast<const float4*>(ms + 8 * rq);
+                v[4 * rq] = v[4 * rq] * sl2 + mv.x;
+                v[4 * rq + 1] = v[4 * rq + 1] * sl2 + mv.y;
+                v[4 * rq + 2] = v[4 * rq + 2] * sl2 + mv.z;
+                v[4 * rq + 3] = v[4 * rq + 3] * sl2 + mv.w;
             }
         }
         if (k0 + FA_BKW > S || (causal && k0 + FA_BKW - 1 > qw0)) {
@@ -386,10 +402,20 @@ tn_status flash64_launch(hipStream_t st, bool f16, int mk, const void* mask, int
 #define TN_FA64(MK, H)                                                                                           \
     hipLaunchKernelGGL((k_fa64<MK, H>), dim3((unsigned)items), dim3(FA_NT), 0, st, q, k, v, (int)(B * Hq), (int)Hq, \
                        (int)Hkv, (int)L, (int)S, (int)nqb, sl2, causal, out, lse, mref)
-    // masked calls run on k_flash16 (sdpa.hip): the mask reads do not fit
-    // this kernel's 128 registers per wave without spilling
-    if (mk != 0) return fail(TN_EINVAL, "flash64: masks are not taken by this kernel");
-    if (f16) TN_FA64(0, true); else TN_FA64(0, false);
+    // a mask that varies along the query rows runs on k_flash16 (sdpa.hip):
+    // its reads per row do not fit this kernel's 128 registers per wave
+    if (mk != 0 && msl != 0) return fail(TN_EINVAL, "flash64: only masks that are the same for every query row");
+    if (f16) {
+        if (mk == 0) TN_FA64(0, true);
+        else if (mk == 1) TN_FA64(1, true);
+        else if (mk == 3) TN_FA64(3, true);
+        else TN_FA64(2, true);
+    } else {
+        if (mk == 0) TN_FA64(0, false);
+        else if (mk == 1) TN_FA64(1, false);
+        else if (mk == 3) TN_FA64(3, false);
+        else TN_FA64(2, false);
+    }
 #undef TN_FA64
     TN_LAUNCHED();
     return TN_OK;

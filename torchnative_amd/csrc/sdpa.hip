@@ -2323,11 +2323,13 @@ tn_status tn_sdpa_fwd(void* stream, int dtype, const void* q, const void* k, con
     if (dtype == TN_BF16 || dtype == TN_F16) {
         // the key/value buffer descriptors cover one head's S*D elements
         if (S * D * 2 > INT32_MAX) return fail(TN_EVALUE, std::string(OP) + ": key length too large");
-        // Small unmasked D=64 work (up to four 64-query blocks per CU, where
-        // the split-row kernel below would have to split rows to fill the
-        // chip) runs without splits on flash64.hip; larger work keeps the
-        // split-row kernel, which is faster once every CU has several blocks.
-        if (D == 64 && mk == 0 && B * Hq * cdiv(L, 64) <= 1024)
+        // Small D=64 work (up to four 64-query blocks per CU, where the
+        // split-row kernel below would have to split rows to fill the chip)
+        // runs without splits on flash64.hip, unmasked or with a mask that is
+        // the same for every query row (a key padding mask, [B, 1, 1, S]);
+        // larger work keeps the split-row kernel, which is faster once every
+        // CU has several blocks.
+        if (D == 64 && (mk == 0 || mref.sl == 0) && B * Hq * cdiv(L, 64) <= 1024)
             return flash64_launch(st, dtype == TN_F16, mk, attn_mask, mref.sb, mref.sh, mref.sl, mref.sk,
                                   static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                                   static_cast<const uint16_t*>(v), B, Hq, Hkv, L, S, sl2, c,
