@@ -214,15 +214,16 @@ __global__ __launch_bounds__(FA_NT) void k_fa64(const uint16_t* __restrict__ Qg,
 #pragma unroll
         for (int r = 0; r < 16; r++) v[r] = acc[r];
         if constexpr (MASK != 0) {
-            // scores to log2 units with the mask added: raw*scale*log2e + mask*log2e
+            // scores to log2 units with the mask added, one rounding:
+            // fma(raw, scale*log2e, mask*log2e)
             const float* ms = sM[decltype(sc)::value] + kr + 4 * hh;
 #pragma unroll
             for (int rq = 0; rq < 4; rq++) {
                 const float4 mv = *reinterpret_cast<const float4*>(ms + 8 * rq);
-                v[4 * rq] = v[4 * rq] * sl2 + mv.x;
-                v[4 * rq + 1] = v[4 * rq + 1] * sl2 + mv.y;
-                v[4 * rq + 2] = v[4 * rq + 2] * sl2 + mv.z;
-                v[4 * rq + 3] = v[4 * rq + 3] * sl2 + mv.w;
+                v[4 * rq] = __builtin_fmaf(v[4 * rq], sl2, mv.x);
+                v[4 * rq + 1] = __builtin_fmaf(v[4 * rq + 1], sl2, mv.y);
+                v[4 * rq + 2] = __builtin_fmaf(v[4 * rq + 2], sl2, mv.z);
+                v[4 * rq + 3] = __builtin_fmaf(v[4 * rq + 3], sl2, mv.w);
             }
         }
         if (k0 + FA_BKW > S || (causal && k0 + FA_BKW - 1 > qw0)) {
