@@ -957,9 +957,13 @@ constexpr int GM_AS = QK + 8;  // LDS row stride (bf16) of the code tiles: 80 B,
 constexpr int GM_RS = 4;       // K blocks whose operands are in flight ahead of the one computed
 
 // WR x WC waves over a GM_BM x BN tile, each wave TI x TJ MFMA tiles of
-// 16x16: <2, 2> is 128 x 128 (waves of 64 x 64), <4, 1> is 128 x 112 (waves
-// of 32 x 112), chosen at launch so the tiles fill the device evenly.
-template <int WR, int WC>
+// 16x16: <2, 2, 4> is 128 x 128 (waves of 64 x 64), <4, 1, 7> is 128 x 112
+// (waves of 32 x 112), chosen at launch so the tiles fill the device evenly.
+// Products with few rows and columns (a prompt's projections) take narrow
+// tiles, <4, 1, TJ> with 16 TJ columns, so that more workgroups share the
+// work: each walks every K block in order whatever its tile, so the number
+// of workgroups, not their width, sets such a call's time.
+template <int WR, int WC, int TJ>
 __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict__ xc,
                                                     const float* __restrict__ dxT,
                                                     const float* __restrict__ corrT, int M, int M_pad, int nb,
@@ -969,8 +973,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
                                                     int y_bf16) {
     static_assert(WR * WC == GM_THREADS / 64, "one wave per sub-tile");
     constexpr int TI = GM_BM / (16 * WR);  // MFMA row tiles per wave
-    constexpr int TJ = WR == 2 ? 4 : 7;    // MFMA column tiles per wave
-    constexpr int BN = 16 * TJ * WC;       // columns per workgroup: 128 or 112
+    constexpr int BN = 16 * TJ * WC;       // columns per workgroup
     static_assert(2 * BN <= GM_THREADS && GM_BM + BN <= GM_THREADS, "staging threads");
     __shared__ __align__(16) uint16_t sA[2][GM_BM * GM_AS];
     __shared__ __align__(16) uint16_t sB[2][BN * GM_AS];
@@ -1533,15 +1536,25 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
                                dxT, corrT);
         TN_LAUNCHED();
         // 112-column tiles when they fill the device in whole rounds of two
-        // workgroups per CU and 128-column ones would not
+        // workgroups per CU and 128-column ones would not; when 128-column
+        // tiles would leave most CUs idle, the widest of 64, 32 or 16 columns
+        // that gives a workgroup per CU (else 16)
         const int64_t mt = M_pad / GM_BM;
         const bool t112 = n % 112 == 0 && (mt * (n / 112)) % 512 == 0 && (mt * cdiv(n, GM_BN)) % 512 != 0;
-        if (t112)
-            hipLaunchKernelGGL((k_gemm<4, 1>), dim3((unsigned)(n / 112), (unsigned)mt), dim3(GM_THREADS), 0, st, xc,
-                               dxT, corrT, (int)m, (int)M_pad, nb, qs, d, (int)n, bias, y, y_bf16);
-        else
-            hipLaunchKernelGGL((k_gemm<2, 2>), grid, dim3(GM_THREADS), 0, st, xc, dxT, corrT, (int)m, (int)M_pad, nb,
-                               qs, d, (int)n, bias, y, y_bf16);
+        int bn = GM_BN;
+        if (mt * cdiv(n, GM_BN) < 128) {
+            bn = 64;
+            while (bn > 16 && mt * cdiv(n, bn) < 256) bn /= 2;
+        }
+#define TN_GEMM(WR, WC, TJ, BNN)                                                                                   \
+    hipLaunchKernelGGL((k_gemm<WR, WC, TJ>), dim3((unsigned)cdiv(n, BNN), (unsigned)mt), dim3(GM_THREADS), 0, st, \
+                       xc, dxT, corrT, (int)m, (int)M_pad, nb, qs, d, (int)n, bias, y, y_bf16)
+        if (t112) TN_GEMM(4, 1, 7, 112);
+        else if (bn == 16) TN_GEMM(4, 1, 1, 16);
+        else if (bn == 32) TN_GEMM(4, 1, 2, 32);
+        else if (bn == 64) TN_GEMM(4, 1, 4, 64);
+        else TN_GEMM(2, 2, 4, GM_BN);
+#undef TN_GEMM
         TN_LAUNCHED();
     }
     return TN_OK;
