@@ -520,17 +520,6 @@ __global__ void k_heads_to_rows(const float* __restrict__ a, int T, int heads, i
         rows[((int64_t)t * heads + h) * d + c] = a[((int64_t)h * T + t) * d + c];
 }
 
-// silu(gate) * up for token rows gu [T][2I] (gate | up) into act [T][I]:
-// k_silu_mul's arithmetic, which the decode step's SiLU prologue reproduces.
-__global__ __launch_bounds__(256) void k_silu_mul_rows(const float* __restrict__ gu, int64_t T, int I,
-                                                       float* __restrict__ act) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= T * I) return;
-    const int64_t t = idx / I, j = idx - t * I;
-    const float g = gu[t * 2 * I + j];
-    act[idx] = (g / (1.0f + expf(-g))) * gu[t * 2 * I + I + j];
-}
-
 // the decode state before the prompt's last position: position T - 1 is the
 // one being processed, so the lm_head's advance moves to T
 __global__ void k_prefill_state(int32_t* state, int last) {
@@ -814,7 +803,7 @@ tn_status tn_llama_step(void* stream, const tn_llama* m) {
 // batched == one-row property); the attention's summation order is the
 // prefill kernel's.
 struct PrefillWork {
-    int64_t h, x, qkv, q, kt, vt, att, rows, o, gu, act, rope, total;
+    int64_t h, x, qkv, q, kt, vt, att, rows, gu, rope, total;
 };
 static PrefillWork prefill_work(const tn_llama* m, int64_t T) {
     PrefillWork w;
@@ -833,9 +822,7 @@ static PrefillWork prefill_work(const tn_llama* m, int64_t T) {
     w.vt = take(T * Hkv * D);
     w.att = take(T * Hq * D);
     w.rows = take(T * Hq * D);
-    w.o = take(T * H);
     w.gu = take(T * 2 * I);
-    w.act = take(T * I);
     w.rope = take(T * D);  // T * D/2 float2
     w.total = o;
     return w;
@@ -861,34 +848,39 @@ tn_status tn_llama_prefill(void* stream, const tn_llama* m, int64_t T, float* wo
     if (T * std::max(nqkv, 2 * I) > INT32_MAX) return fail(TN_EVALUE, "tn_llama_prefill: prompt too long");
     float* h = work + w.h;
     float* x = work + w.x;
-    float* o = work + w.o;
     float2* rope = reinterpret_cast<float2*>(work + w.rope);
+    // the o projection reads the attention output in place when a head's
+    // rows are whole 32-element blocks
+    const bool heads_ok = D % 32 == 0;
     hipLaunchKernelGGL(k_prefill_begin, dim3((unsigned)T), dim3(256), 0, st, m->prompt, (int)T, 0, m->embed,
                        m->vocab, (int)H, h, m->tokens, m->inv_freq, (int)(D / 2), rope);
     TN_LAUNCHED();
     for (int64_t l = 0; l < m->n_layers; l++) {
         const tn_llama_layer& L = m->layers[l];
         TN_TRY(tn_rmsnorm(stream, h, T, H, L.ln1, m->eps, x));
-        TN_TRY(tn_q4_0_linear(stream, x, TN_F32, T, H, L.qkv.qs, L.qkv.d, nqkv, nullptr, work + w.qkv, TN_F32));
+        TN_TRY(linear_prefill(st, x, T, H, XM_ROWS, 0, L.qkv.qs, L.qkv.d, nqkv, nullptr, work + w.qkv));
         hipLaunchKernelGGL(k_prefill_qkv, dim3((unsigned)T, (unsigned)(Hq + 2 * Hkv)), dim3((unsigned)(D / 2)), 0, st,
                            work + w.qkv, (int)T, (int)Hq, (int)Hkv, (int)D, rope, work + w.q, work + w.kt,
                            work + w.vt, L.k_cache, L.v_cache, (int)m->cap, 0);
         TN_LAUNCHED();
         TN_TRY(tn_sdpa_fwd(stream, TN_F32, work + w.q, work + w.kt, work + w.vt, 1, Hq, Hkv, T, T, D, nullptr, 0,
                            nullptr, 1, std::nan(""), work + w.att, nullptr));
-        hipLaunchKernelGGL(k_heads_to_rows, dim3((unsigned)T, (unsigned)Hq), dim3((unsigned)std::min<int64_t>(D, 256)),
-                           0, st, work + w.att, (int)T, (int)Hq, (int)D, work + w.rows);
-        TN_LAUNCHED();
-        TN_TRY(tn_q4_0_linear(stream, work + w.rows, TN_F32, T, Hq * D, L.o.qs, L.o.d, H, nullptr, o, TN_F32));
-        TN_TRY(tn_add(stream, h, o, T * H, h));
+        // the o projection reads the attention's [heads][T][D] output as
+        // token rows and adds the residual in its epilogue: h += o
+        if (heads_ok) {
+            TN_TRY(linear_prefill(st, work + w.att, T, Hq * D, XM_HEADS, (int)D, L.o.qs, L.o.d, H, h, h));
+        } else {
+            hipLaunchKernelGGL(k_heads_to_rows, dim3((unsigned)T, (unsigned)Hq),
+                               dim3((unsigned)std::min<int64_t>(D, 256)), 0, st, work + w.att, (int)T, (int)Hq, (int)D,
+                               work + w.rows);
+            TN_LAUNCHED();
+            TN_TRY(linear_prefill(st, work + w.rows, T, Hq * D, XM_ROWS, 0, L.o.qs, L.o.d, H, h, h));
+        }
         TN_TRY(tn_rmsnorm(stream, h, T, H, L.ln2, m->eps, x));
-        TN_TRY(tn_q4_0_linear(stream, x, TN_F32, T, H, L.gate_up.qs, L.gate_up.d, 2 * I, nullptr, work + w.gu,
-                              TN_F32));
-        hipLaunchKernelGGL(k_silu_mul_rows, dim3((unsigned)cdiv(T * I, 256)), dim3(256), 0, st, work + w.gu, T, (int)I,
-                           work + w.act);
-        TN_LAUNCHED();
-        TN_TRY(tn_q4_0_linear(stream, work + w.act, TN_F32, T, I, L.down.qs, L.down.d, H, nullptr, o, TN_F32));
-        TN_TRY(tn_add(stream, h, o, T * H, h));
+        TN_TRY(linear_prefill(st, x, T, H, XM_ROWS, 0, L.gate_up.qs, L.gate_up.d, 2 * I, nullptr, work + w.gu));
+        // the down projection takes silu(gate) * up of the gate_up rows in
+        // its prepass and adds the residual in its epilogue: h += down(...)
+        TN_TRY(linear_prefill(st, work + w.gu, T, I, XM_GLU, 0, L.down.qs, L.down.d, H, h, h));
     }
     // the last position as a decode step ends it: the logits, their argmax
     // and the advance to position T (the prompt's token there, else the argmax)

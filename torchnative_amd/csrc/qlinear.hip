@@ -919,19 +919,40 @@ __device__ inline void q8_0_quad(const float (&v)[8], int (&q)[8], float* dx, in
     *s = sum;
 }
 
+// How the prepass finds a row's activations (XM_* in tn_common.h). XM_ROWS:
+// row r is x[r][0..K). XM_GLU: x holds [M][2K] rows (gate | up) and the
+// activation is silu(gate) * up, k_silu_mul's arithmetic (decode.hip).
+// XM_HEADS: x is an attention output [K / hd][M][hd] (head-major) and row r
+// is its heads' rows of token r side by side. The last two let a prompt's
+// down and o projections read their producers' outputs without a copy in
+// between.
+
 // k_q8_rows for a 16-byte aligned x: four lanes per (row, block), one 16- or
 // 32-byte load each. Lane part p holds elements 8p .. 8p+7, whose K slots are
 // two runs of four (kslot_of_element), written as two 8-byte stores.
-template <typename XT>
+template <typename XT, int XM = XM_ROWS>
 __global__ __launch_bounds__(256) void k_q8_rows_v(const XT* __restrict__ x, int M, int M_pad, int K, int nb,
                                                    uint16_t* __restrict__ xc, float* __restrict__ dxT,
-                                                   float* __restrict__ corrT) {
+                                                   float* __restrict__ corrT, int hd = 0) {
     const int64_t blk = (int64_t)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
     const int part = threadIdx.x & 3;
     if (blk >= (int64_t)M_pad * nb) return;  // the four lanes of a block leave together
     const int row = (int)(blk / nb), b = (int)(blk - (int64_t)row * nb);
     float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (row < M) load_x8<XT>(x + (int64_t)row * K + b * QK + 8 * part, v);
+    if (row < M) {
+        if constexpr (XM == XM_GLU) {
+            float g[8], u[8];
+            load_x8<XT>(x + (int64_t)row * 2 * K + b * QK + 8 * part, g);
+            load_x8<XT>(x + (int64_t)row * 2 * K + K + b * QK + 8 * part, u);
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = (g[e] / (1.0f + expf(-g[e]))) * u[e];
+        } else if constexpr (XM == XM_HEADS) {
+            const int e0 = b * QK, h = e0 / hd;
+            load_x8<XT>(x + ((int64_t)h * M + row) * hd + (e0 - h * hd) + 8 * part, v);
+        } else {
+            load_x8<XT>(x + (int64_t)row * K + b * QK + 8 * part, v);
+        }
+    }
     int q[8], s;
     float dx;
     q8_0_quad(v, q, &dx, &s);
@@ -969,8 +990,8 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
                                                     const float* __restrict__ corrT, int M, int M_pad, int nb,
                                                     const uint8_t* __restrict__ qs,
                                                     const uint16_t* __restrict__ dw, int N,
-                                                    const float* __restrict__ bias, void* __restrict__ y,
-                                                    int y_bf16) {
+                                                    const float* __restrict__ bias, void* y, int y_bf16,
+                                                    const float* resid = nullptr) {
     static_assert(WR * WC == GM_THREADS / 64, "one wave per sub-tile");
     constexpr int TI = GM_BM / (16 * WR);  // MFMA row tiles per wave
     constexpr int BN = 16 * TJ * WC;       // columns per workgroup
@@ -1180,6 +1201,8 @@ __global__ __launch_bounds__(GM_THREADS) void k_gemm(const uint16_t* __restrict_
                 if (m >= M) continue;
                 float v = acc[i][j][r];
                 if (bias) v = v + bv;
+                // resid + y, tn_add's operation, into y (f32); resid may be y
+                if (resid) v = resid[(int64_t)m * N + n] + v;
                 if (y_bf16)
                     reinterpret_cast<uint16_t*>(y)[(int64_t)m * N + n] = bf16_from_f32(v);
                 else
@@ -1467,6 +1490,31 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
     return TN_OK;
 }
 
+// The q4 GEMM over the prepass's codes: 112-column tiles when they fill the
+// device in whole rounds of two workgroups per CU and 128-column ones would
+// not; when 128-column tiles would leave most CUs idle, the widest of 64, 32
+// or 16 columns that gives a workgroup per CU (else 16).
+void gemm_q4_launch(hipStream_t st, const uint16_t* xc, const float* dxT, const float* corrT, int64_t m,
+                    int64_t M_pad, int nb, const uint8_t* qs, const uint16_t* d, int64_t n, const float* bias, void* y,
+                    int y_bf16, const float* resid) {
+    const int64_t mt = M_pad / GM_BM;
+    const bool t112 = n % 112 == 0 && (mt * (n / 112)) % 512 == 0 && (mt * cdiv(n, GM_BN)) % 512 != 0;
+    int bn = GM_BN;
+    if (mt * cdiv(n, GM_BN) < 128) {
+        bn = 64;
+        while (bn > 16 && mt * cdiv(n, bn) < 256) bn /= 2;
+    }
+#define TN_GEMM(WR, WC, TJ, BNN)                                                                                   \
+    hipLaunchKernelGGL((k_gemm<WR, WC, TJ>), dim3((unsigned)cdiv(n, BNN), (unsigned)mt), dim3(GM_THREADS), 0, st, \
+                       xc, dxT, corrT, (int)m, (int)M_pad, nb, qs, d, (int)n, bias, y, y_bf16, resid)
+    if (t112) TN_GEMM(4, 1, 7, 112);
+    else if (bn == 16) TN_GEMM(4, 1, 1, 16);
+    else if (bn == 32) TN_GEMM(4, 1, 2, 32);
+    else if (bn == 64) TN_GEMM(4, 1, 4, 64);
+    else TN_GEMM(2, 2, 4, GM_BN);
+#undef TN_GEMM
+}
+
 template <int FMT, typename XT>
 tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const uint8_t* qs, const uint16_t* d,
                       int64_t n, const float* bias, void* y, int y_bf16) {
@@ -1535,26 +1583,7 @@ tn_status linear_impl(hipStream_t st, const XT* x, int64_t m, int64_t k, const u
             hipLaunchKernelGGL((k_q8_rows<XT>), dim3(pgrid), dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
                                dxT, corrT);
         TN_LAUNCHED();
-        // 112-column tiles when they fill the device in whole rounds of two
-        // workgroups per CU and 128-column ones would not; when 128-column
-        // tiles would leave most CUs idle, the widest of 64, 32 or 16 columns
-        // that gives a workgroup per CU (else 16)
-        const int64_t mt = M_pad / GM_BM;
-        const bool t112 = n % 112 == 0 && (mt * (n / 112)) % 512 == 0 && (mt * cdiv(n, GM_BN)) % 512 != 0;
-        int bn = GM_BN;
-        if (mt * cdiv(n, GM_BN) < 128) {
-            bn = 64;
-            while (bn > 16 && mt * cdiv(n, bn) < 256) bn /= 2;
-        }
-#define TN_GEMM(WR, WC, TJ, BNN)                                                                                   \
-    hipLaunchKernelGGL((k_gemm<WR, WC, TJ>), dim3((unsigned)cdiv(n, BNN), (unsigned)mt), dim3(GM_THREADS), 0, st, \
-                       xc, dxT, corrT, (int)m, (int)M_pad, nb, qs, d, (int)n, bias, y, y_bf16)
-        if (t112) TN_GEMM(4, 1, 7, 112);
-        else if (bn == 16) TN_GEMM(4, 1, 1, 16);
-        else if (bn == 32) TN_GEMM(4, 1, 2, 32);
-        else if (bn == 64) TN_GEMM(4, 1, 4, 64);
-        else TN_GEMM(2, 2, 4, GM_BN);
-#undef TN_GEMM
+        gemm_q4_launch(st, xc, dxT, corrT, m, M_pad, nb, qs, d, n, bias, y, y_bf16, nullptr);
         TN_LAUNCHED();
     }
     return TN_OK;
@@ -1663,6 +1692,44 @@ tn_status linear_decode_argmax(hipStream_t st, const float* x, int64_t k, const 
     if (s != TN_OK) return s;
     hipLaunchKernelGGL(k_argmax_parts, dim3(1), dim3(GEMV_THREADS), 0, st, po.arg_v, po.arg_i, (int)parts, (int)n,
                        po.state, po.tokens, po.prompt, po.prompt_len, po.cap);
+    TN_LAUNCHED();
+    return TN_OK;
+}
+
+// A prompt's projection through the q4 GEMM, its input in one of the
+// prepass's layouts and the residual added in its epilogue.
+tn_status linear_prefill(hipStream_t st, const float* x, int64_t m, int64_t k, int xm, int hd, const uint8_t* qs,
+                         const uint16_t* d, int64_t n, const float* resid, float* y) {
+    tn_status s = check_weight("linear_prefill", "q4_0", n, k);
+    if (s != TN_OK) return s;
+    if (m == 0 || n == 0) return TN_OK;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(TN_EINVAL, "linear_prefill: x must be 16-byte aligned");
+    if (xm == XM_HEADS && (hd <= 0 || hd % QK != 0 || k % hd != 0))
+        return fail(TN_EINVAL, "linear_prefill: the head dim must divide the row and be a multiple of 32");
+    const int nb = (int)(k / QK);
+    const int64_t M_pad = cdiv(m, GM_BM) * GM_BM;
+    if (M_pad > INT32_MAX || n > INT32_MAX || M_pad * k * (xm == XM_GLU ? 2 : 1) > INT32_MAX)
+        return fail(TN_EVALUE, "linear_prefill: shape too large");
+    const int64_t blocks = M_pad * nb;
+    const size_t dx_bytes = (size_t)M_pad * nb * 4, xc_bytes = (size_t)M_pad * k * 2;
+    void* ws = nullptr;
+    s = workspace(st, xc_bytes + 2 * dx_bytes, &ws);
+    if (s != TN_OK) return s;
+    uint16_t* xc = static_cast<uint16_t*>(ws);
+    float* dxT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes);
+    float* corrT = reinterpret_cast<float*>(static_cast<char*>(ws) + xc_bytes + dx_bytes);
+    const dim3 vgrid((unsigned)cdiv(blocks, 64));  // 4 lanes per block
+    if (xm == XM_GLU)
+        hipLaunchKernelGGL((k_q8_rows_v<float, XM_GLU>), vgrid, dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb, xc,
+                           dxT, corrT, 0);
+    else if (xm == XM_HEADS)
+        hipLaunchKernelGGL((k_q8_rows_v<float, XM_HEADS>), vgrid, dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb,
+                           xc, dxT, corrT, hd);
+    else
+        hipLaunchKernelGGL((k_q8_rows_v<float, XM_ROWS>), vgrid, dim3(256), 0, st, x, (int)m, (int)M_pad, (int)k, nb,
+                           xc, dxT, corrT, 0);
+    TN_LAUNCHED();
+    gemm_q4_launch(st, xc, dxT, corrT, m, M_pad, nb, qs, d, n, nullptr, y, 0, resid);
     TN_LAUNCHED();
     return TN_OK;
 }

@@ -359,5 +359,14 @@ tn_status linear_decode(hipStream_t st, const float* x, int64_t k, int pro, cons
 // TN_ENOTIMPL when the activation row does not fit the GEMV.
 tn_status linear_decode_argmax(hipStream_t st, const float* x, int64_t k, const GemvPro& po, const uint8_t* qs,
                                const uint16_t* d, int64_t n, float* y);
+// A prompt's projection, y = Q4_0 linear of m activation rows (f32, 16-byte
+// aligned) through the q4 GEMM, bit-identical to the separate ops: xm picks
+// where row r's k activations come from (XM_ROWS: x[r][0..k); XM_GLU:
+// silu(gate) * up of x's [m][2k] rows, as tn_silu_mul; XM_HEADS: an
+// attention output [k / hd][m][hd], as the copy to token rows), and a
+// non-null resid is added to the product as tn_add does (resid may be y).
+constexpr int XM_ROWS = 0, XM_GLU = 1, XM_HEADS = 2;
+tn_status linear_prefill(hipStream_t st, const float* x, int64_t m, int64_t k, int xm, int hd, const uint8_t* qs,
+                         const uint16_t* d, int64_t n, const float* resid, float* y);
 
 }  // namespace tn
