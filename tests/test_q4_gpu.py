@@ -129,6 +129,9 @@ def test_gemv_scales_across_every_f16_regime(tn):
 @pytest.mark.parametrize("m,n,k,seed", [
     (5, 11, 512, 21), (17, 10, 512, 22), (130, 9, 512, 23),  # test_qgemm.py row / tail counts
     (128, 256, 1024, 24), (200, 333, 576, 25), (512, 384, 4096, 26),
+    # the tile shapes: 16 columns above, 32 columns (3 row tiles x 157), and
+    # 128 x 128 (2 row tiles x 64, N not a multiple of 112)
+    (300, 5000, 256, 27), (256, 8192, 256, 28),
 ])
 def test_gemm_is_bit_identical_to_the_oracle(tn, m, n, k, seed):
     rng = np.random.default_rng(seed)

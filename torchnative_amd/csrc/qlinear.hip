@@ -1492,25 +1492,22 @@ tn_status launch_gemv(hipStream_t st, const XT* x, int K, const uint8_t* qs, con
 
 // The q4 GEMM over the prepass's codes: 112-column tiles when they fill the
 // device in whole rounds of two workgroups per CU and 128-column ones would
-// not; when 128-column tiles would leave most CUs idle, the widest of 64, 32
-// or 16 columns that gives a workgroup per CU (else 16).
+// not; when 128-column tiles would give fewer than 128 workgroups, 32-column
+// ones if they give a workgroup per CU, else 16-column ones (64 columns
+// would give fewer than 256 workgroups whenever 128 give fewer than 128).
 void gemm_q4_launch(hipStream_t st, const uint16_t* xc, const float* dxT, const float* corrT, int64_t m,
                     int64_t M_pad, int nb, const uint8_t* qs, const uint16_t* d, int64_t n, const float* bias, void* y,
                     int y_bf16, const float* resid) {
     const int64_t mt = M_pad / GM_BM;
     const bool t112 = n % 112 == 0 && (mt * (n / 112)) % 512 == 0 && (mt * cdiv(n, GM_BN)) % 512 != 0;
     int bn = GM_BN;
-    if (mt * cdiv(n, GM_BN) < 128) {
-        bn = 64;
-        while (bn > 16 && mt * cdiv(n, bn) < 256) bn /= 2;
-    }
+    if (mt * cdiv(n, GM_BN) < 128) bn = mt * cdiv(n, 32) >= 256 ? 32 : 16;
 #define TN_GEMM(WR, WC, TJ, BNN)                                                                                   \
     hipLaunchKernelGGL((k_gemm<WR, WC, TJ>), dim3((unsigned)cdiv(n, BNN), (unsigned)mt), dim3(GM_THREADS), 0, st, \
                        xc, dxT, corrT, (int)m, (int)M_pad, nb, qs, d, (int)n, bias, y, y_bf16, resid)
     if (t112) TN_GEMM(4, 1, 7, 112);
     else if (bn == 16) TN_GEMM(4, 1, 1, 16);
     else if (bn == 32) TN_GEMM(4, 1, 2, 32);
-    else if (bn == 64) TN_GEMM(4, 1, 4, 64);
     else TN_GEMM(2, 2, 4, GM_BN);
 #undef TN_GEMM
 }
