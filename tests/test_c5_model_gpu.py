@@ -210,20 +210,27 @@ def test_config5_batched_prefill_then_steps_against_the_oracle(tn, c5, cap):
     print(f"c5 prefill: cap {cap}: worst {worst:.3f} of the bound", flush=True)
 
 
-@pytest.mark.parametrize("n_prompt", [1, 5, 64, 150])
-def test_prefill_generates_the_oracles_greedy_tokens(tn, n_prompt):
+# head dim 48: a head's rows are not whole 32-element Q8_0 blocks, so the
+# prompt's o projection reads the attention output through the copy to
+# token rows instead of in place
+HD48 = OD.LlamaConfig(n_layers=2, hidden=288, n_heads=6, n_kv_heads=2, head_dim=48, inter=256, vocab=512)
+
+
+@pytest.mark.parametrize("cfg,n_prompt", [(NREP3, 1), (NREP3, 5), (NREP3, 64), (NREP3, 150), (HD48, 5), (HD48, 70)],
+                         ids=["hd64-1", "hd64-5", "hd64-64", "hd64-150", "hd48-5", "hd48-70"])
+def test_prefill_generates_the_oracles_greedy_tokens(tn, cfg, n_prompt):
     """A small model: prefill a prompt of n tokens and generate 12 more with
     the steps; every generated token is the oracle's greedy token wherever
     the oracle's top two logits are further apart than twice the bound."""
     from torchnative_amd.decoder import Q4Llama
 
     rng = np.random.default_rng(n_prompt)
-    prompt = [int(t) for t in rng.integers(0, NREP3.vocab, n_prompt)]
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab, n_prompt)]
     n_new = 12
-    model = Q4Llama(NREP3, seed=13, cap=200)
+    model = Q4Llama(cfg, seed=13, cap=200)
     got = model.generate(prompt, n_new, prefill=True)
-    r32 = OD.Decoder(NREP3, 13, 200, np.float32)
-    r64 = OD.Decoder(NREP3, 13, 200, np.float64)
+    r32 = OD.Decoder(cfg, 13, 200, np.float32)
+    r64 = OD.Decoder(cfg, 13, 200, np.float64)
     seq = list(prompt)
     for pos in range(n_prompt + n_new - 1):
         l32 = r32.step(seq[pos], pos).astype(np.float64)

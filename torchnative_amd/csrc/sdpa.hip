@@ -1963,6 +1963,23 @@ tn_status decode_launch(hipStream_t st, int dtype, const void* q, const void* k_
     const int nsplit = (int)cdiv(max_len, DEC_SPLIT);
     const double sc = std::isnan(scale) ? 1.0 / std::sqrt((double)D) : scale;
     const float sl2 = (float)sc * LOG2E;
+    if (D != 64 && D != 128) {
+        // the split kernels below exist for head dims 64 and 128; any other
+        // (up to 256, decode_check) runs on the plain kernel, one query row per
+        // (sequence, head) over the cache's cap rows, as tn_sdpa_decode does
+        const dim3 grid(1u, (unsigned)Hq, (unsigned)B);
+        if (dtype == TN_F32)
+            hipLaunchKernelGGL((k_attn_any<0, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
+                               (int)cap, (int)D, sc, 0, out, lse, MaskRef{}, lens, (int)max_len);
+        else if (dtype == TN_BF16)
+            hipLaunchKernelGGL((k_attn_any<1, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
+                               (int)cap, (int)D, sc, 0, out, lse, MaskRef{}, lens, (int)max_len);
+        else
+            hipLaunchKernelGGL((k_attn_any<2, 0>), grid, dim3(256), 0, st, q, k_cache, v_cache, (int)Hq, (int)Hkv, 1,
+                               (int)cap, (int)D, sc, 0, out, lse, MaskRef{}, lens, (int)max_len);
+        TN_LAUNCHED();
+        return TN_OK;
+    }
     if (dtype == TN_F32) {
         auto qq = static_cast<const float*>(q);
         auto kk = static_cast<const float*>(k_cache);
