@@ -137,8 +137,11 @@ def test_gemm_is_bit_identical_to_the_oracle(tn, m, n, k, seed):
     rng = np.random.default_rng(seed)
     x = (rng.standard_normal((m, k)) * 1.3).astype(np.float32)
     blob = O.synth_q4_0_weight(n, k, 0.01, seed + 100)
-    want = O.q4_0_linear(x, blob, n, threads=8)
-    got = tn._quantized_linear(tn.tensor(x, device="hip"), _qweight(tn, blob, n, k)).numpy()
+    # odd seeds add a bias: the GEMM epilogue's addition, in every tile shape
+    bias = rng.standard_normal(n).astype(np.float32) if seed % 2 else None
+    want = O.q4_0_linear(x, blob, n, bias=bias, threads=8)
+    b = tn.tensor(bias, device="hip") if bias is not None else None
+    got = tn._quantized_linear(tn.tensor(x, device="hip"), _qweight(tn, blob, n, k), b).numpy()
     assert got.tobytes() == want.tobytes(), np.argwhere(got != want)[:5]
 
 
