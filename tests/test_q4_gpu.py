@@ -141,8 +141,12 @@ def test_gemm_is_bit_identical_to_the_oracle(tn, m, n, k, seed):
     bias = rng.standard_normal(n).astype(np.float32) if seed % 2 else None
     want = O.q4_0_linear(x, blob, n, bias=bias, threads=8)
     b = tn.tensor(bias, device="hip") if bias is not None else None
-    got = tn._quantized_linear(tn.tensor(x, device="hip"), _qweight(tn, blob, n, k), b).numpy()
+    q = _qweight(tn, blob, n, k)
+    got = tn._quantized_linear(tn.tensor(x, device="hip"), q, b).numpy()
     assert got.tobytes() == want.tobytes(), np.argwhere(got != want)[:5]
+    # bf16 output: the f32 result narrowed RNE, in every tile shape
+    gb = tn._quantized_linear(tn.tensor(x, device="hip"), q, b, out_dtype="bfloat16").bits()
+    assert np.array_equal(gb, O.bf16_from_f32(want))
 
 
 def test_batched_rows_equal_one_row_calls_on_the_device(tn):
