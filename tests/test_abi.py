@@ -74,6 +74,15 @@ def test_linear_refusals_use_the_reference_wording(L):
         in _lib.last_error()
     st = L.tn_q4_k_linear(None, None, _lib.TN_F32, 2, 288, None, 8, None, None, _lib.TN_F32)
     assert st == _lib.TN_EINVAL and "cannot be multiplied ([2, 288]" in _lib.last_error()
+    # an empty product (no rows, or no output columns) is a success that
+    # touches no pointer, as an empty matmul returns an empty tensor
+    for m, n in ((0, 8), (2, 0), (0, 0)):
+        assert L.tn_q4_0_linear(None, None, _lib.TN_F32, m, 64, None, None, n, None, None, _lib.TN_F32) == _lib.TN_OK
+        assert L.tn_q8_0_linear(None, None, _lib.TN_BF16, m, 64, None, None, n, None, None, _lib.TN_BF16) == _lib.TN_OK
+        assert L.tn_q4_k_linear(None, None, _lib.TN_F32, m, 256, None, n, None, None, _lib.TN_F32) == _lib.TN_OK
+    # ... but the shape check still comes first
+    st = L.tn_q4_0_linear(None, None, _lib.TN_F32, 0, 33, None, None, 8, None, None, _lib.TN_F32)
+    assert st == _lib.TN_EINVAL and "cannot be multiplied ([0, 33]" in _lib.last_error()
     assert L.tn_q4_k_from_blob(None, None, 4, 256, None) == _lib.TN_EVALUE
     assert L.tn_q8_0_dequantize(None, None, None, 4, 96, None) == _lib.TN_EVALUE  # null planes
     assert "null pointer" in _lib.last_error()
