@@ -113,6 +113,9 @@ def test_sdpa_refusals_name_the_reason(L):
     assert call(dtype=_lib.TN_F16, mask=1, mask_dtype=_lib.TN_BF16) == _lib.TN_EINVAL
     # empty batch: nothing to write, success without touching a pointer
     assert call(B=0) == _lib.TN_OK
+    assert call(L=0) == _lib.TN_OK  # no query rows (aten.rs:10242-10259)
+    assert call(L=0, dtype=_lib.TN_F32, mask=1, mask_dtype=_lib.TN_BOOL) == _lib.TN_OK
+    assert call(Hq=0, Hkv=3) == _lib.TN_OK  # 0 % 3: divisible, and nothing to write
     st = L.tn_sdpa_decode(None, _lib.TN_BF16, None, None, None, 2, 32, 8, 64, 128, None, 65, float("nan"),
                           None, None)
     assert st == _lib.TN_EINVAL and "max_len" in _lib.last_error()
