@@ -76,6 +76,7 @@ def test_device_quantiser_matches_the_oracle_on_random_and_edge_blocks(tn):
     (1, 8, 64, 11), (3, 12, 512, 12), (2, 5, 1024, 13),   # test_q4ref.py shapes
     (4, 576, 1536, 2), (1, 49152, 576, 3),                # SmolLM2-shaped down-proj / lm_head
     (1, 100, 32, 4), (1, 3, 16384, 5),                    # one block per row; a long row
+    (1, 3, 24576, 7), (2, 3, 24608, 8),                   # the GEMV's longest row; one block more (GEMM)
 ])
 def test_gemv_is_bit_identical_to_the_oracle(tn, m, n, k, seed):
     rng = np.random.default_rng(seed)
