@@ -77,6 +77,7 @@ def test_reader_round_trip_and_llama_cpps_bits(tn, golden):
     (1, 1536, 576 // 64 * 256, 1), (4, 576, 1536, 2),         # decode-sized
     (1, 3000, 4096, 3), (1, 7, 14336, 4), (2, 9, 28672, 5),   # long rows
     (5, 33, 2048, 6), (17, 40, 512, 7), (64, 96, 1024, 8),    # more rows than one chunk
+    (1, 3, 46080, 9), (3, 3, 46080, 10),                      # rows past the GEMV's LDS: the GEMM
 ])
 def test_linear_is_bit_identical_to_the_oracle(tn, m, n, k, seed):
     rng = np.random.default_rng(seed)

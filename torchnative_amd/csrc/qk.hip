@@ -789,8 +789,10 @@ tn_status linear_qk(hipStream_t st, const XT* x, int64_t m, int64_t k, const uin
     if (m == 0 || n == 0) return TN_OK;
     if (n > INT32_MAX || k > INT32_MAX) return fail(TN_EVALUE, "torch._C._quantized_linear: shape too large");
     const size_t ysz = y_bf16 ? 2 : 4;
-    if (m > 4) {
-        // prefill: Q8_K prepass, then the MFMA GEMM
+    // prefill: Q8_K prepass, then the MFMA GEMM (any row count, and rows of
+    // any length; bit-identical to the GEMV, since every output is the same
+    // recurrence)
+    auto gemm = [&](const XT* x, int64_t m, void* y) -> tn_status {
         const int nsb = (int)(k / QKK);
         const int64_t M_pad = cdiv(m, QM_ROWS) * QM_ROWS;
         if (M_pad > INT32_MAX) return fail(TN_EVALUE, "torch._C._quantized_linear: shape too large");
@@ -809,7 +811,8 @@ tn_status linear_qk(hipStream_t st, const XT* x, int64_t m, int64_t k, const uin
                            bias, y, y_bf16);
         TN_LAUNCHED();
         return TN_OK;
-    }
+    };
+    if (m > 4) return gemm(x, m, y);
     // decode: rows of x in chunks of up to 4 (every output is the same recurrence, so
     // the chunking changes no bit); the widest chunk whose activations fit LDS
     int64_t r = 0;
@@ -831,8 +834,7 @@ tn_status linear_qk(hipStream_t st, const XT* x, int64_t m, int64_t k, const uin
             s = launch_gemv_qk<1, XT>(st, xr, (int)k, w, (int)n, bias, yr, y_bf16);
             c = 1;
         }
-        if (s == TN_ENOTIMPL)
-            return fail(TN_ENOTIMPL, "torch._C._quantized_linear: q4_k rows of this length do not fit the kernel");
+        if (s == TN_ENOTIMPL) return gemm(xr, left, yr);  // a row too long for the GEMV's LDS
         if (s != TN_OK) return s;
         r += c;
     }
